@@ -1,0 +1,901 @@
+"""The ``hip`` backend: a codegen plugin that emits gfx950 kernels and a launch plan.
+
+It implements the plugin protocol the front end drives (the reference's ``Codegen`` surface,
+chroma/_src/codegen/base.py:39-113 and gpu.py:63-435) and replaces the CUDA generator and its cuBLAS
+calls (chroma/_src/codegen/cuda/codegen.py:44-168):
+
+* A non-stored value is a closure ``(kernel, coordinates) -> node`` over the kernel compiler in
+  ``kernel.py``; a consumer kernel inlines it. Materialisation happens when the front end asks for it,
+  when an expression is 24 levels deep, or when it reads 24 buffers.
+* Every launch is a deduplicated ``extern "C"`` kernel whose parameters are buffer base pointers; the
+  plan binds each parameter to a region of the program's single device allocation (weights | workspace |
+  error word | inputs | outputs), so the twelve identical layers of a model share their kernels.
+* Whole-tensor operations (softmax, RMSNorm, reductions, top-k, linear, contractions) are generated
+  around templates in ``csrc/include/chroma_hip`` and keep the reference CPU backend's numerics:
+  float accumulation, division-based normalisation, RNE bfloat16 at every bfloat16 result, lowest-index
+  tie-breaking in top-k with NaN ranked highest.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Callable, Dict, List, Optional, Sequence, Tuple, Union
+
+import torch
+
+from chroma_amd._src.codegen.base import Codegen, GeneratedCode
+from chroma_amd._src.codegen.kernel import ZERO, Aff, Atom, Kernel, choose_lanes, ctype_of, float_literal, is_int
+from chroma_amd._src.spec import Stats, TensorSpec, nbytes
+from chroma_amd._src.value import ITEMSIZE, Value, View, contiguous_strides, contraction, matrix_axes
+
+Closure = Callable[[Kernel, List[Aff]], tuple]
+
+ALIGN = 256
+MAX_DEPTH = 24
+MAX_SOURCES = 24
+MAP_THREADS = 256
+MAX_GRID = 16384
+
+UNARY_OPS = {
+    "reciprocal": "reciprocal",
+    "rsqrt": "rsqrt",
+    "sigmoid": "sigmoid",
+    "sin": "sin",
+    "cos": "cos",
+    "exp": "exp",
+    "neg": "neg",
+    "abs": "abs",
+    "square": "square",
+    "tanh": "tanh",
+    "silu": "silu",
+}
+
+
+@dataclass(frozen=True)
+class Binding:
+    kind: str  # "weight" | "arena" | "input" | "output" | "error"
+    index: Union[int, str] = 0  # input/output position, or arena allocation name
+    offset: int = 0  # byte offset (weights: inside the blob)
+
+
+@dataclass
+class Launch:
+    kernel: str
+    grid: Tuple[int, int, int]
+    block: int
+    bindings: List[Binding]
+    shared: int = 0
+
+
+def _align(value: int) -> int:
+    return -(-value // ALIGN) * ALIGN
+
+
+def _shape(value_shape: Sequence[int]) -> Tuple[int, ...]:
+    return tuple(value_shape) if value_shape else (1,)
+
+
+class HIPCodegen(Codegen):
+    backend = "hip"
+
+    def __init__(self, *, blas: bool = True) -> None:
+        super().__init__()
+        self.blas = blas
+        self.closures: Dict[str, Closure] = {}
+        self.sources: Dict[str, frozenset] = {}
+        self.bindings: Dict[str, Binding] = {}
+        self.dtypes: Dict[str, torch.dtype] = {}
+        self.kernel_names: Dict[str, str] = {}
+        self.kernel_sources: List[str] = []
+        self.launches: List[Launch] = []
+        self.gathers: Dict[str, Tuple[Value, Value]] = {}
+        self.extents: Dict[str, int] = {}
+        self.parallel_reductions = 0
+        self.expert_contractions = 0
+        self.tiled_matmuls = 0
+        self.skinny_matmuls = 0
+
+    # ===================================================================================== storage
+    def extern(self, tensor: torch.Tensor, kind: str, offset: int) -> Value:
+        name = f"v{next(self.counter)}"
+        shape = tuple(tensor.shape)
+        self.bindings[name] = Binding("input", offset) if kind == "input" else Binding("weight", 0, offset)
+        self.dtypes[name] = tensor.dtype
+        self.sources[name] = frozenset({name})
+        self.extents[name] = math.prod(shape)
+        return Value(name, shape, tensor.dtype, stored=True, view=View(None, contiguous_strides(shape)))
+
+    def allocate(self, shape, dtype) -> Value:
+        value = super().allocate(shape, dtype)
+        self.bindings[value.name] = Binding("arena", value.name)
+        self.dtypes[value.name] = dtype
+        self.sources[value.name] = frozenset({value.name})
+        self.extents[value.name] = math.prod(value.shape)
+        return value
+
+    def alias(self, meta: torch.Tensor, root: Value, offset: int) -> Value:
+        shape = tuple(meta.shape)
+        name = f"v{next(self.counter)}"
+        self.sources[name] = self.sources[root.name]
+        return Value(name, shape, meta.dtype, root.deps, stored=True, view=View(root, contiguous_strides(shape), offset))
+
+    # ================================================================================= expressions
+    def expr(self, meta: torch.Tensor, closure: Closure, inputs: Sequence[Value]) -> Value:
+        name = f"e{next(self.counter)}"
+        self.closures[name] = closure
+        self.sources[name] = frozenset().union(*(self.sources[v.name] for v in inputs)) if inputs else frozenset()
+        value = self.expression_value(name, meta, inputs)
+        if value.depth >= MAX_DEPTH or len(self.sources[name]) >= MAX_SOURCES:
+            return self.materialize(value)
+        return value
+
+    def read(self, k: Kernel, value: Value, coords: Sequence[Aff]) -> tuple:
+        """The node for ``value`` at ``coords`` (one affine coordinate per dimension)."""
+        if value.stored:
+            root, view = value.root, value.view
+            address = Aff((), view.offset)
+            for coord, stride, size in zip(coords, view.strides, value.shape):
+                if size != 1 and stride:
+                    address = address + coord.scale(stride)
+            return ("ld", k.slot(root.name, root.dtype, extent=self.extents[root.name]), value.dtype, address)
+        key = (value.name, tuple(coords))
+        node = k.values.get(key)
+        if node is None:
+            node = self.closures[value.name](k, list(coords))
+            k.values[key] = node
+        return node
+
+    def read_flat(self, k: Kernel, value: Value, flat: Aff) -> tuple:
+        if value.stored and value.view.base is None:
+            return ("ld", k.slot(value.name, value.dtype, extent=self.extents[value.name]), value.dtype, flat)
+        return self.read(k, value, k.unflatten(flat, value.shape))
+
+    def broadcast_read(self, k: Kernel, value: Value, coords: Sequence[Aff], shape: Sequence[int]) -> tuple:
+        pad = len(shape) - len(value.shape)
+        mine = [ZERO if size == 1 else coords[d + pad] for d, size in enumerate(value.shape)]
+        return self.read(k, value, mine)
+
+    def materialize(self, value: Value) -> Value:
+        if value.stored:
+            return value
+        if value.name not in self.materialized:
+            out = self.allocate(value.shape, value.dtype)
+            self.map_kernel(out, value)
+            self.materialized[value.name] = out
+        return self.materialized[value.name]
+
+    def reshape(self, meta: torch.Tensor, x: Value) -> Value:
+        if x.stored:
+            return self.alias(meta, x.root, x.view.offset)
+        shape = tuple(meta.shape)
+
+        def closure(k: Kernel, coords: List[Aff]) -> tuple:
+            return self.read_flat(k, x, Kernel.flatten(coords, shape))
+
+        return self.expr(meta, closure, [x])
+
+    def reindex(self, meta: torch.Tensor, x: Value, mapping: Sequence[int], offset: int) -> Value:
+        shape = tuple(meta.shape)
+
+        def closure(k: Kernel, coords: List[Aff]) -> tuple:
+            flat = Aff((), offset)
+            for coord, stride, size in zip(coords, mapping, shape):
+                if size != 1 and stride:
+                    flat = flat + coord.scale(stride)
+            return self.read_flat(k, x, flat)
+
+        return self.expr(meta, closure, [x])
+
+    def cast(self, meta: torch.Tensor, x: Value) -> Value:
+        to_bf16 = meta.dtype == torch.bfloat16 and x.dtype != torch.bfloat16
+
+        def closure(k: Kernel, coords: List[Aff]) -> tuple:
+            node = self.read(k, x, coords)
+            return ("rnd", node) if to_bf16 else node
+
+        return self.expr(meta, closure, [x])
+
+    def elementwise(self, meta, target: str, args, *, alpha: float = 1, low: Optional[float] = None, high: Optional[float] = None) -> Value:
+        shape = tuple(meta.shape)
+        op = target.split(".")[1]
+        bf16 = meta.dtype == torch.bfloat16
+
+        def rounded(node: tuple) -> tuple:
+            return ("rnd", node) if bf16 else node
+
+        def closure(k: Kernel, coords: List[Aff]) -> tuple:
+            def operand(a) -> tuple:
+                return self.broadcast_read(k, a, coords, shape) if isinstance(a, Value) else ("f", float(a))
+
+            a = operand(args[0])
+            if op in ("add", "sub"):
+                b = operand(args[1])
+                if alpha != 1:
+                    b = rounded(("bin", "mul", b, ("f", float(alpha))))
+                node = ("bin", op, a, b)
+            elif op == "rsub":
+                node = ("bin", "sub", operand(args[1]), rounded(("bin", "mul", a, ("f", float(alpha)))))
+            elif op in ("mul", "div"):
+                node = ("bin", op, a, operand(args[1]))
+            elif op == "pow":
+                b = operand(args[1])
+                node = ("un", "square", a) if b == ("f", 2.0) else ("bin", "pow", a, b)
+            elif op == "clamp":
+                node = a
+                if low is not None:
+                    node = ("bin", "lowclamp", node, ("f", float(low)))
+                if high is not None:
+                    node = ("bin", "highclamp", node, ("f", float(high)))
+            else:
+                node = ("un", UNARY_OPS[op], a)
+            return rounded(node)
+
+        return self.expr(meta, closure, [v for v in args if isinstance(v, Value)])
+
+    def gather(self, meta, x: Value, indices: Value, negative: bool) -> Value:
+        index_rank = len(indices.shape)
+        rows = x.shape[0]
+
+        def closure(k: Kernel, coords: List[Aff]) -> tuple:
+            selected = self.read(k, indices, coords[:index_rank])
+            row = k.index_atom(selected, rows, negative)
+            return self.read(k, x, [row, *coords[index_rank:]])
+
+        value = self.expr(meta, closure, [x, indices])
+        if negative and not value.stored:
+            self.gathers[value.name] = (x, indices)
+        return value
+
+    def triangular(self, meta, x: Value, diagonal: int, upper: bool) -> Value:
+        zero = ("i", 0) if is_int(meta.dtype) else ("f", 0.0)
+
+        def closure(k: Kernel, coords: List[Aff]) -> tuple:
+            keep = ("cmp", ">=" if upper else "<=", coords[-1], coords[-2], int(diagonal))
+            return ("sel", keep, self.read(k, x, coords), zero)
+
+        return self.expr(meta, closure, [x])
+
+    # ================================================================================= launching
+    def binding_of(self, buffer: str) -> Binding:
+        return self.bindings[buffer]
+
+    def launch(self, k: Kernel, grid: Union[int, Tuple[int, int, int]], block: int, inputs: Sequence[Value], *, prologue: Sequence[str] = ()) -> None:
+        source = k.render("KERNEL_NAME", block, prologue)
+        name = self.kernel_names.get(source)
+        if name is None:
+            name = f"chroma_k{len(self.kernel_sources)}"
+            self.kernel_names[source] = name
+            self.kernel_sources.append(source.replace("KERNEL_NAME", name, 1))
+        grid3 = (grid, 1, 1) if isinstance(grid, int) else grid
+        if any(g > 2**31 - 1 for g in grid3):
+            raise ValueError("HIP dispatch exceeds the grid limit")
+        bindings = [self.binding_of(buffer) for buffer in k.slots]
+        for buffer in k.slots:
+            allocation = self.allocations.get(buffer)
+            if allocation is not None:
+                allocation.end = max(allocation.end, self.kernels)
+        self.record_usage(inputs)
+        self.launches.append(Launch(name, grid3, block, bindings))
+        self.kernels += 1
+
+    def map_kernel(self, out: Value, value: Value, target: Optional[str] = None) -> None:
+        """out[i] = value[i] over a contiguous destination (an allocation or an output region)."""
+        shape = _shape(value.shape)
+        count = math.prod(shape)
+        lanes = choose_lanes(shape[-1], value.dtype)
+        k = Kernel(lanes)
+        slot = k.slot(target or out.name, value.dtype, writable=True, extent=self.extents[target or out.name])
+        vectors = count // lanes
+        wide = vectors > 2**31 - 1
+        itype = "uint64_t" if wide else "uint32_t"
+        loop = f"for ({itype} v = {itype}(blockIdx.x) * {MAP_THREADS}u + threadIdx.x; v < {vectors}u; v += {itype}(gridDim.x) * {MAP_THREADS}u) {{"
+        with k.block(loop):
+            v = Atom("v", vectors - 1)
+            vshape = shape[:-1] + (shape[-1] // lanes,)
+            coords = k.unflatten(Aff.of(v), vshape)
+            if lanes > 1:
+                coords[-1] = Aff.of(k.vector_atom(f"({coords[-1].code()}) * {lanes}u", shape[-1] - 1))
+            node = self.read(k, value, coords if value.shape else coords[:0])
+            k.store(slot, value.dtype, Kernel.flatten(coords, shape), node)
+        grid = max(1, min(-(-vectors // MAP_THREADS), MAX_GRID))
+        self.launch(k, grid, MAP_THREADS, [value])
+
+    # ==================================================================================== outputs
+    def output(self, index: int, value: Value) -> None:
+        if self.promote_output(index, value):
+            return
+        name = f"output{index}"
+        self.bindings[name] = Binding("output", index)
+        self.dtypes[name] = value.dtype
+        self.extents[name] = math.prod(value.shape)
+        out = Value(name, value.shape, value.dtype, stored=True, view=View(None, contiguous_strides(value.shape)))
+        self.map_kernel(out, value, target=name)
+
+    # =================================================================================== concat
+    def concatenate(self, meta, values: Sequence[Value], dim: int) -> Value:
+        out = self.allocate(tuple(meta.shape), meta.dtype)
+        shape = _shape(out.shape)
+        innermost = dim == len(shape) - 1
+        lanes = choose_lanes(shape[-1], meta.dtype)
+        if innermost:
+            while lanes > 1 and any(v.shape[dim] % lanes for v in values):
+                lanes //= 2
+        count = math.prod(shape)
+        k = Kernel(lanes)
+        slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        vectors = count // lanes
+        with k.block(f"for (uint32_t v = blockIdx.x * {MAP_THREADS}u + threadIdx.x; v < {vectors}u; v += gridDim.x * {MAP_THREADS}u) {{"):
+            v = Atom("v", vectors - 1)
+            vshape = shape[:-1] + (shape[-1] // lanes,)
+            coords = k.unflatten(Aff.of(v), vshape)
+            if lanes > 1:
+                coords[-1] = Aff.of(k.vector_atom(f"({coords[-1].code()}) * {lanes}u", shape[-1] - 1))
+            along = coords[dim]
+            along_code = k.atom(along.code(), shape[dim] - 1, prefix="c") if not innermost or lanes == 1 else None
+            start = 0
+            for i, value in enumerate(values):
+                end = start + value.shape[dim]
+                if innermost and lanes > 1:
+                    test = f"{coords[-1].code()} < {end}u"
+                else:
+                    test = f"{along_code.name} < {end}u"
+                opener = ("if (" if i == 0 else "} else if (") + test + ") {" if i < len(values) - 1 else ("} else {" if i else "{")
+                k.line(opener)
+                k.indent += 1
+                saved = (dict(k.atoms), dict(k.nodes), dict(k.values))
+                local = list(coords)
+                if innermost and lanes > 1:
+                    local[dim] = Aff.of(k.vector_atom(f"{coords[dim].code()} - {start}u", value.shape[dim] - 1))
+                else:
+                    local[dim] = Aff.of(k.atom(f"{along_code.name} - {start}u", value.shape[dim] - 1, prefix="c"))
+                node = self.read(k, value, local)
+                k.store(slot, out.dtype, Kernel.flatten(coords, shape), node)
+                k.atoms, k.nodes, k.values = saved
+                k.indent -= 1
+                start = end
+            k.line("}")
+        grid = max(1, min(-(-vectors // MAP_THREADS), MAX_GRID))
+        self.launch(k, grid, MAP_THREADS, values)
+        return out
+
+    # ================================================================================ row kernels
+    def _row_layout(self, shape: Sequence[int], dim: int) -> Tuple[int, int, int]:
+        width = shape[dim]
+        inner = math.prod(shape[dim + 1 :])
+        outer = math.prod(shape[:dim])
+        return width, inner, outer
+
+    def _row_coords(self, k: Kernel, row: Aff, shape: Sequence[int], dim: int, along: Aff) -> List[Aff]:
+        """Coordinates of element ``along`` of row ``row`` (rows enumerate outer x inner positions)."""
+        inner_shape = tuple(shape[dim + 1 :])
+        inner = math.prod(inner_shape)
+        outer_coords = k.unflatten(k.div(row, inner), tuple(shape[:dim])) if dim else []
+        inner_coords = k.unflatten(k.mod(row, inner), inner_shape) if inner_shape else []
+        return [*outer_coords, along, *inner_coords]
+
+    def softmax(self, meta, x: Value, dim: int) -> Value:
+        out = self.allocate(tuple(meta.shape), meta.dtype)
+        shape = tuple(x.shape)
+        width, inner, outer = self._row_layout(shape, dim)
+        rows = outer * inner
+        if inner == 1 and width >= 64:
+            self._row_softmax(out, x, shape, dim, width, rows)
+            self.parallel_reductions += 1
+        else:
+            self._thread_softmax(out, x, shape, dim, width, rows)
+        return out
+
+    def _row_plan(self, width: int, dtype: torch.dtype) -> Tuple[int, int, int, bool]:
+        threads = 256 if width >= 2048 else 64
+        lanes = choose_lanes(width, dtype)
+        chunks = -(-width // (threads * lanes))
+        resident = chunks * lanes <= 32
+        return threads, lanes, chunks, resident
+
+    def _row_softmax(self, out: Value, x: Value, shape, dim: int, width: int, rows: int) -> None:
+        threads, lanes, chunks, resident = self._row_plan(width, x.dtype)
+        waves = threads // 64
+        k = Kernel(lanes)
+        slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        row_atom = k.atom("blockIdx.x", rows - 1, prefix="r")
+        row = Aff.of(row_atom)
+        step = threads * lanes
+        ragged = width % step != 0
+        neg_inf = float_literal(-math.inf)
+
+        def element(j: Aff) -> tuple:
+            return self.read(k, x, self._row_coords(k, row, shape, dim, j))
+
+        def out_address(j: Aff) -> Aff:
+            return Kernel.flatten(self._row_coords(k, row, shape, dim, j), shape)
+
+        def lane_names(node) -> List[str]:
+            names = k.emit(node)
+            return names if isinstance(names, list) else [names] * lanes
+
+        if resident:
+            k.line(f"float vals[{chunks}][{lanes}];")
+            k.line(f"float peak = {neg_inf};")
+            k.line("#pragma unroll")
+            with k.block(f"for (uint32_t c = 0; c < {chunks}u; ++c) {{"):
+                j = Aff.of(k.vector_atom(f"c * {step}u + threadIdx.x * {lanes}u", width - 1))
+                guard = ragged
+                if guard:
+                    k.line(f"if ({j.code()} < {width}u) {{")
+                    k.indent += 1
+                names = lane_names(element(j))
+                for lane, name in enumerate(names):
+                    k.line(f"vals[c][{lane}] = {name}; peak = __builtin_fmaxf(peak, {name});")
+                if guard:
+                    k.indent -= 1
+                    k.line("} else {")
+                    k.line("    " + " ".join(f"vals[c][{lane}] = {neg_inf};" for lane in range(lanes)))
+                    k.line("}")
+            k.line(f"peak = chroma::block_max<{waves}>(peak, scratch);")
+            k.line("float total = 0.0f;")
+            k.line("#pragma unroll")
+            k.line(f"for (uint32_t c = 0; c < {chunks}u; ++c) {{")
+            k.line(f"    #pragma unroll")
+            k.line(f"    for (uint32_t l = 0; l < {lanes}u; ++l) {{ vals[c][l] = chroma::fast_exp(vals[c][l] - peak); total += vals[c][l]; }}")
+            k.line("}")
+            k.line(f"total = chroma::block_sum<{waves}>(total, scratch);")
+            k.line("const float inverse = 1.0f / total;")
+            k.line("#pragma unroll")
+            with k.block(f"for (uint32_t c = 0; c < {chunks}u; ++c) {{"):
+                j = Aff.of(k.vector_atom(f"c * {step}u + threadIdx.x * {lanes}u", width - 1))
+                if ragged:
+                    k.line(f"if ({j.code()} < {width}u) {{")
+                    k.indent += 1
+                result = self._lane_values(k, [f"vals[c][{lane}] * inverse" for lane in range(lanes)])
+                k.store(slot, out.dtype, out_address(j), result)
+                if ragged:
+                    k.indent -= 1
+                    k.line("}")
+        else:
+            k.line(f"float peak = {neg_inf}, total = 0.0f;")
+            with k.block(f"for (uint32_t base = threadIdx.x * {lanes}u; base < {width}u; base += {step}u) {{"):
+                j = Aff.of(k.vector_atom("base", width - 1))
+                for name in lane_names(element(j)):
+                    k.line(f"{{ const float top = __builtin_fmaxf(peak, {name});")
+                    k.line(f"  total = top == {neg_inf} ? 0.0f : total * chroma::fast_exp(peak - top) + chroma::fast_exp({name} - top);")
+                    k.line("  peak = top; }")
+            k.line(f"const float row_peak = chroma::block_max<{waves}>(peak, scratch);")
+            k.line(f"total = chroma::block_sum<{waves}>(peak == {neg_inf} ? 0.0f : total * chroma::fast_exp(peak - row_peak), scratch);")
+            k.line("const float inverse = 1.0f / total;")
+            with k.block(f"for (uint32_t base = threadIdx.x * {lanes}u; base < {width}u; base += {step}u) {{"):
+                j = Aff.of(k.vector_atom("base", width - 1))
+                names = lane_names(element(j))
+                result = self._lane_values(k, [f"chroma::fast_exp({name} - row_peak) * inverse" for name in names])
+                k.store(slot, out.dtype, out_address(j), result)
+        self.launch(k, rows, threads, [x], prologue=[f"__shared__ float scratch[{max(waves, 1)}];"])
+
+    def _lane_values(self, k: Kernel, codes: Sequence[str]) -> tuple:
+        """A varying node whose lane l is the C expression ``codes[l]`` (declared now)."""
+        names = [k.fresh("q") for _ in codes]
+        for name, code in zip(names, codes):
+            k.line(f"const float {name} = {code};")
+        node = ("raw", tuple(names))
+        k.nodes[node] = names if k.lanes > 1 else names[0]
+        return node
+
+    def _thread_softmax(self, out: Value, x: Value, shape, dim: int, width: int, rows: int) -> None:
+        k = Kernel(1)
+        slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        neg_inf = float_literal(-math.inf)
+        with k.block(f"for (uint32_t r = blockIdx.x * 256u + threadIdx.x; r < {rows}u; r += gridDim.x * 256u) {{"):
+            row = Aff.of(Atom("r", rows - 1))
+            j_atom = Atom("j", width - 1)
+
+            def element() -> tuple:
+                return self.read(k, x, self._row_coords(k, row, shape, dim, Aff.of(j_atom)))
+
+            k.line(f"float peak = {neg_inf};")
+            with k.block(f"for (uint32_t j = 0; j < {width}u; ++j) {{"):
+                k.line(f"peak = __builtin_fmaxf(peak, {k.emit(element())});")
+            k.line("float total = 0.0f;")
+            with k.block(f"for (uint32_t j = 0; j < {width}u; ++j) {{"):
+                k.line(f"total += chroma::fast_exp({k.emit(element())} - peak);")
+            k.line("const float inverse = 1.0f / total;")
+            with k.block(f"for (uint32_t j = 0; j < {width}u; ++j) {{"):
+                value = self._lane_values(k, [f"chroma::fast_exp({k.emit(element())} - peak) * inverse"])
+                k.store(slot, out.dtype, Kernel.flatten(self._row_coords(k, row, shape, dim, Aff.of(j_atom)), shape), value)
+        self.launch(k, max(1, min(-(-rows // 256), MAX_GRID)), 256, [x])
+
+    # -------------------------------------------------------------------------------- RMSNorm
+    def norm(self, meta, x: Value, weight: Value, epsilon: float) -> Value:
+        out = self.allocate(tuple(meta.shape), meta.dtype)
+        shape = _shape(x.shape)
+        columns = shape[-1]
+        rows = math.prod(shape) // columns
+        dim = len(shape) - 1
+        threads, lanes, chunks, resident = self._row_plan(columns, x.dtype)
+        waves = threads // 64
+        k = Kernel(lanes)
+        slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        row = Aff.of(k.atom("blockIdx.x", rows - 1, prefix="r"))
+        step = threads * lanes
+        ragged = columns % step != 0
+        eps = float_literal(epsilon)
+
+        def coords(j: Aff) -> List[Aff]:
+            return self._row_coords(k, row, shape, dim, j)
+
+        def names_of(node) -> List[str]:
+            names = k.emit(node)
+            return names if isinstance(names, list) else [names] * lanes
+
+        k.line("float squares = 0.0f;")
+        if resident:
+            k.line(f"float vals[{chunks}][{lanes}];")
+        with k.block(f"for (uint32_t c = 0; c < {chunks}u; ++c) {{") if resident else k.block(
+            f"for (uint32_t base = threadIdx.x * {lanes}u; base < {columns}u; base += {step}u) {{"
+        ):
+            j = Aff.of(k.vector_atom(f"c * {step}u + threadIdx.x * {lanes}u" if resident else "base", columns - 1))
+            if resident and ragged:
+                k.line(f"if ({j.code()} < {columns}u) {{")
+                k.indent += 1
+            for lane, name in enumerate(names_of(self.read(k, x, coords(j)))):
+                if resident:
+                    k.line(f"vals[c][{lane}] = {name};")
+                k.line(f"squares += {name} * {name};")
+            if resident and ragged:
+                k.indent -= 1
+                k.line("}")
+        k.line(f"squares = chroma::block_sum<{waves}>(squares, scratch);")
+        k.line(f"const float scale = 1.0f / sqrtf(squares / {float_literal(columns)} + {eps});")
+        with k.block(f"for (uint32_t c = 0; c < {chunks}u; ++c) {{") if resident else k.block(
+            f"for (uint32_t base = threadIdx.x * {lanes}u; base < {columns}u; base += {step}u) {{"
+        ):
+            j = Aff.of(k.vector_atom(f"c * {step}u + threadIdx.x * {lanes}u" if resident else "base", columns - 1))
+            if ragged and resident:
+                k.line(f"if ({j.code()} < {columns}u) {{")
+                k.indent += 1
+            xs = [f"vals[c][{lane}]" for lane in range(lanes)] if resident else names_of(self.read(k, x, coords(j)))
+            ws = names_of(self.read(k, weight, [j]))
+            result = self._lane_values(k, [f"{xv} * scale * {wv}" for xv, wv in zip(xs, ws)])
+            k.store(slot, out.dtype, Kernel.flatten(coords(j), shape), result)
+            if ragged and resident:
+                k.indent -= 1
+                k.line("}")
+        self.launch(k, rows, threads, [x, weight], prologue=[f"__shared__ float scratch[{waves}];"])
+        self.parallel_reductions += 1
+        return out
+
+    # ------------------------------------------------------------------------------ reduction
+    def reduction(self, meta, x: Value, axes: Sequence[int], keepdim: bool, mean: bool) -> Value:
+        out = self.allocate(tuple(meta.shape), meta.dtype)
+        out_shape = _shape(out.shape)
+        x_shape = tuple(x.shape)
+        reduce_shape = tuple(x_shape[d] for d in axes) or (1,)
+        width = math.prod(reduce_shape)
+        outputs = math.prod(out_shape)
+        parallel = width >= 64
+        k = Kernel(1)
+        slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        divisor = float_literal(width if mean else 1)
+
+        def element(out_coords: List[Aff], reduce_coords: List[Aff]) -> tuple:
+            coords, o, r = [], 0, 0
+            kept = [c for c, size in zip(out_coords, out_shape)] if out.shape else []
+            for d in range(len(x_shape)):
+                if d in axes:
+                    coords.append(reduce_coords[r])
+                    r += 1
+                    if keepdim:
+                        o += 1
+                else:
+                    coords.append(kept[o])
+                    o += 1
+            return self.read(k, x, coords)
+
+        if parallel:
+            groups = 4
+            k.line(f"const uint32_t o = blockIdx.x * {groups}u + threadIdx.x / 64u;")
+            k.line(f"if (o >= {outputs}u) return;")
+            k.line("float sum = 0.0f;")
+            out_coords = k.unflatten(Aff.of(Atom("o", outputs - 1)), out_shape) if out.shape else []
+            with k.block(f"for (uint32_t r = threadIdx.x % 64u; r < {width}u; r += 64u) {{"):
+                reduce_coords = k.unflatten(Aff.of(Atom("r", width - 1)), reduce_shape)
+                k.line(f"sum += {k.emit(element(out_coords, reduce_coords))};")
+            k.line("sum = chroma::wave_sum(sum);")
+            k.line("if (threadIdx.x % 64u == 0) {")
+            k.indent += 1
+            k.store(slot, out.dtype, Aff.of(Atom("o", outputs - 1)), self._lane_values(k, [f"sum / {divisor}"]))
+            k.indent -= 1
+            k.line("}")
+            self.launch(k, -(-outputs // groups), 64 * groups, [x])
+            self.parallel_reductions += 1
+        else:
+            with k.block(f"for (uint32_t o = blockIdx.x * 256u + threadIdx.x; o < {outputs}u; o += gridDim.x * 256u) {{"):
+                out_coords = k.unflatten(Aff.of(Atom("o", outputs - 1)), out_shape) if out.shape else []
+                k.line("float sum = 0.0f;")
+                with k.block(f"for (uint32_t r = 0; r < {width}u; ++r) {{"):
+                    reduce_coords = k.unflatten(Aff.of(Atom("r", width - 1)), reduce_shape)
+                    k.line(f"sum += {k.emit(element(out_coords, reduce_coords))};")
+                k.store(slot, out.dtype, Aff.of(Atom("o", outputs - 1)), self._lane_values(k, [f"sum / {divisor}"]))
+            self.launch(k, max(1, min(-(-outputs // 256), MAX_GRID)), 256, [x])
+        return out
+
+    # ------------------------------------------------------------------------------------ top-k
+    def topk(self, meta, x: Value, dim: int, largest: bool, sort: bool):
+        values = self.allocate(tuple(meta[0].shape), meta[0].dtype)
+        indices = self.allocate(tuple(meta[1].shape), meta[1].dtype)
+        shape = tuple(x.shape)
+        width, inner, outer = self._row_layout(shape, dim)
+        count = meta[0].shape[dim]
+        rows = outer * inner
+        per_lane = -(-width // 64)
+        groups = 4
+        k = Kernel(1)
+        value_slot = k.slot(values.name, values.dtype, writable=True, extent=self.extents[values.name])
+        index_slot = k.slot(indices.name, indices.dtype, writable=True, extent=self.extents[indices.name])
+        k.line(f"const uint32_t r = blockIdx.x * {groups}u + threadIdx.x / 64u;")
+        k.line(f"if (r >= {rows}u) return;")
+        k.line("const uint32_t lane = threadIdx.x % 64u;")
+        k.line(f"uint64_t keys[{per_lane}];")
+        k.line(f"float vals[{per_lane}];")
+        row = Aff.of(Atom("r", rows - 1))
+        k.line("#pragma unroll")
+        with k.block(f"for (uint32_t p = 0; p < {per_lane}u; ++p) {{"):
+            k.line("const uint32_t j = p * 64u + lane;")
+            k.line(f"if (j < {width}u) {{")
+            k.indent += 1
+            j = Aff.of(Atom("j", width - 1))
+            name = k.emit(self.read(k, x, self._row_coords(k, row, shape, dim, j)))
+            k.line(f"vals[p] = {name}; keys[p] = chroma::topk_key({name}, j, {str(bool(largest)).lower()});")
+            k.indent -= 1
+            k.line("} else { vals[p] = 0.0f; keys[p] = 0; }")
+        with k.block(f"for (uint32_t s = 0; s < {count}u; ++s) {{"):
+            k.line("uint64_t best = 0;")
+            k.line("#pragma unroll")
+            k.line(f"for (uint32_t p = 0; p < {per_lane}u; ++p) best = keys[p] > best ? keys[p] : best;")
+            k.line("const uint64_t top = chroma::wave_max_u64(best);")
+            k.line("const uint32_t winner = 0xffffffffu - uint32_t(top);")
+            k.line("if (winner % 64u == lane) {")
+            k.indent += 1
+            k.line("float chosen = 0.0f;")
+            k.line("#pragma unroll")
+            k.line(f"for (uint32_t p = 0; p < {per_lane}u; ++p) if (p == winner / 64u) {{ chosen = vals[p]; keys[p] = 0; }}")
+            s = Aff.of(Atom("s", count - 1))
+            out_coords = self._row_coords(k, row, tuple(meta[0].shape), dim, s)
+            address = Kernel.flatten(out_coords, tuple(meta[0].shape))
+            k.store(value_slot, values.dtype, address, self._lane_values(k, ["chosen"]))
+            k.line(f"{index_slot}[{address.code()}] = int64_t(winner);")
+            k.indent -= 1
+            k.line("}")
+        self.launch(k, -(-rows // groups), 64 * groups, [x])
+        return values, indices
+
+    # =================================================================================== linear
+    def linear(self, meta, x: Value, weight: Value, bias: Optional[Value]) -> Value:
+        rows, columns, inner = math.prod(x.shape[:-1]), weight.shape[0], weight.shape[1]
+        if max(rows, columns, inner) > 2**31 - 1:
+            raise ValueError("Matrix dimensions exceed the integer range of the matrix kernels")
+        x, weight = self.materialize(x), self.materialize(weight)
+        bias = self.materialize(bias) if bias is not None else None
+        out = self.allocate(tuple(meta.shape), meta.dtype)
+        dtypes = {x.dtype, weight.dtype, meta.dtype} | ({bias.dtype} if bias is not None else set())
+        if len(dtypes) != 1:
+            raise NotImplementedError(f"mixed-dtype linear {dtypes}")
+        inputs = [x, weight] + ([bias] if bias is not None else [])
+        if self.blas and rows <= 16 and inner % 4 == 0:
+            self._skinny_linear(out, x, weight, bias, rows, columns, inner)
+            self.skinny_matmuls += 1
+        elif self.blas and inner % 4 == 0:
+            self._tiled_linear(out, x, weight, bias, rows, columns, inner)
+            self.tiled_matmuls += 1
+        else:
+            self._scalar_linear(out, x, weight, bias, rows, columns, inner)
+        return out
+
+    def _matrix_slot(self, k: Kernel, value: Value) -> str:
+        """A pointer to a stored, row-major value (an alias is rebased onto its root at its offset)."""
+        root = value.root
+        slot = k.slot(root.name, root.dtype)
+        offset = value.view.offset
+        return f"({slot} + {offset}u)" if offset else slot
+
+    def _skinny_linear(self, out, x, weight, bias, rows, columns, inner) -> None:
+        lanes_per_row = 64
+        while lanes_per_row > 1 and inner % (4 * lanes_per_row):
+            lanes_per_row //= 2
+        k = Kernel(1)
+        args = [self._matrix_slot(k, x), self._matrix_slot(k, weight), self._matrix_slot(k, bias) if bias is not None else "nullptr"]
+        out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        rows_per_wave = 64 // lanes_per_row
+        waves = -(-columns // rows_per_wave)
+        blocks = min(-(-waves // 4), 8192)
+        ctype = ctype_of(out.dtype)
+        k.line(
+            f"chroma::skinny_linear<{rows}, {inner}, {lanes_per_row}, {ctype}>("
+            f"{args[0]}, {args[1]}, {args[2]}, {out_slot}, {columns}u);"
+        )
+        self.launch(k, blocks, 256, [x, weight] + ([bias] if bias is not None else []))
+
+    def _tiled_linear(self, out, x, weight, bias, rows, columns, inner) -> None:
+        k = Kernel(1)
+        args = [self._matrix_slot(k, x), self._matrix_slot(k, weight), self._matrix_slot(k, bias) if bias is not None else "nullptr"]
+        out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        ctype = ctype_of(out.dtype)
+        k.line(f"chroma::tiled_linear<{ctype}>({args[0]}, {args[1]}, {args[2]}, {out_slot}, {rows}u, {columns}u, {inner}u);")
+        self.launch(k, (-(-columns // 64), -(-rows // 64), 1), 256, [x, weight] + ([bias] if bias is not None else []))
+
+    def _scalar_linear(self, out, x, weight, bias, rows, columns, inner) -> None:
+        k = Kernel(1)
+        slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        total = rows * columns
+        with k.block(f"for (uint32_t o = blockIdx.x * 256u + threadIdx.x; o < {total}u; o += gridDim.x * 256u) {{"):
+            o = Atom("o", total - 1)
+            row, column = k.div(Aff.of(o), columns), k.mod(Aff.of(o), columns)
+            kk = Aff.of(Atom("kk", inner - 1))
+            k.line("float sum = 0.0f;")
+            with k.block(f"for (uint32_t kk = 0; kk < {inner}u; ++kk) {{"):
+                a = k.emit(self.read_flat(k, x, row.scale(inner) + kk))
+                b = k.emit(self.read_flat(k, weight, column.scale(inner) + kk))
+                k.line(f"sum += {a} * {b};")
+            if bias is not None:
+                k.line(f"sum += {k.emit(self.read(k, bias, [column]))};")
+            k.store(slot, out.dtype, Aff.of(o), self._lane_values(k, ["sum"]))
+        self.launch(k, max(1, min(-(-total // 256), MAX_GRID)), 256, [x, weight] + ([bias] if bias is not None else []))
+
+    # ================================================================================= einsum
+    def einsum(self, meta, eqn: str, values: Sequence[Value]) -> Value:
+        labels, output, sizes, reduction = contraction(eqn, values)
+        eqn = eqn.replace(" ", "")
+        expert = self._expert_einsum(meta, eqn, labels, sizes, values)
+        if expert is not None:
+            return expert
+        prepared = []
+        for label, value in zip(labels, values):
+            reuse = math.prod(sizes[letter] for letter in output if letter not in label)
+            if not value.stored and value.view is None and reuse >= 8:
+                value = self.materialize(value)
+            prepared.append(value)
+        return self._loop_einsum(meta, labels, output, sizes, reduction, prepared)
+
+    def _expert_einsum(self, meta, eqn, labels, sizes, values) -> Optional[Value]:
+        if not self.blas or eqn not in ("beck,bk->bec", "beck,bek->bec"):
+            return None
+        source = self.gathers.get(values[0].name)
+        if source is None:
+            return None
+        for label, value in zip(labels, values):
+            if any(size != sizes[letter] for letter, size in zip(label, value.shape)):
+                return None
+        weight, indices = source
+        if weight.dtype != meta.dtype or weight.shape[-1] % 4:
+            return None
+        weight, indices, x = self.materialize(weight), self.materialize(indices), self.materialize(values[1])
+        if x.dtype != meta.dtype:
+            return None
+        out = self.allocate(tuple(meta.shape), meta.dtype)
+        tokens, selected, channels = out.shape
+        inner = weight.shape[-1]
+        experts = weight.shape[0]
+        lanes_per_row = 64
+        while lanes_per_row > 1 and inner % (4 * lanes_per_row):
+            lanes_per_row //= 2
+        k = Kernel(1)
+        w, idx, xs = self._matrix_slot(k, weight), self._matrix_slot(k, indices), self._matrix_slot(k, x)
+        out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        k.uses_error = True
+        per_expert = "true" if eqn == "beck,bek->bec" else "false"
+        rows_per_wave = 64 // lanes_per_row
+        blocks_per_slot = -(-(-(-channels // rows_per_wave)) // 4)
+        k.line(
+            f"chroma::expert_linear<{inner}, {lanes_per_row}, {ctype_of(out.dtype)}, {per_expert}>("
+            f"{w}, {idx}, {xs}, {out_slot}, {selected}u, {experts}u, {channels}u, {blocks_per_slot}u, error);"
+        )
+        self.launch(k, (blocks_per_slot, tokens * selected, 1), 256, [weight, indices, x])
+        self.expert_contractions += 1
+        return out
+
+    def _loop_einsum(self, meta, labels, output, sizes, reduction, values) -> Value:
+        out = self.allocate(tuple(meta.shape), meta.dtype)
+        out_shape = _shape(out.shape)
+        outputs = math.prod(out_shape)
+        reduce_shape = tuple(sizes[letter] for letter in reduction) or (1,)
+        width = math.prod(reduce_shape) if reduction else 1
+        parallel = width >= 512
+        k = Kernel(1)
+        slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+
+        def product(out_coords: List[Aff], reduce_coords: List[Aff]) -> str:
+            by_label = dict(zip(output, out_coords))
+            by_label.update(zip(reduction, reduce_coords))
+            factors = []
+            for label, value in zip(labels, values):
+                coords = [ZERO if size == 1 else by_label[letter] for letter, size in zip(label, value.shape)]
+                factors.append(k.emit(self.read(k, value, coords)))
+            return f"{factors[0]} * {factors[1]}"
+
+        if parallel:
+            groups = 4
+            k.line(f"const uint32_t o = blockIdx.x * {groups}u + threadIdx.x / 64u;")
+            k.line(f"if (o >= {outputs}u) return;")
+            out_coords = k.unflatten(Aff.of(Atom("o", outputs - 1)), out_shape) if meta.shape else []
+            k.line("float sum = 0.0f;")
+            with k.block(f"for (uint32_t r = threadIdx.x % 64u; r < {width}u; r += 64u) {{"):
+                reduce_coords = k.unflatten(Aff.of(Atom("r", width - 1)), reduce_shape)
+                k.line(f"sum += {product(out_coords, reduce_coords)};")
+            k.line("sum = chroma::wave_sum(sum);")
+            k.line("if (threadIdx.x % 64u == 0) {")
+            k.indent += 1
+            k.store(slot, out.dtype, Aff.of(Atom("o", outputs - 1)), self._lane_values(k, ["sum"]))
+            k.indent -= 1
+            k.line("}")
+            self.launch(k, -(-outputs // groups), 64 * groups, values)
+            self.parallel_reductions += 1
+        else:
+            with k.block(f"for (uint32_t o = blockIdx.x * 256u + threadIdx.x; o < {outputs}u; o += gridDim.x * 256u) {{"):
+                out_coords = k.unflatten(Aff.of(Atom("o", outputs - 1)), out_shape) if meta.shape else []
+                k.line("float sum = 0.0f;")
+                if reduction:
+                    with k.block(f"for (uint32_t r = 0; r < {width}u; ++r) {{"):
+                        reduce_coords = k.unflatten(Aff.of(Atom("r", width - 1)), reduce_shape)
+                        k.line(f"sum += {product(out_coords, reduce_coords)};")
+                else:
+                    k.line(f"sum += {product(out_coords, [])};")
+                k.store(slot, out.dtype, Aff.of(Atom("o", outputs - 1)), self._lane_values(k, ["sum"]))
+            self.launch(k, max(1, min(-(-outputs // 256), MAX_GRID)), 256, values)
+        return out
+
+    # ================================================================================== finish
+    def generate(self, inputs: List[TensorSpec], outputs: List[TensorSpec], stats: Stats) -> GeneratedCode:
+        weights_size = len(self.weights)
+        workspace_base = _align(weights_size)
+        error_base = workspace_base + _align(stats["workspace_bytes"])
+        position = error_base + ALIGN
+        input_regions, output_regions = [], []
+        for spec in inputs:
+            input_regions.append((position, nbytes(spec)))
+            position += _align(max(nbytes(spec), 1))
+        for spec in outputs:
+            output_regions.append((position, nbytes(spec)))
+            position += _align(max(nbytes(spec), 1))
+        total = position
+
+        def resolve(binding: Binding) -> int:
+            if binding.kind == "weight":
+                return binding.offset
+            if binding.kind == "input":
+                return input_regions[binding.index][0] + binding.offset
+            if binding.kind == "output":
+                return output_regions[binding.index][0] + binding.offset
+            if binding.kind == "arena":
+                name = binding.index
+                if name in self.output_buffers:
+                    return output_regions[self.output_buffers[name]][0] + binding.offset
+                return workspace_base + self.allocations[name].offset + binding.offset
+            if binding.kind == "error":
+                return error_base
+            raise AssertionError(binding)
+
+        lines = [
+            "chroma-hip-plan 1",
+            f"arena {total}",
+            f"weights {weights_size}",
+            f"error {error_base}",
+        ]
+        lines += [f"input {i} {offset} {size}" for i, (offset, size) in enumerate(input_regions)]
+        lines += [f"output {i} {offset} {size}" for i, (offset, size) in enumerate(output_regions)]
+        for launch in self.launches:
+            offsets = [resolve(b) for b in launch.bindings] + [error_base]
+            grid = " ".join(map(str, launch.grid))
+            lines.append(f"launch {launch.kernel} {grid} {launch.block} {launch.shared} {len(offsets)} {' '.join(map(str, offsets))}")
+        stats = dict(
+            stats,
+            backend="hip",
+            input_bytes=sum(map(nbytes, inputs)),
+            hip_buffer_bytes=total,
+            parallel_reductions=self.parallel_reductions,
+            expert_contractions=self.expert_contractions,
+            tiled_matmuls=self.tiled_matmuls,
+            skinny_matmuls=self.skinny_matmuls,
+            unique_kernels=len(self.kernel_sources),
+            launches=len(self.launches),
+        )
+        source = "#include <chroma_hip/kernels.h>\n\n" + "\n\n".join(self.kernel_sources) + "\n"
+        plan = "\n".join(lines) + "\n"
+        return GeneratedCode({"model.hip": source, "model.plan": plan}, "model.hip", [], stats, inputs, outputs, bytes(self.weights))

@@ -1,0 +1,114 @@
+"""Locate, build and bind the hip runtime library (``libchroma_hip.so``, C ABI in include/chroma_hip.h).
+
+The library is built in-tree (``chroma_amd/lib``) by ``build_runtime``; loading never builds, so a GPU
+host runs exactly the library that was compiled and shipped with the tree. There is no fallback: if the
+library is missing, loading a program fails with a message saying how to build it.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import shlex
+import subprocess
+import threading
+from pathlib import Path
+
+PACKAGE = Path(__file__).resolve().parents[1]
+REPO = PACKAGE.parent
+LIBRARY = PACKAGE / "lib" / "libchroma_hip.so"
+RUNTIME_SOURCE = PACKAGE / "csrc" / "runtime.cpp"
+DEVICE_INCLUDE = PACKAGE / "csrc" / "include"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+
+OK, INDEX_ERROR, RUNTIME_ERROR = 0, 1, 2
+
+_lock = threading.Lock()
+_library = None
+
+
+def build_runtime(output: Path = LIBRARY) -> Path:
+    """Compile the host runtime (no device code) against the HIP runtime library."""
+    output.parent.mkdir(parents=True, exist_ok=True)
+    temporary = output.with_suffix(".so.tmp")
+    command = [
+        *shlex.split(os.environ.get("CXX", "g++")),
+        "-std=c++17",
+        "-O2",
+        "-shared",
+        "-fPIC",
+        "-fvisibility=hidden",
+        "-D__HIP_PLATFORM_AMD__",
+        f"-I{ROCM / 'include'}",
+        str(RUNTIME_SOURCE),
+        "-o",
+        str(temporary),
+        f"-L{ROCM / 'lib'}",
+        f"-Wl,-rpath,{ROCM / 'lib'}",
+        "-lamdhip64",
+    ]
+    result = subprocess.run(command, capture_output=True, text=True, check=False)
+    if result.returncode:
+        raise RuntimeError(f"Building the hip runtime failed:\n{result.stderr[-4000:]}")
+    os.replace(temporary, output)
+    return output
+
+
+def library() -> ctypes.CDLL:
+    global _library
+    with _lock:
+        if _library is not None:
+            return _library
+        if not LIBRARY.exists():
+            raise RuntimeError(
+                f"The hip runtime library {LIBRARY} is not built; run __graft_entry__.build() "
+                "(or chroma_amd._src.native.build_runtime()) first"
+            )
+        lib = ctypes.CDLL(str(LIBRARY))
+        c = ctypes
+        lib.chroma_hip_create.argtypes = [c.c_char_p, c.POINTER(c.c_void_p), c.c_char_p, c.c_size_t]
+        lib.chroma_hip_run.argtypes = [c.c_void_p, c.c_void_p, c.c_void_p, c.c_char_p, c.c_size_t]
+        lib.chroma_hip_device_name.argtypes = [c.c_void_p]
+        lib.chroma_hip_device_name.restype = c.c_char_p
+        lib.chroma_hip_signature.argtypes = [c.c_void_p]
+        lib.chroma_hip_signature.restype = c.c_char_p
+        lib.chroma_hip_destroy.argtypes = [c.c_void_p]
+        lib.chroma_hip_destroy.restype = None
+        lib.chroma_hip_upload.argtypes = [c.c_void_p, c.c_void_p, c.c_char_p, c.c_size_t]
+        lib.chroma_hip_execute.argtypes = [c.c_void_p, c.c_int, c.POINTER(c.c_float), c.c_char_p, c.c_size_t]
+        lib.chroma_hip_download.argtypes = [c.c_void_p, c.c_void_p, c.c_char_p, c.c_size_t]
+        lib.chroma_hip_set_graph.argtypes = [c.c_void_p, c.c_int]
+        lib.chroma_hip_launch_count.argtypes = [c.c_void_p]
+        lib.chroma_hip_device_base.argtypes = [c.c_void_p]
+        lib.chroma_hip_device_base.restype = c.c_void_p
+        _library = lib
+        return lib
+
+
+EXPORTED = (
+    "chroma_hip_create",
+    "chroma_hip_run",
+    "chroma_hip_device_name",
+    "chroma_hip_signature",
+    "chroma_hip_destroy",
+    "chroma_hip_upload",
+    "chroma_hip_execute",
+    "chroma_hip_download",
+    "chroma_hip_set_graph",
+    "chroma_hip_launch_count",
+    "chroma_hip_device_base",
+)
+
+
+def check(status: int, error: ctypes.Array) -> None:
+    if status == OK:
+        return
+    message = error.value.decode(errors="replace")
+    if status == INDEX_ERROR:
+        raise IndexError(message)
+    raise RuntimeError(message)
+
+
+def pointer_array(pointers) -> ctypes.Array:
+    pointers = list(pointers)
+    return (ctypes.c_void_p * max(1, len(pointers)))(*pointers)

@@ -1,0 +1,199 @@
+"""Load and call a compiled hip artifact: the runtime half of the public API.
+
+``Program(directory)`` mirrors the reference loader (chroma/_src/program.py:73-153): it checks the
+manifest version and interpreter ABI ("recompile" on mismatch), loads the native program, compares the
+tensor signature ("metadata" on mismatch), and serializes calls with one lock. The array checks the
+reference performs in its pybind11 layer (chroma/_src/core/bindings.h:17-75) happen here, before the
+C ABI is called: argument count, dtype/shape ("shape or dtype"), C-contiguity/alignment/writability of
+outputs, and overlap between any output and any other array ("output overlap"). ctypes releases the
+GIL for the duration of the native call. Loading needs NumPy only (no torch, no pybind11).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import json
+import sysconfig
+import threading
+from pathlib import Path
+from typing import Any, List, Optional, Sequence, Tuple, Union
+
+import numpy as np
+
+from chroma_amd._src import native
+from chroma_amd._src.dtypes import BFLOAT16, numpy_dtype
+from chroma_amd._src.spec import MANIFEST_VERSION, signature
+
+Array = np.ndarray
+
+
+def _checked(value: Any, spec: dict, output: bool) -> np.ndarray:
+    if not isinstance(value, np.ndarray):
+        raise TypeError("not a numpy array")
+    dtype = numpy_dtype(spec["dtype"])
+    if value.dtype != dtype or list(value.shape) != list(spec["shape"]):
+        raise ValueError("shape or dtype")
+    if not value.flags.c_contiguous or value.ctypes.data % dtype.alignment or (output and not value.flags.writeable):
+        raise ValueError("want C-contiguous, aligned, writable outputs")
+    return value
+
+
+class NativeModel:
+    """The object the reference exposes as the extension's ``Model``: ``.device`` and ``.run``."""
+
+    def __init__(self, directory: Path, inputs: List[dict], outputs: List[dict]) -> None:
+        self._lib = native.library()
+        self._inputs, self._outputs = inputs, outputs
+        handle = ctypes.c_void_p()
+        error = ctypes.create_string_buffer(1024)
+        native.check(self._lib.chroma_hip_create(str(directory).encode(), ctypes.byref(handle), error, len(error)), error)
+        self._handle = handle
+        self.device = self._lib.chroma_hip_device_name(handle).decode()
+        self.signature = self._lib.chroma_hip_signature(handle).decode()
+
+    def run(self, inputs: List[np.ndarray], outputs: List[np.ndarray]) -> None:
+        if not isinstance(inputs, list) or not isinstance(outputs, list):
+            raise TypeError("run takes two lists of arrays")
+        if len(inputs) != len(self._inputs) or len(outputs) != len(self._outputs):
+            raise ValueError("wrong number of arrays")
+        regions: List[Tuple[int, int]] = []
+        for value, spec in zip(inputs, self._inputs):
+            array = _checked(value, spec, False)
+            regions.append((array.ctypes.data, array.ctypes.data + array.nbytes))
+        for value, spec in zip(outputs, self._outputs):
+            array = _checked(value, spec, True)
+            begin, end = array.ctypes.data, array.ctypes.data + array.nbytes
+            if any(begin < last and first < end for first, last in regions):
+                raise ValueError("output overlap")
+            regions.append((begin, end))
+        error = ctypes.create_string_buffer(1024)
+        status = self._lib.chroma_hip_run(
+            self._handle,
+            native.pointer_array(a.ctypes.data for a in inputs),
+            native.pointer_array(a.ctypes.data for a in outputs),
+            error,
+            len(error),
+        )
+        native.check(status, error)
+
+    # Device-resident helpers (benchmarks and tests): upload once, execute many times, download.
+    def upload(self, inputs: Sequence[np.ndarray]) -> None:
+        arrays = [_checked(np.ascontiguousarray(a), s, False) for a, s in zip(inputs, self._inputs)]
+        error = ctypes.create_string_buffer(1024)
+        native.check(self._lib.chroma_hip_upload(self._handle, native.pointer_array(a.ctypes.data for a in arrays), error, len(error)), error)
+
+    def execute(self, iterations: int = 1, timed: bool = False) -> Optional[float]:
+        error = ctypes.create_string_buffer(1024)
+        elapsed = ctypes.c_float(0.0)
+        status = self._lib.chroma_hip_execute(self._handle, iterations, ctypes.byref(elapsed) if timed else None, error, len(error))
+        native.check(status, error)
+        return elapsed.value if timed else None
+
+    def download(self, outputs: Sequence[np.ndarray]) -> None:
+        for array, spec in zip(outputs, self._outputs):
+            _checked(array, spec, True)
+        error = ctypes.create_string_buffer(1024)
+        native.check(self._lib.chroma_hip_download(self._handle, native.pointer_array(a.ctypes.data for a in outputs), error, len(error)), error)
+
+    def set_graph(self, enabled: bool) -> bool:
+        return bool(self._lib.chroma_hip_set_graph(self._handle, int(bool(enabled))))
+
+    @property
+    def launch_count(self) -> int:
+        return int(self._lib.chroma_hip_launch_count(self._handle))
+
+    def close(self) -> None:
+        if self._handle is not None and self._handle.value:
+            self._lib.chroma_hip_destroy(self._handle)
+        self._handle = None
+
+    def __del__(self) -> None:  # pragma: no cover - interpreter shutdown order
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Program:
+    def __init__(self, directory: Union[str, Path]) -> None:
+        manifest, model = self._load(directory)
+        self._lock = threading.Lock()
+        self._model: Optional[NativeModel] = model
+        self._inputs = manifest["inputs"]
+        self._outputs = manifest["outputs"]
+        self._stats = manifest["stats"]
+        self._device = model.device
+
+    @staticmethod
+    def _load(directory: Union[str, Path]):
+        directory = Path(directory).resolve()
+        manifest = json.loads((directory / "model.json").read_text())
+        if manifest.get("version") != MANIFEST_VERSION or manifest.get("python_abi") != sysconfig.get_config_var("SOABI"):
+            raise ValueError("Incompatible Chroma artifact; recompile it with this Python interpreter")
+        if manifest.get("stats", {}).get("backend") != "hip":
+            raise ValueError("Not a hip artifact; recompile it with backend='hip'")
+        model = NativeModel(directory, manifest["inputs"], manifest["outputs"])
+        if model.signature != signature(manifest["inputs"], manifest["outputs"]):
+            model.close()
+            raise ValueError("Artifact tensor metadata does not match its native library")
+        return manifest, model
+
+    @property
+    def device(self) -> str:
+        return self._device
+
+    @property
+    def inputs(self) -> List[dict]:
+        return self._inputs
+
+    @property
+    def outputs(self) -> List[dict]:
+        return self._outputs
+
+    @property
+    def stats(self) -> dict:
+        return self._stats
+
+    @staticmethod
+    def _array(value: Any) -> Array:
+        if isinstance(value, np.ndarray):
+            array = value
+        else:
+            tensor = value.detach()
+            if str(tensor.dtype) == "torch.bfloat16":
+                import torch
+
+                array = tensor.view(torch.uint16).numpy().view(BFLOAT16)
+            else:
+                array = tensor.numpy()
+        return np.require(array, requirements=["C", "A"])
+
+    def __call__(self, *inputs: Any, out: Union[Array, Sequence[Array], None] = None):
+        arrays = [self._array(value) for value in inputs]
+        if out is None:
+            results = [np.empty(spec["shape"], dtype=numpy_dtype(spec["dtype"])) for spec in self._outputs]
+        else:
+            results = [out] if isinstance(out, np.ndarray) else list(out)
+        with self._lock:
+            if self._model is None:
+                raise RuntimeError("Model is closed")
+            self._model.run(arrays, results)
+        return results[0] if len(results) == 1 else tuple(results)
+
+    @property
+    def native(self) -> NativeModel:
+        if self._model is None:
+            raise RuntimeError("Model is closed")
+        return self._model
+
+    def close(self) -> None:
+        with self._lock:
+            if self._model is not None:
+                self._model.close()
+            self._model = None
+
+    def __enter__(self) -> "Program":
+        return self
+
+    def __exit__(self, *exc: Any) -> None:
+        self.close()

@@ -1,0 +1,5 @@
+// Umbrella header included by every generated model.hip of the hip backend.
+#pragma once
+
+#include "device.h"
+#include "linear.h"

@@ -1,0 +1,439 @@
+// Host runtime of the hip backend: the C ABI declared in include/chroma_hip.h.
+//
+// A program is one hipMalloc'd allocation laid out by the compiler (weights | workspace | error word |
+// inputs | outputs), one non-blocking stream, the code object's kernels and a launch list whose
+// arguments are pre-resolved device pointers. ``run`` uploads inputs, launches every kernel (or replays
+// the captured hipGraph), downloads the error word and the outputs, and synchronizes once.
+#include "../../include/chroma_hip.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <map>
+#include <memory>
+#include <sstream>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace {
+
+struct HipError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+struct IndexError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+void check(hipError_t status, const char* what) {
+    if (status != hipSuccess) {
+        throw HipError(std::string(what) + ": " + hipGetErrorString(status));
+    }
+}
+
+class DeviceGuard {
+public:
+    explicit DeviceGuard(int device) {
+        check(hipGetDevice(&previous_), "hipGetDevice");
+        if (previous_ != device) {
+            check(hipSetDevice(device), "hipSetDevice");
+        }
+        device_ = device;
+    }
+    ~DeviceGuard() {
+        if (previous_ != device_) {
+            hipSetDevice(previous_);
+        }
+    }
+
+private:
+    int previous_ = 0;
+    int device_ = 0;
+};
+
+struct Region {
+    size_t offset = 0;
+    size_t bytes = 0;
+};
+
+struct Launch {
+    std::string kernel;
+    unsigned grid[3] = {1, 1, 1};
+    unsigned block = 1;
+    unsigned shared = 0;
+    std::vector<size_t> offsets;
+    hipFunction_t function = nullptr;
+    std::vector<void*> pointers;  // device pointers, one per kernel parameter
+    std::vector<void*> arguments;  // addresses of ``pointers`` entries, as hipModuleLaunchKernel wants
+};
+
+struct Plan {
+    std::string signature, code_object, weights_file;
+    size_t arena = 0, weight_bytes = 0, error = 0;
+    std::vector<Region> inputs, outputs;
+    std::vector<Launch> launches;
+};
+
+Plan read_plan(const std::string& path) {
+    std::ifstream stream(path);
+    if (!stream) {
+        throw std::runtime_error("Cannot open the launch plan " + path);
+    }
+    Plan plan;
+    std::string line;
+    std::getline(stream, line);
+    if (line != "chroma-hip-plan 1") {
+        throw std::runtime_error("Unsupported launch plan version in " + path);
+    }
+    while (std::getline(stream, line)) {
+        std::istringstream fields(line);
+        std::string key;
+        fields >> key;
+        if (key == "signature") {
+            fields >> plan.signature;
+        } else if (key == "code_object") {
+            fields >> plan.code_object;
+        } else if (key == "weights_file") {
+            fields >> plan.weights_file;
+        } else if (key == "arena") {
+            fields >> plan.arena;
+        } else if (key == "weights") {
+            fields >> plan.weight_bytes;
+        } else if (key == "error") {
+            fields >> plan.error;
+        } else if (key == "input" || key == "output") {
+            size_t index = 0;
+            Region region;
+            fields >> index >> region.offset >> region.bytes;
+            auto& list = key == "input" ? plan.inputs : plan.outputs;
+            if (index != list.size()) {
+                throw std::runtime_error("Launch plan regions out of order");
+            }
+            list.push_back(region);
+        } else if (key == "launch") {
+            Launch launch;
+            size_t count = 0;
+            fields >> launch.kernel >> launch.grid[0] >> launch.grid[1] >> launch.grid[2] >> launch.block >> launch.shared >> count;
+            launch.offsets.resize(count);
+            for (auto& offset : launch.offsets) {
+                fields >> offset;
+            }
+            if (!fields) {
+                throw std::runtime_error("Malformed launch line: " + line);
+            }
+            plan.launches.push_back(std::move(launch));
+        } else if (!key.empty()) {
+            throw std::runtime_error("Unknown launch plan entry: " + key);
+        }
+    }
+    for (const auto& launch : plan.launches) {
+        for (size_t offset : launch.offsets) {
+            if (offset >= plan.arena) {
+                throw std::runtime_error("Launch plan argument outside the program allocation");
+            }
+        }
+    }
+    return plan;
+}
+
+class Program {
+public:
+    Program(const std::string& directory) {
+        plan_ = read_plan(directory + "/model.plan");
+        check(hipGetDevice(&device_), "hipGetDevice");
+        hipDeviceProp_t properties{};
+        check(hipGetDeviceProperties(&properties, device_), "hipGetDeviceProperties");
+        name_ = std::string(properties.name) + " (" + properties.gcnArchName + ")";
+        check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+        check(hipEventCreate(&start_), "hipEventCreate");
+        check(hipEventCreate(&stop_), "hipEventCreate");
+        check(hipHostMalloc(reinterpret_cast<void**>(&error_host_), sizeof(unsigned), hipHostMallocDefault), "hipHostMalloc");
+        check(hipMalloc(&base_, plan_.arena ? plan_.arena : 1), "hipMalloc program allocation");
+        check(hipMemset(static_cast<char*>(base_) + plan_.error, 0, sizeof(unsigned)), "Clear index error");
+        upload_weights(directory + "/" + plan_.weights_file);
+        check(hipModuleLoad(&module_, (directory + "/" + plan_.code_object).c_str()), "hipModuleLoad");
+        std::map<std::string, hipFunction_t> functions;
+        for (auto& launch : plan_.launches) {
+            auto found = functions.find(launch.kernel);
+            if (found == functions.end()) {
+                hipFunction_t function = nullptr;
+                check(hipModuleGetFunction(&function, module_, launch.kernel.c_str()), "hipModuleGetFunction");
+                found = functions.emplace(launch.kernel, function).first;
+            }
+            launch.function = found->second;
+            launch.pointers.resize(launch.offsets.size());
+            launch.arguments.resize(launch.offsets.size());
+            for (size_t i = 0; i < launch.offsets.size(); ++i) {
+                launch.pointers[i] = static_cast<char*>(base_) + launch.offsets[i];
+                launch.arguments[i] = &launch.pointers[i];
+            }
+        }
+        const char* graph = std::getenv("CHROMA_HIP_GRAPH");
+        use_graph_ = graph != nullptr && std::strcmp(graph, "1") == 0;
+    }
+
+    ~Program() {
+        DeviceGuard guard(device_);
+        if (stream_) {
+            hipStreamSynchronize(stream_);
+        }
+        if (graph_exec_) {
+            hipGraphExecDestroy(graph_exec_);
+        }
+        if (graph_) {
+            hipGraphDestroy(graph_);
+        }
+        if (module_) {
+            hipModuleUnload(module_);
+        }
+        if (base_) {
+            hipFree(base_);
+        }
+        if (error_host_) {
+            hipHostFree(error_host_);
+        }
+        if (start_) {
+            hipEventDestroy(start_);
+        }
+        if (stop_) {
+            hipEventDestroy(stop_);
+        }
+        if (stream_) {
+            hipStreamDestroy(stream_);
+        }
+    }
+
+    const std::string& name() const { return name_; }
+    const std::string& signature() const { return plan_.signature; }
+    int launch_count() const { return static_cast<int>(plan_.launches.size()); }
+    void* base() const { return base_; }
+
+    int set_graph(int enabled) {
+        const int previous = use_graph_ ? 1 : 0;
+        use_graph_ = enabled != 0;
+        return previous;
+    }
+
+    void run(const void* const* inputs, void* const* outputs) {
+        DeviceGuard guard(device_);
+        try {
+            upload(inputs);
+            launch_all();
+            check(hipMemcpyAsync(error_host_, static_cast<char*>(base_) + plan_.error, sizeof(unsigned), hipMemcpyDeviceToHost, stream_),
+                  "Read index error");
+            download(outputs);
+            check(hipStreamSynchronize(stream_), "HIP execution");
+            raise_index_error();
+        } catch (const HipError&) {
+            hipStreamSynchronize(stream_);  // host arrays must outlive every queued copy
+            throw;
+        }
+    }
+
+    void upload(const void* const* inputs) {
+        DeviceGuard guard(device_);
+        for (size_t i = 0; i < plan_.inputs.size(); ++i) {
+            if (plan_.inputs[i].bytes) {
+                check(hipMemcpyAsync(static_cast<char*>(base_) + plan_.inputs[i].offset, inputs[i], plan_.inputs[i].bytes,
+                                     hipMemcpyHostToDevice, stream_),
+                      "Upload input");
+            }
+        }
+    }
+
+    void download(void* const* outputs) {
+        DeviceGuard guard(device_);
+        for (size_t i = 0; i < plan_.outputs.size(); ++i) {
+            if (plan_.outputs[i].bytes) {
+                check(hipMemcpyAsync(outputs[i], static_cast<char*>(base_) + plan_.outputs[i].offset, plan_.outputs[i].bytes,
+                                     hipMemcpyDeviceToHost, stream_),
+                      "Download output");
+            }
+        }
+    }
+
+    void finish_download() { check(hipStreamSynchronize(stream_), "Download output"); }
+
+    float execute(int iterations, bool timed) {
+        DeviceGuard guard(device_);
+        if (timed) {
+            check(hipEventRecord(start_, stream_), "hipEventRecord");
+        }
+        for (int i = 0; i < iterations; ++i) {
+            launch_all();
+        }
+        float milliseconds = 0.0f;
+        if (timed) {
+            check(hipEventRecord(stop_, stream_), "hipEventRecord");
+        }
+        check(hipMemcpyAsync(error_host_, static_cast<char*>(base_) + plan_.error, sizeof(unsigned), hipMemcpyDeviceToHost, stream_),
+              "Read index error");
+        check(hipStreamSynchronize(stream_), "HIP execution");
+        if (timed) {
+            check(hipEventElapsedTime(&milliseconds, start_, stop_), "hipEventElapsedTime");
+        }
+        raise_index_error();
+        return milliseconds;
+    }
+
+private:
+    void raise_index_error() {
+        if (*error_host_) {
+            *error_host_ = 0;
+            check(hipMemsetAsync(static_cast<char*>(base_) + plan_.error, 0, sizeof(unsigned), stream_), "Clear index error");
+            check(hipStreamSynchronize(stream_), "Clear index error");
+            throw IndexError("Tensor index out of range");
+        }
+    }
+
+    void launch_direct() {
+        for (auto& launch : plan_.launches) {
+            check(hipModuleLaunchKernel(launch.function, launch.grid[0], launch.grid[1], launch.grid[2], launch.block, 1, 1,
+                                        launch.shared, stream_, launch.arguments.data(), nullptr),
+                  "hipModuleLaunchKernel");
+        }
+    }
+
+    void launch_all() {
+        if (!use_graph_ || plan_.launches.empty()) {
+            launch_direct();
+            return;
+        }
+        if (!graph_exec_) {
+            check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+            try {
+                launch_direct();
+            } catch (...) {
+                hipGraph_t broken = nullptr;
+                hipStreamEndCapture(stream_, &broken);
+                if (broken) {
+                    hipGraphDestroy(broken);
+                }
+                throw;
+            }
+            check(hipStreamEndCapture(stream_, &graph_), "hipStreamEndCapture");
+            check(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0), "hipGraphInstantiate");
+        }
+        check(hipGraphLaunch(graph_exec_, stream_), "hipGraphLaunch");
+    }
+
+    void upload_weights(const std::string& path) {
+        std::FILE* file = std::fopen(path.c_str(), "rb");
+        long size = -1;
+        if (file && std::fseek(file, 0, SEEK_END) == 0) {
+            size = std::ftell(file);
+        }
+        if (!file || size < 0 || static_cast<size_t>(size) != plan_.weight_bytes) {
+            if (file) {
+                std::fclose(file);
+            }
+            throw std::runtime_error("Missing weights file or incorrect byte size");
+        }
+        std::rewind(file);
+        // Stream through a pinned staging buffer so large weight files never need a host copy of their size.
+        const size_t chunk = size_t(64) << 20;
+        char* staging = nullptr;
+        check(hipHostMalloc(reinterpret_cast<void**>(&staging), chunk, hipHostMallocDefault), "hipHostMalloc");
+        std::unique_ptr<char, hipError_t (*)(void*)> owner(staging, hipHostFree);
+        for (size_t done = 0; done < plan_.weight_bytes;) {
+            const size_t bytes = std::min(chunk, plan_.weight_bytes - done);
+            if (std::fread(staging, 1, bytes, file) != bytes) {
+                std::fclose(file);
+                throw std::runtime_error("Cannot read weights");
+            }
+            check(hipMemcpy(static_cast<char*>(base_) + done, staging, bytes, hipMemcpyHostToDevice), "Upload weights");
+            done += bytes;
+        }
+        std::fclose(file);
+    }
+
+    Plan plan_;
+    int device_ = -1;
+    std::string name_;
+    hipStream_t stream_ = nullptr;
+    hipEvent_t start_ = nullptr, stop_ = nullptr;
+    void* base_ = nullptr;
+    unsigned* error_host_ = nullptr;
+    hipModule_t module_ = nullptr;
+    bool use_graph_ = false;
+    hipGraph_t graph_ = nullptr;
+    hipGraphExec_t graph_exec_ = nullptr;
+};
+
+int fail(int status, const char* message, char* error, size_t size) {
+    if (error && size) {
+        std::snprintf(error, size, "%s", message);
+    }
+    return status;
+}
+
+template <class F> int guarded(char* error, size_t size, F body) {
+    try {
+        body();
+        return CHROMA_HIP_OK;
+    } catch (const IndexError& e) {
+        return fail(CHROMA_HIP_INDEX_ERROR, e.what(), error, size);
+    } catch (const std::exception& e) {
+        return fail(CHROMA_HIP_RUNTIME_ERROR, e.what(), error, size);
+    } catch (...) {
+        return fail(CHROMA_HIP_RUNTIME_ERROR, "unknown error", error, size);
+    }
+}
+
+Program* program(void* handle) { return static_cast<Program*>(handle); }
+
+}  // namespace
+
+extern "C" {
+
+__attribute__((visibility("default"))) int chroma_hip_create(const char* artifact_dir, void** handle, char* error, size_t error_size) {
+    return guarded(error, error_size, [&] {
+        *handle = nullptr;
+        *handle = new Program(artifact_dir);
+    });
+}
+
+__attribute__((visibility("default"))) int chroma_hip_run(void* handle, const void* const* inputs, void* const* outputs, char* error,
+                                                          size_t error_size) {
+    return guarded(error, error_size, [&] { program(handle)->run(inputs, outputs); });
+}
+
+__attribute__((visibility("default"))) const char* chroma_hip_device_name(void* handle) { return program(handle)->name().c_str(); }
+
+__attribute__((visibility("default"))) const char* chroma_hip_signature(void* handle) { return program(handle)->signature().c_str(); }
+
+__attribute__((visibility("default"))) void chroma_hip_destroy(void* handle) { delete program(handle); }
+
+__attribute__((visibility("default"))) int chroma_hip_upload(void* handle, const void* const* inputs, char* error, size_t error_size) {
+    return guarded(error, error_size, [&] {
+        program(handle)->upload(inputs);
+        program(handle)->finish_download();
+    });
+}
+
+__attribute__((visibility("default"))) int chroma_hip_execute(void* handle, int iterations, float* milliseconds, char* error,
+                                                              size_t error_size) {
+    return guarded(error, error_size, [&] {
+        const float elapsed = program(handle)->execute(iterations, milliseconds != nullptr);
+        if (milliseconds) {
+            *milliseconds = elapsed;
+        }
+    });
+}
+
+__attribute__((visibility("default"))) int chroma_hip_download(void* handle, void* const* outputs, char* error, size_t error_size) {
+    return guarded(error, error_size, [&] {
+        program(handle)->download(outputs);
+        program(handle)->finish_download();
+    });
+}
+
+__attribute__((visibility("default"))) int chroma_hip_set_graph(void* handle, int enabled) { return program(handle)->set_graph(enabled); }
+
+__attribute__((visibility("default"))) int chroma_hip_launch_count(void* handle) { return program(handle)->launch_count(); }
+
+__attribute__((visibility("default"))) void* chroma_hip_device_base(void* handle) { return program(handle)->base(); }
+}

@@ -1,0 +1,73 @@
+/* C ABI of the hip backend runtime (libchroma_hip.so).
+ *
+ * The runtime owns one device allocation per program (weights | workspace | error word | input staging |
+ * output staging), uploads the weights once, and runs the compiled launch plan with
+ * hipModuleLaunchKernel (optionally replayed as a captured hipGraph) on its own stream.
+ *
+ * Status codes: 0 ok, 1 index error (a gather or expert index was out of range; the program stays usable),
+ * 2 runtime error. On a non-zero status ``error`` receives a NUL-terminated message (at most
+ * ``error_size`` bytes including the terminator).
+ */
+#ifndef CHROMA_HIP_H
+#define CHROMA_HIP_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CHROMA_HIP_OK 0
+#define CHROMA_HIP_INDEX_ERROR 1
+#define CHROMA_HIP_RUNTIME_ERROR 2
+
+/* Load the compiled artifact in ``artifact_dir`` (its model.plan, code object and weights file) on the
+ * current device. Replaces the reference's generated ``create_model(const char* weights)`` +
+ * ``chroma::cuda::Runner::initialize`` (chroma/_src/codegen/cuda/codegen.py:35-40,
+ * chroma/_src/codegen/cuda/runtime.h:116-145). A weights file of the wrong size fails with
+ * "Missing weights file or incorrect byte size" (chroma/_src/core/tensor.h:29-33). */
+int chroma_hip_create(const char* artifact_dir, void** handle, char* error, size_t error_size);
+
+/* One synchronous call: copy every input from host memory, run the plan, copy every output back.
+ * Replaces ``ModelProgram::run(const void* const* inputs, void* const* outputs)`` /
+ * ``Runner::run`` (chroma/_src/codegen/cuda/codegen.py:29-33, runtime.h:147-173). Input and output
+ * pointers are host buffers with exactly the manifest's byte sizes. */
+int chroma_hip_run(void* handle, const void* const* inputs, void* const* outputs, char* error, size_t error_size);
+
+/* Device name for ``Program.device`` (the reference's ``Runner::device_name``, runtime.h:182). */
+const char* chroma_hip_device_name(void* handle);
+
+/* sha256 signature of the tensor specs the plan was compiled for (the reference extension's
+ * ``signature`` attribute, chroma/_src/build.py:53-57, checked by program.py:98-99). */
+const char* chroma_hip_signature(void* handle);
+
+/* Release every device allocation after the stream drains (runtime.h:94-114). */
+void chroma_hip_destroy(void* handle);
+
+/* --- device-resident execution (no counterpart in the reference: benchmarking and callers that keep
+ * data on the device between calls) --- */
+
+/* Copy host inputs into the program's input staging regions (no launch). */
+int chroma_hip_upload(void* handle, const void* const* inputs, char* error, size_t error_size);
+
+/* Run the plan ``iterations`` times on whatever the staging regions hold, then synchronize and check the
+ * error word. If ``milliseconds`` is non-null it receives the total time between hipEvents recorded on
+ * the runtime's stream around the launches. */
+int chroma_hip_execute(void* handle, int iterations, float* milliseconds, char* error, size_t error_size);
+
+/* Copy the output staging regions to host buffers. */
+int chroma_hip_download(void* handle, void* const* outputs, char* error, size_t error_size);
+
+/* Select plain launches (0) or hipGraph replay of the whole plan (1). Returns the previous mode. */
+int chroma_hip_set_graph(void* handle, int enabled);
+
+/* Number of launches in the plan, and the device address of the program's allocation (for tests that
+ * inspect device memory through another API). */
+int chroma_hip_launch_count(void* handle);
+void* chroma_hip_device_base(void* handle);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CHROMA_HIP_H */

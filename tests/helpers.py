@@ -1,0 +1,97 @@
+"""Shared test helpers: wrap functions for torch.export, build small seeded transformers, compare arrays."""
+
+from __future__ import annotations
+
+import dataclasses
+from typing import Any, Callable
+
+import numpy as np
+import torch
+
+from chroma_amd._src.dtypes import BFLOAT16, bf16_to_float32
+from chroma_amd.models.gpt_oss import ModelConfig, Transformer
+from chroma_amd.models.variants import dev
+
+
+class Function(torch.nn.Module):
+    """Wraps a plain function so torch.export can trace it."""
+
+    def __init__(self, fn: Callable[..., Any]) -> None:
+        super().__init__()
+        self.fn = fn
+
+    def forward(self, *args: Any) -> Any:
+        return self.fn(*args)
+
+
+def export(module: torch.nn.Module, *inputs: torch.Tensor) -> torch.export.ExportedProgram:
+    with torch.no_grad():
+        return torch.export.export(module.eval(), inputs)
+
+
+def random_transformer(config: ModelConfig, *, seed: int, std: float, dtype: torch.dtype = torch.float32) -> Transformer:
+    """Unit norm scales and N(0, std) elsewhere, drawn in fp32 without disturbing the global RNG."""
+    with torch.random.fork_rng(devices=[]), torch.no_grad():
+        torch.manual_seed(seed)
+        model = Transformer(config, device=torch.device("cpu")).float().eval().requires_grad_(False)
+        for name, parameter in model.named_parameters():
+            if name.endswith(".scale"):
+                parameter.fill_(1)
+            else:
+                parameter.normal_(std=std)
+    return model.to(dtype)
+
+
+def small_config(**changes: Any) -> ModelConfig:
+    base = dict(
+        num_hidden_layers=1,
+        num_experts=2,
+        experts_per_token=2,
+        vocab_size=17,
+        hidden_size=8,
+        intermediate_size=8,
+        head_dim=4,
+        num_attention_heads=2,
+        num_key_value_heads=1,
+        sliding_window=3,
+    )
+    base.update(changes)
+    return dataclasses.replace(dev, **base)
+
+
+def numpy_of(value: Any) -> np.ndarray:
+    if isinstance(value, np.ndarray):
+        return value
+    tensor = value.detach().contiguous()
+    if tensor.dtype == torch.bfloat16:
+        return tensor.view(torch.uint16).numpy().view(BFLOAT16)
+    return tensor.numpy()
+
+
+def as_float(array: np.ndarray) -> np.ndarray:
+    if array.dtype == BFLOAT16:
+        return bf16_to_float32(array)
+    return np.asarray(array)
+
+
+def assert_close(actual: Any, expected: Any, *, rtol: float = 2e-5, atol: float = 2e-6) -> None:
+    """Compare one array (NumPy result) with an expected tensor/array: int64 exactly, floats within tolerance."""
+    expected = numpy_of(expected)
+    actual = np.asarray(actual) if not isinstance(actual, np.ndarray) else actual
+    assert actual.dtype == expected.dtype, (actual.dtype, expected.dtype)
+    assert actual.shape == expected.shape, (actual.shape, expected.shape)
+    if expected.dtype == np.int64:
+        np.testing.assert_array_equal(actual, expected)
+    else:
+        np.testing.assert_allclose(as_float(actual), as_float(expected), rtol=rtol, atol=atol, equal_nan=True)
+
+
+def leaves(value: Any) -> list:
+    if isinstance(value, (tuple, list)):
+        out = []
+        for item in value:
+            out.extend(leaves(item))
+        return out
+    if hasattr(value, "values") and hasattr(value, "indices") and not isinstance(value, (np.ndarray, torch.Tensor)):
+        return [value.values, value.indices]
+    return [value]
