@@ -18,6 +18,7 @@ calls (chroma/_src/codegen/cuda/codegen.py:44-168):
 
 from __future__ import annotations
 
+import hashlib
 import math
 from dataclasses import dataclass, field
 from typing import Callable, Dict, List, Optional, Sequence, Tuple, Union
@@ -36,6 +37,13 @@ MAX_DEPTH = 24
 MAX_SOURCES = 24
 MAP_THREADS = 256
 MAX_GRID = 16384
+# Row kernels: threads per row for rows of at least 2048 elements (smaller rows use one wave), the most
+# elements a thread keeps in registers for a single-pass row, and whether results that nothing in the
+# same kernel reads again are written with non-temporal (streaming) stores.
+ROW_THREADS = 256
+ROW_RESIDENT = 32
+STREAMING_STORES = True
+STREAMING_BYTES = 64 << 20  # below this a result may stay in the 4 MiB-per-XCD L2 for its consumer
 
 UNARY_OPS = {
     "reciprocal": "reciprocal",
@@ -260,11 +268,17 @@ class HIPCodegen(Codegen):
     def binding_of(self, buffer: str) -> Binding:
         return self.bindings[buffer]
 
-    def launch(self, k: Kernel, grid: Union[int, Tuple[int, int, int]], block: int, inputs: Sequence[Value], *, prologue: Sequence[str] = ()) -> None:
+    def launch(
+        self, k: Kernel, grid: Union[int, Tuple[int, int, int]], block: int, inputs: Sequence[Value], *, kind: str, prologue: Sequence[str] = ()
+    ) -> None:
+        """Record one launch of ``k``; identical kernels (same code, same parameter types) are emitted once.
+
+        Kernels are named ``chroma_<kind>_<hash of their source>`` so profiles stay readable and
+        stable across programs."""
         source = k.render("KERNEL_NAME", block, prologue)
         name = self.kernel_names.get(source)
         if name is None:
-            name = f"chroma_k{len(self.kernel_sources)}"
+            name = f"chroma_{kind}_{hashlib.sha256(source.encode()).hexdigest()[:8]}"
             self.kernel_names[source] = name
             self.kernel_sources.append(source.replace("KERNEL_NAME", name, 1))
         grid3 = (grid, 1, 1) if isinstance(grid, int) else grid
@@ -285,6 +299,7 @@ class HIPCodegen(Codegen):
         count = math.prod(shape)
         lanes = choose_lanes(shape[-1], value.dtype)
         k = Kernel(lanes)
+        k.streaming = STREAMING_STORES and count * ITEMSIZE[value.dtype] >= STREAMING_BYTES
         slot = k.slot(target or out.name, value.dtype, writable=True, extent=self.extents[target or out.name])
         vectors = count // lanes
         wide = vectors > 2**31 - 1
@@ -299,7 +314,7 @@ class HIPCodegen(Codegen):
             node = self.read(k, value, coords if value.shape else coords[:0])
             k.store(slot, value.dtype, Kernel.flatten(coords, shape), node)
         grid = max(1, min(-(-vectors // MAP_THREADS), MAX_GRID))
-        self.launch(k, grid, MAP_THREADS, [value])
+        self.launch(k, grid, MAP_THREADS, [value], kind="map")
 
     # ==================================================================================== outputs
     def output(self, index: int, value: Value) -> None:
@@ -356,7 +371,7 @@ class HIPCodegen(Codegen):
                 start = end
             k.line("}")
         grid = max(1, min(-(-vectors // MAP_THREADS), MAX_GRID))
-        self.launch(k, grid, MAP_THREADS, values)
+        self.launch(k, grid, MAP_THREADS, values, kind="concat")
         return out
 
     # ================================================================================ row kernels
@@ -387,16 +402,17 @@ class HIPCodegen(Codegen):
         return out
 
     def _row_plan(self, width: int, dtype: torch.dtype) -> Tuple[int, int, int, bool]:
-        threads = 256 if width >= 2048 else 64
+        threads = ROW_THREADS if width >= 2048 else 64
         lanes = choose_lanes(width, dtype)
         chunks = -(-width // (threads * lanes))
-        resident = chunks * lanes <= 32
+        resident = chunks * lanes <= ROW_RESIDENT
         return threads, lanes, chunks, resident
 
     def _row_softmax(self, out: Value, x: Value, shape, dim: int, width: int, rows: int) -> None:
         threads, lanes, chunks, resident = self._row_plan(width, x.dtype)
         waves = threads // 64
         k = Kernel(lanes)
+        k.streaming = STREAMING_STORES and math.prod(shape) * ITEMSIZE[out.dtype] >= STREAMING_BYTES
         slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
         row_atom = k.atom("blockIdx.x", rows - 1, prefix="r")
         row = Aff.of(row_atom)
@@ -468,7 +484,7 @@ class HIPCodegen(Codegen):
                 names = lane_names(element(j))
                 result = self._lane_values(k, [f"chroma::fast_exp({name} - row_peak) * inverse" for name in names])
                 k.store(slot, out.dtype, out_address(j), result)
-        self.launch(k, rows, threads, [x], prologue=[f"__shared__ float scratch[{max(waves, 1)}];"])
+        self.launch(k, rows, threads, [x], kind="softmax_rows", prologue=[f"__shared__ float scratch[{max(waves, 1)}];"])
 
     def _lane_values(self, k: Kernel, codes: Sequence[str]) -> tuple:
         """A varying node whose lane l is the C expression ``codes[l]`` (declared now)."""
@@ -500,7 +516,7 @@ class HIPCodegen(Codegen):
             with k.block(f"for (uint32_t j = 0; j < {width}u; ++j) {{"):
                 value = self._lane_values(k, [f"chroma::fast_exp({k.emit(element())} - peak) * inverse"])
                 k.store(slot, out.dtype, Kernel.flatten(self._row_coords(k, row, shape, dim, Aff.of(j_atom)), shape), value)
-        self.launch(k, max(1, min(-(-rows // 256), MAX_GRID)), 256, [x])
+        self.launch(k, max(1, min(-(-rows // 256), MAX_GRID)), 256, [x], kind="softmax_lines")
 
     # -------------------------------------------------------------------------------- RMSNorm
     def norm(self, meta, x: Value, weight: Value, epsilon: float) -> Value:
@@ -558,7 +574,7 @@ class HIPCodegen(Codegen):
             if ragged and resident:
                 k.indent -= 1
                 k.line("}")
-        self.launch(k, rows, threads, [x, weight], prologue=[f"__shared__ float scratch[{waves}];"])
+        self.launch(k, rows, threads, [x, weight], kind="rmsnorm", prologue=[f"__shared__ float scratch[{waves}];"])
         self.parallel_reductions += 1
         return out
 
@@ -604,7 +620,7 @@ class HIPCodegen(Codegen):
             k.store(slot, out.dtype, Aff.of(Atom("o", outputs - 1)), self._lane_values(k, [f"sum / {divisor}"]))
             k.indent -= 1
             k.line("}")
-            self.launch(k, -(-outputs // groups), 64 * groups, [x])
+            self.launch(k, -(-outputs // groups), 64 * groups, [x], kind="reduce_waves")
             self.parallel_reductions += 1
         else:
             with k.block(f"for (uint32_t o = blockIdx.x * 256u + threadIdx.x; o < {outputs}u; o += gridDim.x * 256u) {{"):
@@ -614,7 +630,7 @@ class HIPCodegen(Codegen):
                     reduce_coords = k.unflatten(Aff.of(Atom("r", width - 1)), reduce_shape)
                     k.line(f"sum += {k.emit(element(out_coords, reduce_coords))};")
                 k.store(slot, out.dtype, Aff.of(Atom("o", outputs - 1)), self._lane_values(k, [f"sum / {divisor}"]))
-            self.launch(k, max(1, min(-(-outputs // 256), MAX_GRID)), 256, [x])
+            self.launch(k, max(1, min(-(-outputs // 256), MAX_GRID)), 256, [x], kind="reduce")
         return out
 
     # ------------------------------------------------------------------------------------ top-k
@@ -664,7 +680,7 @@ class HIPCodegen(Codegen):
             k.line(f"{index_slot}[{address.code()}] = int64_t(winner);")
             k.indent -= 1
             k.line("}")
-        self.launch(k, -(-rows // groups), 64 * groups, [x])
+        self.launch(k, -(-rows // groups), 64 * groups, [x], kind="topk")
         return values, indices
 
     # =================================================================================== linear
@@ -711,7 +727,7 @@ class HIPCodegen(Codegen):
             f"chroma::skinny_linear<{rows}, {inner}, {lanes_per_row}, {ctype}>("
             f"{args[0]}, {args[1]}, {args[2]}, {out_slot}, {columns}u);"
         )
-        self.launch(k, blocks, 256, [x, weight] + ([bias] if bias is not None else []))
+        self.launch(k, blocks, 256, [x, weight] + ([bias] if bias is not None else []), kind="linear_skinny")
 
     def _tiled_linear(self, out, x, weight, bias, rows, columns, inner) -> None:
         k = Kernel(1)
@@ -719,7 +735,7 @@ class HIPCodegen(Codegen):
         out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
         ctype = ctype_of(out.dtype)
         k.line(f"chroma::tiled_linear<{ctype}>({args[0]}, {args[1]}, {args[2]}, {out_slot}, {rows}u, {columns}u, {inner}u);")
-        self.launch(k, (-(-columns // 64), -(-rows // 64), 1), 256, [x, weight] + ([bias] if bias is not None else []))
+        self.launch(k, (-(-columns // 64), -(-rows // 64), 1), 256, [x, weight] + ([bias] if bias is not None else []), kind="linear_tiled")
 
     def _scalar_linear(self, out, x, weight, bias, rows, columns, inner) -> None:
         k = Kernel(1)
@@ -737,7 +753,7 @@ class HIPCodegen(Codegen):
             if bias is not None:
                 k.line(f"sum += {k.emit(self.read(k, bias, [column]))};")
             k.store(slot, out.dtype, Aff.of(o), self._lane_values(k, ["sum"]))
-        self.launch(k, max(1, min(-(-total // 256), MAX_GRID)), 256, [x, weight] + ([bias] if bias is not None else []))
+        self.launch(k, max(1, min(-(-total // 256), MAX_GRID)), 256, [x, weight] + ([bias] if bias is not None else []), kind="linear_scalar")
 
     # ================================================================================= einsum
     def einsum(self, meta, eqn: str, values: Sequence[Value]) -> Value:
@@ -787,7 +803,7 @@ class HIPCodegen(Codegen):
             f"chroma::expert_linear<{inner}, {lanes_per_row}, {ctype_of(out.dtype)}, {per_expert}>("
             f"{w}, {idx}, {xs}, {out_slot}, {selected}u, {experts}u, {channels}u, {blocks_per_slot}u, error);"
         )
-        self.launch(k, (blocks_per_slot, tokens * selected, 1), 256, [weight, indices, x])
+        self.launch(k, (blocks_per_slot, tokens * selected, 1), 256, [weight, indices, x], kind="expert_linear")
         self.expert_contractions += 1
         return out
 
@@ -825,7 +841,7 @@ class HIPCodegen(Codegen):
             k.store(slot, out.dtype, Aff.of(Atom("o", outputs - 1)), self._lane_values(k, ["sum"]))
             k.indent -= 1
             k.line("}")
-            self.launch(k, -(-outputs // groups), 64 * groups, values)
+            self.launch(k, -(-outputs // groups), 64 * groups, values, kind="contract_waves")
             self.parallel_reductions += 1
         else:
             with k.block(f"for (uint32_t o = blockIdx.x * 256u + threadIdx.x; o < {outputs}u; o += gridDim.x * 256u) {{"):
@@ -838,7 +854,7 @@ class HIPCodegen(Codegen):
                 else:
                     k.line(f"sum += {product(out_coords, [])};")
                 k.store(slot, out.dtype, Aff.of(Atom("o", outputs - 1)), self._lane_values(k, ["sum"]))
-            self.launch(k, max(1, min(-(-outputs // 256), MAX_GRID)), 256, values)
+            self.launch(k, max(1, min(-(-outputs // 256), MAX_GRID)), 256, values, kind="contract")
         return out
 
     # ================================================================================== finish

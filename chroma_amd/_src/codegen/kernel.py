@@ -181,6 +181,7 @@ class Kernel:
         self.indent = 1
         self.definitions: Dict[str, Tuple[str, "Aff", int]] = {}  # opaque atom -> (op, operand, constant)
         self.uses_error = False
+        self.streaming = False  # vector float stores bypass the caches (results read by later kernels only)
         self.shared: List[str] = []
 
     # -- parameters ------------------------------------------------------------------------------
@@ -447,6 +448,9 @@ class Kernel:
         if vector is not None and self.lanes > 1 and not is_int(dtype) and self._vector_aligned(aff, vector):
             base = aff.code(0, wide)
             if dtype == torch.float32:
+                if self.streaming:
+                    self.line(f"chroma::store_streaming{self.lanes}({slot} + {base}, {', '.join(per_lane)});")
+                    return
                 vtype = {2: "float2", 4: "float4"}[self.lanes]
                 self.line(f"*reinterpret_cast<{vtype}*>({slot} + {base}) = {vtype}{{{', '.join(per_lane)}}};")
             else:

@@ -71,6 +71,19 @@ __device__ __forceinline__ float fast_tanh(float x) {
 __device__ __forceinline__ float fast_silu(float x) { return x * fast_sigmoid(x); }
 
 // ---------------------------------------------------------------------------------------------
+// Streaming (non-temporal) vector stores for results no later instruction of the same kernel reads.
+typedef float float2_nt __attribute__((ext_vector_type(2)));
+typedef float float4_nt __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void store_streaming4(float* p, float a, float b, float c, float d) {
+    __builtin_nontemporal_store(float4_nt{a, b, c, d}, reinterpret_cast<float4_nt*>(p));
+}
+
+__device__ __forceinline__ void store_streaming2(float* p, float a, float b) {
+    __builtin_nontemporal_store(float2_nt{a, b}, reinterpret_cast<float2_nt*>(p));
+}
+
+// ---------------------------------------------------------------------------------------------
 // Wave64 reductions (butterfly over all 64 lanes; every lane receives the result).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -51,6 +51,8 @@ def compile_library(source: Path, library: Path, flags: Sequence[str], include_r
 class OracleProgram:
     """Runs one compiled oracle program on NumPy arrays (inputs and outputs follow the manifest specs)."""
 
+    device = "CPU"
+
     def __init__(self, library: Path, weights: Path, inputs: List[dict], outputs: List[dict], stats: dict) -> None:
         self.inputs, self.outputs, self.stats = inputs, outputs, stats
         self._lib = ctypes.CDLL(str(library))

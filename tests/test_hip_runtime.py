@@ -1,0 +1,503 @@
+"""GPU parity of the hip backend against the CPU oracle (and eager torch where the reference checks it).
+
+Mirrors the reference's hardware suite (tests/test_cuda.py:279-519) with the oracle as the expected
+value. Tolerances are the north star's: int64 indices and argmax bit-exact; float32 rel 1e-4 / abs 1e-5;
+bfloat16 rel 2e-2 (abs 1e-2 for values near zero). Every case runs two input sets, checks ``out=``
+returns the given arrays, that a later call leaves earlier results untouched, and reloads the artifact.
+"""
+
+from __future__ import annotations
+
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import chroma_amd
+from chroma_amd import Decoder, Program
+from chroma_amd._src.dtypes import BFLOAT16
+from oracle import compile_cpu
+from tests.helpers import Function, as_float, assert_close, export, leaves, numpy_of, random_transformer, small_config
+
+pytestmark = pytest.mark.gpu
+
+F32 = dict(rtol=1e-4, atol=1e-5)
+BF16 = dict(rtol=2e-2, atol=1e-2)
+
+
+def tolerance(array):
+    return BF16 if array.dtype == BFLOAT16 else F32
+
+
+def compare(actual, expected):
+    for got, want in zip(leaves(actual), leaves(expected)):
+        want = numpy_of(want)
+        assert_close(got, want, **tolerance(want))
+
+
+def check(tmp_path, module, *inputs, blas=True, eager=True, second=True):
+    exported = torch.export.export(module, inputs)
+    oracle = compile_cpu(exported, tmp_path / "oracle", blas=blas)
+    sets = [inputs] + ([tuple(x + 1 if x.dtype != torch.int64 else x for x in inputs)] if second else [])
+    with chroma_amd.compile(exported, tmp_path / "hip", blas=blas) as model:
+        assert model.stats["backend"] == "hip"
+        for values in sets:
+            actual = model(*values)
+            compare(actual, oracle(*[numpy_of(v) for v in values]))
+            if eager:
+                with torch.no_grad():
+                    compare(actual, leaves(module(*values)))
+            reused = model(*values, out=actual)
+            for got, original in zip(leaves(reused), leaves(actual)):
+                assert got is original
+        saved = [np.array(a, copy=True) for a in leaves(actual)]
+        model(*sets[-1])
+        for got, want in zip(leaves(actual), saved):
+            np.testing.assert_array_equal(got.view(np.uint8), want.view(np.uint8))
+    with Program(tmp_path / "hip") as loaded:
+        compare(loaded(*inputs), oracle(*[numpy_of(v) for v in inputs]))
+    return oracle
+
+
+class BandwidthGraph(torch.nn.Module):
+    def forward(self, x, y):
+        z = torch.tanh(x * 0.5 + y) * torch.sigmoid(y) - torch.exp(torch.clamp(x, -8, 8)) * 1e-3
+        return torch.softmax(z, -1)
+
+
+def uniform(seed, *shape):
+    generator = torch.Generator().manual_seed(seed)
+    return torch.rand(*shape, generator=generator) * 8 - 4
+
+
+# ----------------------------------------------------------------------------------- C2 bandwidth graph
+@pytest.mark.parametrize("shape", [(64, 8192), (33, 1000), (5, 40000), (7, 64), (3, 63), (4, 2050)])
+def test_bandwidth_graph_matches_oracle(tmp_path, shape):
+    check(tmp_path, BandwidthGraph(), uniform(1, *shape), uniform(2, *shape), eager=True)
+
+
+def test_bandwidth_graph_softmax_over_a_leading_axis(tmp_path):
+    class Leading(torch.nn.Module):
+        def forward(self, x, y):
+            return torch.softmax(torch.tanh(x * 0.5 + y) * torch.sigmoid(y), 0)
+
+    check(tmp_path, Leading(), uniform(3, 70, 3, 5), uniform(4, 70, 3, 5))
+
+
+def test_bandwidth_graph_full_size(tmp_path):
+    """BASELINE C2 at its real size: every row is a distribution, and sampled rows match the oracle."""
+    x, y = uniform(1, 16384, 8192), uniform(2, 16384, 8192)
+    exported = torch.export.export(BandwidthGraph(), (x, y))
+    with chroma_amd.compile(exported, tmp_path / "hip") as model:
+        out = model(x, y)
+    assert out.shape == (16384, 8192) and np.isfinite(out).all() and (out > 0).all()
+    np.testing.assert_allclose(out.sum(axis=1, dtype=np.float64), 1.0, rtol=2e-5)
+    rows = torch.tensor([0, 1, 4095, 8191, 12288, 16383])
+    sample = compile_cpu(torch.export.export(BandwidthGraph(), (x[rows], y[rows])), tmp_path / "oracle")
+    np.testing.assert_allclose(out[rows.numpy()], sample(x[rows].numpy(), y[rows].numpy()), **F32)
+
+
+# ---------------------------------------------------------------------------------------- C1 MLP block
+def test_mlp_block(tmp_path):
+    from oracle.ref import mlp_module
+
+    x = torch.randn(8, 1024, generator=torch.Generator().manual_seed(0))
+    check(tmp_path, mlp_module(1024, 4096, seed=0), x)
+
+
+# ------------------------------------------------------------------------------ operator coverage
+def test_fused_views_and_wide_int64(tmp_path):
+    def fn(x, y, ids):
+        z = (x.sin() + y).clamp(-1, 1)
+        return z, z, z.t().reshape(3, 514)[:, 1::2], x, ids.t(), ids[1:, 1:]
+
+    ids = torch.tensor([[2**60 + 7, -(2**60) - 3, 2**40], [-11, 2**62 - 1, 0]], dtype=torch.int64)
+    check(tmp_path, Function(fn), torch.linspace(-3, 3, 1542).reshape(514, 3), torch.ones(3), ids)
+
+
+@pytest.mark.parametrize("blas", [True, False])
+def test_linear_kernels(tmp_path, blas):
+    torch.manual_seed(42)
+
+    def fn(x, w, b):
+        y = torch.nn.functional.linear(x[:, ::2], w.t(), b)
+        return y.sigmoid(), y, torch.nn.functional.linear(x[:, ::2] + 1, w.t())
+
+    check(tmp_path / "a", Function(fn), torch.randn(35, 34), torch.randn(17, 8), torch.randn(8), blas=blas)
+    check(tmp_path / "b", torch.nn.Linear(16, 7).eval(), torch.randn(16), blas=blas)
+    check(tmp_path / "c", torch.nn.Linear(64, 300, bias=False).eval(), torch.randn(2, 3, 64), blas=blas)
+    check(tmp_path / "d", torch.nn.Linear(128, 96).eval(), torch.randn(100, 128), blas=blas)
+
+
+def test_aliases_and_live_workspace_across_linear_layers(tmp_path):
+    def fn(x, w):
+        first = torch.nn.functional.linear(x, w)
+        shared = first.sin()
+        second = torch.nn.functional.linear(shared + 1, w)
+        third = torch.nn.functional.linear(second + shared, w)
+        return third, first[:, 1:], shared
+
+    check(tmp_path, Function(fn), torch.randn(3, 16), torch.eye(16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_reductions_softmax_gather_cat_triangular_norm_and_einsum(tmp_path, dtype):
+    from chroma_amd.models.gpt_oss import RMSNorm
+
+    def fn(x, y, ids):
+        selected = x[ids]
+        values, indices = selected.topk(2, dim=0, largest=False)
+        return (
+            selected.sum(0),
+            selected.mean(1, keepdim=True),
+            selected.softmax(0),
+            values,
+            indices,
+            torch.cat((selected, y), dim=0),
+            torch.triu(selected, 1),
+            torch.tril(selected, -1),
+            torch.einsum("ij,kj->ik", selected, y),
+        )
+
+    torch.manual_seed(9)
+    ids = torch.tensor([4, -1, 0], dtype=torch.int64)
+    check(tmp_path / "ops", Function(fn), torch.arange(-12, 12, dtype=torch.float32).reshape(6, 4).to(dtype), torch.randn(2, 4).to(dtype), ids)
+    check(tmp_path / "norm", RMSNorm(17).to(dtype).eval(), torch.randn(5, 17).to(dtype))
+
+
+def test_int64_gather_cat_masks_bounds_and_recovery(tmp_path):
+    def fn(x, ids):
+        selected = x[ids]
+        return selected, torch.cat((selected, x[:1]), dim=0), torch.triu(x, 1), torch.tril(x, -1)
+
+    x = torch.arange(12, dtype=torch.int64).reshape(4, 3)
+    ids = torch.tensor([3, -1, 0], dtype=torch.int64)
+    with chroma_amd.compile(torch.export.export(Function(fn), (x, ids)), tmp_path) as model:
+        expected = fn(x, ids)
+        compare(model(x, ids), expected)
+        for bad in (-5, 4, 2**40):
+            with pytest.raises(IndexError):
+                model(x, torch.tensor([bad, 0, 0], dtype=torch.int64))
+            compare(model(x, ids), expected)
+
+
+def test_strided_axes_nonfinite_values_and_topk_ties(tmp_path):
+    def strided(x):
+        y = x.t()[1::2]
+        values, indices = y.topk(3, dim=1, largest=False)
+        return y, y.sum(0), y.mean(1), y.softmax(0), values, indices, torch.tril(y, 1)
+
+    x = torch.randn(17, 8, generator=torch.Generator().manual_seed(3))
+    x[2, 1] = float("nan")
+    x[5, 3] = float("inf")
+    x[9, 5] = -float("inf")
+    check(tmp_path / "strided", Function(strided), x, second=False)
+
+    tied = torch.tensor([[2.0, 1.0, 0.0], [2.0, 1.0, 0.0], [1.0, 2.0, 0.0], [1.0, 2.0, 3.0], [0.0, 3.0, 3.0], [0.0, 3.0, 3.0]])
+    for largest in (True, False):
+        module = Function(lambda x, largest=largest: torch.topk(x, 4, dim=0, largest=largest, sorted=False))
+        with chroma_amd.compile(torch.export.export(module, (tied,)), tmp_path / str(largest)) as model:
+            values, indices = model(tied)
+            expected = module(tied).values.numpy()
+            np.testing.assert_allclose(np.sort(values, axis=0), np.sort(expected, axis=0))
+            np.testing.assert_array_equal(values, np.take_along_axis(tied.numpy(), indices, axis=0))
+            assert all(len(set(column)) == 4 for column in indices.T)
+            # Ties go to the lowest index, and the selection comes back sorted.
+            order = np.argsort(-tied.numpy() if largest else tied.numpy(), axis=0, kind="stable")[:4]
+            np.testing.assert_array_equal(indices, order)
+
+
+@pytest.mark.parametrize("width", [12, 256, 4096])
+def test_topk_matches_oracle_exactly_without_ties(tmp_path, width):
+    x = torch.randn(9, width, generator=torch.Generator().manual_seed(width))
+    module = Function(lambda x: torch.topk(x, 4, dim=-1))
+    exported = torch.export.export(module, (x,))
+    with chroma_amd.compile(exported, tmp_path / "hip") as model:
+        values, indices = model(x)
+    expected_values, expected_indices = compile_cpu(exported, tmp_path / "cpu")(x.numpy())
+    np.testing.assert_array_equal(indices, expected_indices)
+    np.testing.assert_array_equal(values, expected_values)
+
+
+def test_wave_reductions_norm_and_general_contractions(tmp_path):
+    from chroma_amd.models.gpt_oss import RMSNorm
+
+    def reductions(x):
+        return x.sum(1), x.mean((0, 2), keepdim=True), x.softmax(1)
+
+    def contractions(a, b, c, d, e, f, g, h):
+        return (torch.einsum("ij,j->i", a, b), torch.einsum("bik,bkj->bij", c, d), torch.einsum("km,kn->mn", e, f), torch.einsum("ij,ik->ijk", g, h))
+
+    for dtype in (torch.float32, torch.bfloat16):
+        x = torch.linspace(-3, 3, 3 * 65 * 17).reshape(3, 65, 17).to(dtype)
+        check(tmp_path / f"r{dtype}", Function(reductions), x)
+        check(tmp_path / f"n{dtype}", RMSNorm(65).to(dtype).eval(), torch.randn(4, 65).to(dtype))
+    inputs = (
+        torch.linspace(-1, 1, 4 * 1025).reshape(4, 1025),
+        torch.linspace(0.5, 1.5, 1025),
+        torch.linspace(-1, 1, 2 * 3 * 17).reshape(2, 3, 17),
+        torch.linspace(1, -1, 17 * 5).reshape(1, 17, 5),
+        torch.linspace(-0.5, 0.5, 17 * 3).reshape(17, 3),
+        torch.linspace(0.75, -0.75, 17 * 5).reshape(17, 5),
+        torch.linspace(-1, 1, 2 * 3).reshape(2, 3),
+        torch.linspace(1, -1, 2 * 4).reshape(2, 4),
+    )
+    check(tmp_path / "c", Function(contractions), *inputs)
+
+
+def test_wide_vocabulary_softmax_and_norm(tmp_path):
+    """Rows wider than a workgroup's registers take the two-pass streaming path."""
+    from chroma_amd.models.gpt_oss import RMSNorm
+
+    x = torch.randn(3, 201088, generator=torch.Generator().manual_seed(5)) * 3
+    check(tmp_path / "softmax", Function(lambda x: x.softmax(-1)), x, second=False)
+    check(tmp_path / "norm", RMSNorm(201088).eval(), x, second=False)
+
+
+def test_bfloat16_storage_rounding_and_float_accumulation(tmp_path):
+    def rounding(x, y, one):
+        rounded = y.bfloat16()
+        return x.sin() + x, rounded, rounded.float(), (one + 2**-8) + 2**-8, (one * 0.333984375) - 0.333
+
+    x = torch.linspace(-1, 1, 16).bfloat16()
+    y = torch.tensor([1 + 2**-8, 1 + 3 * 2**-8, -1 - 2**-8, -1 - 3 * 2**-8, float("inf"), float("nan")])
+    one = torch.ones(1, dtype=torch.bfloat16)
+    module = Function(rounding)
+    with chroma_amd.compile(torch.export.export(module, (x, y, one)), tmp_path / "round") as model:
+        actual = model(x, y, one)
+        expected = module(x, y, one)
+        for got, want in zip(actual[1:], expected[1:]):
+            assert_close(got, want, rtol=0, atol=0)
+        assert_close(actual[0], expected[0], **BF16)
+        assert [value.itemsize for value in actual] == [2, 2, 4, 2, 2]
+        np.testing.assert_array_equal(as_float(actual[3]), np.ones(1, dtype=np.float32))
+
+    def linear(x, weight, bias):
+        return torch.nn.functional.linear(x, weight, bias), torch.einsum("mk,nk->mn", x, weight), weight.sum(dim=1)
+
+    # Exact known answers: float accumulation with one rounding at the end (reference test_bf16.py:193-216),
+    # through the scalar kernels (K = 17) and the vectorised matrix kernels (K = 32).
+    for inner, head, answers in ((17, [1.0], (1.09375, 1.0625, 1.0625)), (32, [0.5, 0.5], (1.1484375, 1.1171875, 1.1171875))):
+        weight = torch.full((5, inner), 2**-8, dtype=torch.bfloat16)
+        weight[:, : len(head)] = torch.tensor(head, dtype=torch.bfloat16)
+        values = (torch.ones(2, inner, dtype=torch.bfloat16), weight, torch.full((5,), 2**-5, dtype=torch.bfloat16))
+        for blas in (True, False):
+            with chroma_amd.compile(torch.export.export(Function(linear), values), tmp_path / f"linear{inner}{blas}", blas=blas) as model:
+                got = model(*values)
+                np.testing.assert_array_equal(as_float(got[0]), np.full((2, 5), answers[0], dtype=np.float32))
+                np.testing.assert_array_equal(as_float(got[1]), np.full((2, 5), answers[1], dtype=np.float32))
+                np.testing.assert_array_equal(as_float(got[2]), np.full(5, answers[2], dtype=np.float32))
+
+
+def test_nonfinite_math_scalars_and_long_chains(tmp_path):
+    def fn(x):
+        z = x.clamp(-1, 1)
+        for _ in range(80):
+            z = z.clamp(-1, 1)
+        return z, torch.add(x, x, alpha=0.25), torch.rsub(x, 3, alpha=0.5), 2.0**x, x.clamp(max=float("nan"))
+
+    check(tmp_path / "a", Function(fn), torch.tensor([-float("inf"), -2, 0.5, float("inf"), float("nan")]))
+    check(tmp_path / "b", Function(lambda x: x.sin() + 1), torch.tensor(0.5))
+    check(tmp_path / "c", Function(lambda x: (torch.arange(4), x)), torch.ones(1))
+
+
+# --------------------------------------------------------------------------------- transformer + decoder
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_small_transformer_and_decoder(tmp_path, dtype):
+    from chroma_amd.models.cached import export_cached
+
+    eager = random_transformer(small_config(), seed=5, std=0.1, dtype=dtype)
+    tokens = (torch.arange(14) * 7 + 3) % 17
+    with torch.no_grad():
+        expected = eager(tokens)
+    tol = F32 if dtype == torch.float32 else dict(rtol=0.03, atol=0.01)
+    context = 5
+    full = chroma_amd.compile(torch.export.export(eager, (tokens[:4],)), tmp_path / "full")
+    prefill = chroma_amd.compile(export_cached(eager, context, context), tmp_path / "prefill")
+    step = chroma_amd.compile(export_cached(eager, context, 1), tmp_path / "step")
+    with full, Decoder(prefill, step, sliding_window=3) as decoder:
+        assert full.device
+        assert_close(full(tokens[:4]), expected[:4], **tol)
+        for bad in (-1, 17, 2**40):
+            with pytest.raises(IndexError):
+                full(torch.full((4,), bad, dtype=torch.int64))
+            assert_close(full(tokens[:4]), expected[:4], **tol)
+        position = 0
+        for size in (2, 1, 4, 5, 2):
+            logits = decoder.append(tokens[position : position + size].numpy())
+            position += size
+            assert_close(logits, expected[position - 1 : position], **tol)
+        preserved = logits.copy()
+        decoder.reset()
+        assert decoder.position == 0
+        assert_close(decoder.append(tokens.numpy()), expected[-1:], **tol)
+        np.testing.assert_array_equal(logits.view(np.uint8), preserved.view(np.uint8))
+
+
+def test_yarn_sliding_window_lengths(tmp_path):
+    import dataclasses
+
+    from chroma_amd.models.variants import dev
+
+    for length in (1, 17):
+        config = dataclasses.replace(dev, num_hidden_layers=2, hidden_size=16, head_dim=64, num_attention_heads=4, num_key_value_heads=2,
+                                     vocab_size=257, sliding_window=3, initial_context_length=4096, rope_scaling_factor=32.0)
+        model = random_transformer(config, seed=length, std=0.04)
+        tokens = torch.arange(length, dtype=torch.int64)
+        check(tmp_path / str(length), model, tokens)
+
+
+# ------------------------------------------------------------------------------ C3 / C4 dev model
+@pytest.fixture(scope="module")
+def dev_model():
+    from chroma_amd.models.dev import make_dev_model
+
+    return make_dev_model(0)
+
+
+def test_dev_model_forward(tmp_path, dev_model):
+    tokens = torch.arange(8, dtype=torch.int64)
+    exported = export(dev_model, tokens)
+    oracle = compile_cpu(exported, tmp_path / "cpu")
+    with chroma_amd.compile(exported, tmp_path / "hip") as model:
+        sets = [tokens, (tokens * 7919 + 17) % 201088, torch.zeros_like(tokens), torch.randint(0, 201088, (8,), generator=torch.Generator().manual_seed(0))]
+        for values in sets:
+            got, want = model(values), oracle(values.numpy())
+            np.testing.assert_allclose(got, want, **F32)
+            top = np.sort(want, axis=-1)[:, -2:]
+            decisive = top[:, 1] - top[:, 0] > 1e-4
+            np.testing.assert_array_equal(got.argmax(-1)[decisive], want.argmax(-1)[decisive])
+            with torch.no_grad():
+                np.testing.assert_allclose(got, dev_model(values).numpy(), rtol=2e-4, atol=2e-5)
+        first = model(tokens)
+        preserved = first.copy()
+        model(tokens + 1)
+        np.testing.assert_array_equal(first, preserved)
+        assert model.stats["expert_contractions"] == 24
+        assert model.stats["workspace_bytes"] <= 74 * 1024
+
+
+def test_graph_replay_matches_direct_launches(tmp_path, dev_model):
+    tokens = torch.arange(8, dtype=torch.int64)
+    with chroma_amd.compile(export(dev_model, tokens), tmp_path) as model:
+        model.native.set_graph(False)
+        direct = model(tokens)
+        other = model((tokens * 31 + 5) % 201088)
+        model.native.set_graph(True)
+        for _ in range(4):
+            np.testing.assert_array_equal(model(tokens), direct)
+            _ = torch.randn(64, 64) @ torch.randn(64, 64)  # eager host work between replays
+            np.testing.assert_array_equal(model((tokens * 31 + 5) % 201088), other)
+
+
+def test_dev_decoder_with_wraparound(tmp_path, dev_model):
+    """C4: the KV-cached decoder against the oracle's decoder, past the end of a 32-position cache."""
+    from chroma_amd.models.cached import export_cached
+
+    context = 32
+    graphs = [export_cached(dev_model, context, context), export_cached(dev_model, context, 1)]
+    hip = [chroma_amd.compile(g, tmp_path / f"hip{i}") for i, g in enumerate(graphs)]
+    cpu = [compile_cpu(g, tmp_path / f"cpu{i}") for i, g in enumerate(graphs)]
+    tokens = ((np.arange(48) * 7919 + 17) % 201088).astype(np.int64)
+    with Decoder(*hip) as decoder, Decoder(*cpu) as reference:
+        for start, end in ((0, 8), *((i, i + 1) for i in range(8, 40)), (40, 48)):
+            got, want = decoder.append(tokens[start:end]), reference.append(tokens[start:end])
+            np.testing.assert_allclose(got, want, **F32)
+        assert decoder.position == 48
+
+
+def test_device_resident_execution(tmp_path):
+    x, y = uniform(1, 64, 8192), uniform(2, 64, 8192)
+    exported = torch.export.export(BandwidthGraph(), (x, y))
+    with chroma_amd.compile(exported, tmp_path) as model:
+        expected = model(x, y)
+        native = model.native
+        native.upload([x.numpy(), y.numpy()])
+        milliseconds = native.execute(3, timed=True)
+        assert milliseconds > 0
+        out = np.empty_like(expected)
+        native.download([out])
+        np.testing.assert_array_equal(out, expected)
+
+
+# ------------------------------------------------------------------------------------ bindings
+def test_array_validation_rebuild_and_runtime_only_reload(tmp_path):
+    x = torch.arange(4, dtype=torch.float32)
+    layer = torch.nn.Linear(4, 4).eval().requires_grad_(False)
+    with chroma_amd.compile(torch.export.export(layer, (x,)), tmp_path, blas=False) as first:
+        expected = layer(x).numpy()
+        np.testing.assert_allclose(first(x), expected, **F32)
+        out = np.empty(4, dtype=np.float32)
+        unaligned = np.ndarray((4,), dtype=np.float32, buffer=bytearray(17), offset=1)
+        readonly = out.copy()
+        readonly.setflags(write=False)
+        model = first.native
+        for inputs, outputs in (
+            ([], [out]),
+            ([x.numpy()], []),
+            ([x.numpy().astype(np.float64)], [out]),
+            ([x.numpy().astype(">f4")], [out]),
+            ([unaligned], [out]),
+            ([x.numpy()[:2]], [out]),
+            ([x.numpy()], [readonly]),
+            ([x.numpy()], [unaligned]),
+            ([x.numpy()], [x.numpy()]),
+        ):
+            with pytest.raises(ValueError):
+                model.run(inputs, outputs)
+        with pytest.raises(TypeError):
+            model.run([[0, 1, 2, 3]], [out])
+        replacement = torch.nn.Linear(4, 2).eval().requires_grad_(False)
+        with chroma_amd.compile(torch.export.export(replacement, (x,)), tmp_path, blas=False) as second:
+            np.testing.assert_allclose(second(x), replacement(x).numpy(), **F32)
+            np.testing.assert_allclose(first(x), expected, **F32)
+            with Program(tmp_path) as loaded:
+                np.testing.assert_array_equal(loaded(x), second(x))
+            assert len(list(tmp_path.glob("_chroma_*"))) == 1
+            assert len(list(tmp_path.glob("weights-*.bin"))) == 1
+            np.save(tmp_path / "expected.npy", second(x))
+    code = """
+import importlib.abc, sys
+import numpy as np
+class RuntimeOnly(importlib.abc.MetaPathFinder):
+    def find_spec(self, fullname, path=None, target=None):
+        if fullname.split('.')[0] in {'torch', 'pybind11'}:
+            raise ModuleNotFoundError(fullname)
+sys.meta_path.insert(0, RuntimeOnly())
+from chroma_amd import Program
+with Program(sys.argv[1]) as model:
+    np.testing.assert_array_equal(model(np.arange(4, dtype=np.float32)), np.load(sys.argv[1] + '/expected.npy'))
+assert 'torch' not in sys.modules
+"""
+    root = Path(__file__).resolve().parents[1]
+    subprocess.run([sys.executable, "-c", code, str(tmp_path)], check=True, cwd=root)
+    import json
+
+    manifest = json.loads((tmp_path / "model.json").read_text())
+    for incompatible in ({"version": 1}, {"python_abi": "different"}):
+        (tmp_path / "model.json").write_text(json.dumps({**manifest, **incompatible}))
+        with pytest.raises(ValueError, match="recompile"):
+            Program(tmp_path)
+    bad = dict(manifest)
+    bad["inputs"] = [dict(manifest["inputs"][0], shape=[1])]
+    (tmp_path / "model.json").write_text(json.dumps(bad))
+    with pytest.raises(ValueError, match="metadata"):
+        Program(tmp_path)
+    (tmp_path / "model.json").write_text(json.dumps(manifest))
+    (tmp_path / manifest["weights"]).write_bytes(b"bad")
+    with pytest.raises(RuntimeError, match="byte size"):
+        Program(tmp_path)
+
+
+def test_jit(tmp_path):
+    @chroma_amd.jit
+    def fn(x):
+        return x.sin() + x
+
+    x = torch.arange(8, dtype=torch.float32)
+    np.testing.assert_allclose(fn(x), (x.sin() + x).numpy(), **F32)
+    out = fn(x)
+    assert fn(x * 2, out=out) is out
