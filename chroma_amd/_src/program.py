@@ -78,7 +78,7 @@ class NativeModel:
 
     # Device-resident helpers (benchmarks and tests): upload once, execute many times, download.
     def upload(self, inputs: Sequence[np.ndarray]) -> None:
-        arrays = [_checked(np.ascontiguousarray(a), s, False) for a, s in zip(inputs, self._inputs)]
+        arrays = [_checked(np.require(a, requirements=["C", "A"]), s, False) for a, s in zip(inputs, self._inputs)]
         error = ctypes.create_string_buffer(1024)
         native.check(self._lib.chroma_hip_upload(self._handle, native.pointer_array(a.ctypes.data for a in arrays), error, len(error)), error)
 

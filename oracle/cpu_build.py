@@ -75,7 +75,7 @@ class OracleProgram:
         for value, spec in zip(inputs, self.inputs):
             if not isinstance(value, np.ndarray):
                 value = _numpy(value)
-            array = np.ascontiguousarray(value)
+            array = np.require(value, requirements=["C", "A"])
             if array.dtype != numpy_dtype(spec["dtype"]) or list(array.shape) != spec["shape"]:
                 raise ValueError("shape or dtype")
             arrays.append(array)

@@ -1,0 +1,194 @@
+"""The hip backend without a GPU: generated source, launch plans, statistics, the C ABI library.
+
+The counterpart of the reference's GPU-less codegen tests (tests/test_cuda.py:107-276): lowering
+decisions are asserted on the generated text and statistics, every operator family is cross-compiled
+for gfx950 with hipcc, and the runtime library is checked to export every entry point of
+include/chroma_hip.h.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import json
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from chroma_amd._src import native
+from chroma_amd._src.build import build
+from chroma_amd._src.codegen.hip import HIPCodegen
+from chroma_amd._src.compiler import Compiler, compile_for_backend, lower_program
+from chroma_amd.models.gpt_oss import RMSNorm
+from tests.helpers import Function, export, random_transformer, small_config
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def lower(module, *inputs, blas=True):
+    return lower_program(export(module, *inputs), HIPCodegen(blas=blas))
+
+
+class Bandwidth(torch.nn.Module):
+    def forward(self, x, y):
+        z = torch.tanh(x * 0.5 + y) * torch.sigmoid(y) - torch.exp(torch.clamp(x, -8, 8)) * 1e-3
+        return torch.softmax(z, -1)
+
+
+def test_bandwidth_graph_is_one_single_pass_kernel():
+    generated = lower(Bandwidth(), torch.rand(64, 8192), torch.rand(64, 8192))
+    source = generated.files["model.hip"]
+    assert generated.stats["kernels"] == 1 and generated.stats["workspace_bytes"] == 0
+    assert generated.stats["backend"] == "hip"
+    # x and y are each read once with 128-bit loads; the softmax output is written in place (promoted).
+    assert source.count("reinterpret_cast<const float4*>") == 2
+    assert "chroma::fast_tanh" in source and "chroma::block_max<4>" in source and "chroma::block_sum<4>" in source
+    plan = generated.files["model.plan"].splitlines()
+    launches = [line for line in plan if line.startswith("launch ")]
+    assert len(launches) == 1 and launches[0].split()[2:5] == ["64", "1", "1"]
+
+
+def test_dev_model_reuses_kernels_across_layers():
+    from chroma_amd.models.dev import make_dev_model
+
+    generated = lower(make_dev_model(0), torch.arange(8, dtype=torch.int64))
+    stats = generated.stats
+    assert stats["expert_contractions"] == 24
+    assert stats["workspace_bytes"] == 75776
+    assert stats["unique_kernels"] <= 32 < stats["launches"]
+    assert stats["launches"] == stats["kernels"]
+
+
+def test_linear_kernel_selection():
+    module = torch.nn.Linear(16, 7).eval()
+    for blas, rows, kind in ((True, 3, "linear_skinny"), (True, 40, "linear_tiled"), (False, 3, "linear_scalar")):
+        generated = lower(module, torch.ones(rows, 16), blas=blas)
+        assert kind in generated.files["model.hip"], kind
+        assert generated.stats["workspace_bytes"] == 0  # the result is written straight into the output
+    # bfloat16 keeps float accumulation in both paths
+    generated = lower(torch.nn.Linear(17, 7).bfloat16().eval(), torch.ones(3, 5, 17, dtype=torch.bfloat16))
+    assert generated.inputs[0]["dtype"] == "bfloat16" and generated.outputs[0]["dtype"] == "bfloat16"
+    assert "float sum = 0.0f" in generated.files["model.hip"]
+
+
+def test_shared_expressions_and_workspace_reuse():
+    def fn(x, w):
+        first = torch.nn.functional.linear(x, w)
+        shared = first.sin()
+        second = torch.nn.functional.linear(shared + 1, w)
+        third = torch.nn.functional.linear(second + shared, w)
+        return third, first[:, 1:], shared
+
+    compiler = Compiler.from_export(export(Function(fn), torch.ones(3, 16), torch.eye(16)), HIPCodegen())
+    generated = compiler.lower()
+    assert generated.stats["workspace_bytes"] > 0
+    allocations = list(compiler.codegen.allocations.values())
+    for i, a in enumerate(allocations):
+        for b in allocations[i + 1 :]:
+            if a.start <= b.end and b.start <= a.end:
+                assert a.offset + a.size <= b.offset or b.offset + b.size <= a.offset
+    assert generated.stats["workspace_bytes"] < generated.stats["unreused_workspace_bytes"]
+
+
+def test_long_expressions_stay_bounded():
+    def fn(x):
+        for _ in range(80):
+            x = x.clamp(-1, 1)
+        return x
+
+    generated = lower(Function(fn), torch.ones(257))
+    assert generated.stats["kernels"] == 4
+    assert len(generated.files["model.hip"]) < 60_000
+
+
+def test_plan_regions_are_aligned_disjoint_and_every_argument_is_inside_the_allocation():
+    generated = lower(random_transformer(small_config(), seed=5, std=0.1), torch.tensor([1, 4, 2, 7]))
+    lines = generated.files["model.plan"].splitlines()
+    arena = int(next(l for l in lines if l.startswith("arena")).split()[1])
+    regions = []
+    for line in lines:
+        if line.startswith(("input", "output")):
+            _, _, offset, size = line.split()
+            assert int(offset) % 256 == 0
+            regions.append((int(offset), int(offset) + int(size)))
+    regions.sort()
+    for (a0, a1), (b0, b1) in zip(regions, regions[1:]):
+        assert a1 <= b0
+    for line in lines:
+        if line.startswith("launch"):
+            fields = line.split()
+            count = int(fields[7])
+            offsets = list(map(int, fields[8 : 8 + count]))
+            assert len(offsets) == count and all(0 <= o < arena for o in offsets)
+
+
+OPERATIONS_SOURCE = """
+def fn(x, y, ids):
+    selected = x[ids]
+    values, indices = selected.topk(2, dim=0, largest=False, sorted=False)
+    return (selected.sum(0), selected.mean(1, keepdim=True), selected.softmax(0), values, indices,
+            torch.cat((selected, y), dim=0), torch.triu(selected, 1), torch.tril(selected, -1),
+            torch.einsum("ij,kj->ik", selected, y))
+"""
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_every_operation_family_cross_compiles_for_gfx950(tmp_path, dtype):
+    namespace = {"torch": torch}
+    exec(OPERATIONS_SOURCE, namespace)
+    generated = lower(Function(namespace["fn"]), torch.randn(6, 4, dtype=dtype), torch.randn(2, 4, dtype=dtype), torch.tensor([4, -1, 0]))
+    assert generated.outputs[3]["dtype"] == str(dtype).removeprefix("torch.")
+    assert generated.outputs[4]["dtype"] == "int64"
+    build(generated, tmp_path / "ops", load=False)
+    norm = lower(RMSNorm(65).to(dtype).eval(), torch.randn(4, 65, dtype=dtype))
+    build(norm, tmp_path / "norm", load=False)
+    model = random_transformer(small_config(), seed=5, std=0.1, dtype=dtype)
+    build(lower(model, torch.tensor([1, 4, 2, 7])), tmp_path / "model", load=False)
+    from chroma_amd.models.cached import export_cached
+
+    for steps in (1, 5):
+        cached = lower_program(export_cached(model, 5, steps), HIPCodegen())
+        assert [o["dtype"] for o in cached.outputs] == [str(dtype).removeprefix("torch.")] * 3
+        build(cached, tmp_path / f"cached{steps}", load=False)
+
+
+def test_build_publishes_and_replaces_artifacts(tmp_path):
+    x = torch.arange(4, dtype=torch.float32)
+    build(lower(torch.nn.Linear(4, 4).eval(), x), tmp_path, load=False)
+    build(lower(torch.nn.Linear(4, 2).eval(), x), tmp_path, load=False)
+    assert len(list(tmp_path.glob("_chroma_*.hsaco"))) == 1
+    assert len(list(tmp_path.glob("weights-*.bin"))) == 1
+    manifest = json.loads((tmp_path / "model.json").read_text())
+    assert manifest["version"] == 2 and manifest["stats"]["backend"] == "hip"
+    plan = (tmp_path / "model.plan").read_text().splitlines()
+    assert plan[0] == "chroma-hip-plan 1" and any(line.startswith("signature ") for line in plan)
+    assert (tmp_path / manifest["library"]).stat().st_size > 0
+
+
+def test_backend_dispatch_and_unsupported_dtypes():
+    exported = torch.export.export(torch.nn.Identity(), (torch.ones(4),))
+    with pytest.raises(ValueError, match="Unknown runtime backend"):
+        compile_for_backend(exported, "unused", backend="cuda")
+    with pytest.raises(ValueError, match="Unsupported dtype torch.float16"):
+        lower(torch.nn.Identity(), torch.ones(4, dtype=torch.float16))
+
+
+def test_c_abi_library_exports_every_declared_entry_point():
+    header = (ROOT / "include" / "chroma_hip.h").read_text()
+    declared = sorted(set(re.findall(r"\b(chroma_hip_\w+)\s*\(", header)))
+    assert declared == sorted(native.EXPORTED)
+    if not native.LIBRARY.exists():
+        native.build_runtime()
+    library = ctypes.CDLL(str(native.LIBRARY))
+    for name in declared:
+        assert hasattr(library, name), name
+
+
+def test_program_load_fails_loudly_without_a_built_library(tmp_path, monkeypatch):
+    from chroma_amd._src import native as module
+
+    monkeypatch.setattr(module, "LIBRARY", tmp_path / "missing.so")
+    monkeypatch.setattr(module, "_library", None)
+    with pytest.raises(RuntimeError, match="not built"):
+        module.library()

@@ -249,12 +249,25 @@ def test_wave_reductions_norm_and_general_contractions(tmp_path):
 
 
 def test_wide_vocabulary_softmax_and_norm(tmp_path):
-    """Rows wider than a workgroup's registers take the two-pass streaming path."""
+    """Rows wider than a workgroup's registers take the two-pass streaming path.
+
+    Over 201,088 terms the oracle's sequential float32 sum (the reference CPU algorithm) itself drifts:
+    its softmax rows here sum to 1 + 3.3e-4. The device result is therefore held to the float32
+    tolerance against a float64 evaluation, and to 1e-3 against the oracle."""
     from chroma_amd.models.gpt_oss import RMSNorm
 
     x = torch.randn(3, 201088, generator=torch.Generator().manual_seed(5)) * 3
-    check(tmp_path / "softmax", Function(lambda x: x.softmax(-1)), x, second=False)
-    check(tmp_path / "norm", RMSNorm(201088).eval(), x, second=False)
+    for name, module in (("softmax", Function(lambda x: x.softmax(-1))), ("norm", RMSNorm(201088).eval())):
+        exported = torch.export.export(module, (x,))
+        with chroma_amd.compile(exported, tmp_path / name) as model:
+            got = model(x)
+        wide = x.double().numpy()
+        if name == "norm":
+            exact = wide / np.sqrt((wide**2).mean(axis=-1, keepdims=True) + 1e-5)
+        else:
+            exact = torch.softmax(x.double(), -1).numpy()
+        np.testing.assert_allclose(got, exact, **F32)
+        np.testing.assert_allclose(got, compile_cpu(exported, tmp_path / f"{name}_cpu")(x.numpy()), rtol=1e-3, atol=1e-5)
 
 
 def test_bfloat16_storage_rounding_and_float_accumulation(tmp_path):
