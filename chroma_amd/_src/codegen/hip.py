@@ -43,7 +43,9 @@ MAX_GRID = 16384
 ROW_THREADS = 256
 ROW_RESIDENT = 32
 STREAMING_STORES = True
-STREAMING_BYTES = 64 << 20  # below this a result may stay in the 4 MiB-per-XCD L2 for its consumer
+STREAMING_BYTES = 64 << 20
+FUSED_CONCAT_ELEMENTS = 1 << 16  # smaller concatenations are fused into their consumers
+DEFERRED_ELEMENTS = 1 << 16  # smaller expressions the front end asks to store stay fused instead  # below this a result may stay in the 4 MiB-per-XCD L2 for its consumer
 
 UNARY_OPS = {
     "reciprocal": "reciprocal",
@@ -135,7 +137,7 @@ class HIPCodegen(Codegen):
         self.sources[name] = frozenset().union(*(self.sources[v.name] for v in inputs)) if inputs else frozenset()
         value = self.expression_value(name, meta, inputs)
         if value.depth >= MAX_DEPTH or len(self.sources[name]) >= MAX_SOURCES:
-            return self.materialize(value)
+            return self.store(value)
         return value
 
     def read(self, k: Kernel, value: Value, coords: Sequence[Aff]) -> tuple:
@@ -165,6 +167,25 @@ class HIPCodegen(Codegen):
         return self.read(k, value, mine)
 
     def materialize(self, value: Value) -> Value:
+        """The front end's request to store ``value`` (``clone``/``contiguous``, or an elementwise result
+        with several consumers). Values are immutable, so storage is a performance decision here:
+
+        * a strided view of a stored buffer already has storage and is returned as one (consumers read it
+          through its strides; matrix kernels ask for ``contiguous`` instead);
+        * an expression of at most ``DEFERRED_ELEMENTS`` elements stays fused into each consumer, where it
+          costs a few instructions instead of a launch (consumers evaluate shared subexpressions once);
+        * anything larger is written to the arena once.
+        """
+        if value.stored:
+            return value
+        if value.view is not None and value.view.base is not None:
+            return Value(value.name, value.shape, value.dtype, value.deps, stored=True, view=value.view)
+        if math.prod(value.shape) <= DEFERRED_ELEMENTS:
+            return value
+        return self.store(value)
+
+    def store(self, value: Value) -> Value:
+        """Write ``value`` to a fresh arena allocation (once; later requests reuse it)."""
         if value.stored:
             return value
         if value.name not in self.materialized:
@@ -173,8 +194,26 @@ class HIPCodegen(Codegen):
             self.materialized[value.name] = out
         return self.materialized[value.name]
 
+    @staticmethod
+    def is_contiguous(value: Value) -> bool:
+        if not value.stored:
+            return False
+        natural = contiguous_strides(value.shape)
+        return all(size == 1 or a == b for size, a, b in zip(value.shape, value.view.strides, natural))
+
+    def contiguous(self, value: Value) -> Value:
+        """A stored, row-major copy of ``value`` (the value itself when it already is one)."""
+        if self.is_contiguous(value):
+            return value
+        key = value.name + "#contiguous"
+        if key not in self.materialized:
+            out = self.allocate(value.shape, value.dtype)
+            self.map_kernel(out, value)
+            self.materialized[key] = out
+        return self.materialized[key]
+
     def reshape(self, meta: torch.Tensor, x: Value) -> Value:
-        if x.stored:
+        if self.is_contiguous(x):
             return self.alias(meta, x.root, x.view.offset)
         shape = tuple(meta.shape)
 
@@ -329,6 +368,8 @@ class HIPCodegen(Codegen):
 
     # =================================================================================== concat
     def concatenate(self, meta, values: Sequence[Value], dim: int) -> Value:
+        if math.prod(meta.shape) <= FUSED_CONCAT_ELEMENTS:
+            return self._concat_expression(meta, values, dim)
         out = self.allocate(tuple(meta.shape), meta.dtype)
         shape = _shape(out.shape)
         innermost = dim == len(shape) - 1
@@ -373,6 +414,26 @@ class HIPCodegen(Codegen):
         grid = max(1, min(-(-vectors // MAP_THREADS), MAX_GRID))
         self.launch(k, grid, MAP_THREADS, values, kind="concat")
         return out
+
+    def _concat_expression(self, meta, values: Sequence[Value], dim: int) -> Value:
+        """Concatenation folded into its consumer: a select over the parts along ``dim``. Every part is
+        evaluated, each at its coordinate clamped into range, so unselected reads stay in bounds."""
+        starts = [0]
+        for value in values:
+            starts.append(starts[-1] + value.shape[dim])
+
+        def closure(k: Kernel, coords: List[Aff]) -> tuple:
+            along = coords[dim]
+            node = None
+            for i in reversed(range(len(values))):
+                start, size = starts[i], values[i].shape[dim]
+                local = list(coords)
+                local[dim] = k.derived(along, f"({{0}}) < {start}u ? 0u : (({{0}}) - {start}u < {size}u ? ({{0}}) - {start}u : {size - 1}u)", size - 1)
+                part = self.read(k, values[i], local)
+                node = part if node is None else ("sel", ("cmp", "<", along, ZERO, starts[i + 1]), part, node)
+            return node
+
+        return self.expr(meta, closure, list(values))
 
     # ================================================================================ row kernels
     def _row_layout(self, shape: Sequence[int], dim: int) -> Tuple[int, int, int]:
@@ -688,8 +749,8 @@ class HIPCodegen(Codegen):
         rows, columns, inner = math.prod(x.shape[:-1]), weight.shape[0], weight.shape[1]
         if max(rows, columns, inner) > 2**31 - 1:
             raise ValueError("Matrix dimensions exceed the integer range of the matrix kernels")
-        x, weight = self.materialize(x), self.materialize(weight)
-        bias = self.materialize(bias) if bias is not None else None
+        x, weight = self.contiguous(x), self.contiguous(weight)
+        bias = self.contiguous(bias) if bias is not None else None
         out = self.allocate(tuple(meta.shape), meta.dtype)
         dtypes = {x.dtype, weight.dtype, meta.dtype} | ({bias.dtype} if bias is not None else set())
         if len(dtypes) != 1:
@@ -765,8 +826,8 @@ class HIPCodegen(Codegen):
         prepared = []
         for label, value in zip(labels, values):
             reuse = math.prod(sizes[letter] for letter in output if letter not in label)
-            if not value.stored and value.view is None and reuse >= 8:
-                value = self.materialize(value)
+            if not value.stored and value.view is None and reuse >= 8 and math.prod(value.shape) > DEFERRED_ELEMENTS:
+                value = self.store(value)
             prepared.append(value)
         return self._loop_einsum(meta, labels, output, sizes, reduction, prepared)
 
@@ -782,7 +843,7 @@ class HIPCodegen(Codegen):
         weight, indices = source
         if weight.dtype != meta.dtype or weight.shape[-1] % 4:
             return None
-        weight, indices, x = self.materialize(weight), self.materialize(indices), self.materialize(values[1])
+        weight, indices, x = self.contiguous(weight), self.contiguous(indices), self.contiguous(values[1])
         if x.dtype != meta.dtype:
             return None
         out = self.allocate(tuple(meta.shape), meta.dtype)

@@ -258,7 +258,7 @@ class Kernel:
             return Aff.of(self.atoms[key])
         wide = aff.hi() > U32_LIMIT
         ctype = "uint64_t" if max(hi, aff.hi()) > U32_LIMIT else "uint32_t"
-        op = "div" if key[0] == "div" else "mod"
+        op = key[0]
         if aff.varying:
             atom = Atom(self.fresh("a"), hi, varying=True)
             for lane in range(self.lanes):
@@ -269,6 +269,11 @@ class Kernel:
         self.definitions[atom.name] = (op, aff, key[2])
         self.atoms[key] = atom
         return Aff.of(atom)
+
+    def derived(self, aff: Aff, fmt: str, hi: int) -> Aff:
+        """An integer computed from ``aff`` by the C template ``fmt`` (``{}`` = the affine value), with
+        inclusive maximum ``hi``; one value per lane when ``aff`` varies across lanes."""
+        return self._opaque(("derived", aff, fmt), aff, fmt, hi)
 
     def div(self, aff: Aff, divisor: int) -> Aff:
         if divisor == 1:

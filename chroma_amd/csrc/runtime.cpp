@@ -171,8 +171,9 @@ public:
                 launch.arguments[i] = &launch.pointers[i];
             }
         }
+        // The whole plan replays as one captured hipGraph unless CHROMA_HIP_GRAPH=0.
         const char* graph = std::getenv("CHROMA_HIP_GRAPH");
-        use_graph_ = graph != nullptr && std::strcmp(graph, "1") == 0;
+        use_graph_ = graph == nullptr || std::strcmp(graph, "0") != 0;
     }
 
     ~Program() {

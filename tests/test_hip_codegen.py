@@ -55,9 +55,11 @@ def test_dev_model_reuses_kernels_across_layers():
     generated = lower(make_dev_model(0), torch.arange(8, dtype=torch.int64))
     stats = generated.stats
     assert stats["expert_contractions"] == 24
-    assert stats["workspace_bytes"] == 75776
-    assert stats["unique_kernels"] <= 32 < stats["launches"]
-    assert stats["launches"] == stats["kernels"]
+    assert stats["workspace_bytes"] < stats["unreused_workspace_bytes"]
+    # Small concatenations, clones of views and multi-consumer expressions fuse into their consumers:
+    # 14 launches per layer plus the final norm and unembedding (the reference's CUDA backend: 361).
+    assert stats["launches"] == stats["kernels"] == 12 * 14 + 3
+    assert stats["unique_kernels"] < stats["launches"] // 3
 
 
 def test_linear_kernel_selection():
