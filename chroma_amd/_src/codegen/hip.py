@@ -45,7 +45,8 @@ ROW_RESIDENT = 32
 STREAMING_STORES = True
 STREAMING_BYTES = 64 << 20
 FUSED_CONCAT_ELEMENTS = 1 << 16  # smaller concatenations are fused into their consumers
-DEFERRED_ELEMENTS = 1 << 16  # smaller expressions the front end asks to store stay fused instead  # below this a result may stay in the 4 MiB-per-XCD L2 for its consumer
+DEFERRED_ELEMENTS = 1 << 16  # smaller expressions the front end asks to store stay fused instead
+REUSED_EVALUATIONS = 1 << 18  # a contraction operand is stored when (elements x reuse) reaches this  # below this a result may stay in the 4 MiB-per-XCD L2 for its consumer
 
 UNARY_OPS = {
     "reciprocal": "reciprocal",
@@ -105,6 +106,7 @@ class HIPCodegen(Codegen):
         self.expert_contractions = 0
         self.tiled_matmuls = 0
         self.skinny_matmuls = 0
+        self.mfma_matmuls = 0
 
     # ===================================================================================== storage
     def extern(self, tensor: torch.Tensor, kind: str, offset: int) -> Value:
@@ -759,7 +761,10 @@ class HIPCodegen(Codegen):
         if self.blas and rows <= 16 and inner % 4 == 0:
             self._skinny_linear(out, x, weight, bias, rows, columns, inner)
             self.skinny_matmuls += 1
-        elif self.blas and inner % 4 == 0:
+        elif self.blas and inner % (8 if meta.dtype == torch.bfloat16 else 4) == 0:
+            self._mfma_linear(out, x, weight, bias, rows, columns, inner)
+            self.mfma_matmuls += 1
+        elif self.blas:
             self._tiled_linear(out, x, weight, bias, rows, columns, inner)
             self.tiled_matmuls += 1
         else:
@@ -789,6 +794,14 @@ class HIPCodegen(Codegen):
             f"{args[0]}, {args[1]}, {args[2]}, {out_slot}, {columns}u);"
         )
         self.launch(k, blocks, 256, [x, weight] + ([bias] if bias is not None else []), kind="linear_skinny")
+
+    def _mfma_linear(self, out, x, weight, bias, rows, columns, inner) -> None:
+        k = Kernel(1)
+        args = [self._matrix_slot(k, x), self._matrix_slot(k, weight), self._matrix_slot(k, bias) if bias is not None else "nullptr"]
+        out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        function = "mfma_linear_bf16" if out.dtype == torch.bfloat16 else "mfma_linear_f32"
+        k.line(f"chroma::{function}({args[0]}, {args[1]}, {args[2]}, {out_slot}, {rows}u, {columns}u, {inner}u);")
+        self.launch(k, (-(-columns // 128), -(-rows // 128), 1), 256, [x, weight] + ([bias] if bias is not None else []), kind="linear_mfma")
 
     def _tiled_linear(self, out, x, weight, bias, rows, columns, inner) -> None:
         k = Kernel(1)
@@ -826,7 +839,8 @@ class HIPCodegen(Codegen):
         prepared = []
         for label, value in zip(labels, values):
             reuse = math.prod(sizes[letter] for letter in output if letter not in label)
-            if not value.stored and value.view is None and reuse >= 8 and math.prod(value.shape) > DEFERRED_ELEMENTS:
+            # An expression re-evaluated for many outputs is worth one store once the re-evaluations add up.
+            if not value.stored and value.view is None and reuse >= 8 and math.prod(value.shape) * reuse >= REUSED_EVALUATIONS:
                 value = self.store(value)
             prepared.append(value)
         return self._loop_einsum(meta, labels, output, sizes, reduction, prepared)
@@ -970,6 +984,7 @@ class HIPCodegen(Codegen):
             expert_contractions=self.expert_contractions,
             tiled_matmuls=self.tiled_matmuls,
             skinny_matmuls=self.skinny_matmuls,
+            mfma_matmuls=self.mfma_matmuls,
             unique_kernels=len(self.kernel_sources),
             launches=len(self.launches),
         )

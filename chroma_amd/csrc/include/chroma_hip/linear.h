@@ -195,4 +195,206 @@ __device__ __forceinline__ void tiled_linear(const T* __restrict__ x, const T* _
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Matrix-core product for bfloat16: Y[M, N] = X[M, K] . W[N, K]^T (+ bias), float32 accumulation in
+// the MFMA accumulators, one bfloat16 rounding of (sum + bias) at the end - the reference's bf16 linear
+// numerics (chroma/_src/codegen/cpu/kernels.h:63-74) with a different summation order.
+//
+// Workgroup: 256 threads = 4 waves, a 128 x 128 output tile, K staged through LDS 32 at a time
+// (rows padded by 8 elements against bank conflicts), double-buffered: the next K slice is loaded from
+// HBM into registers while the current one feeds the matrix cores. Each wave owns a 64 x 64 quadrant
+// as 4 x 4 tiles of v_mfma_f32_16x16x32_bf16. Operand layout of that instruction on gfx950: lane l
+// supplies A[row l % 16][k 8 * (l / 16) .. + 7] and B[k 8 * (l / 16) .. + 7][column l % 16]; it receives
+// D[rows 4 * (l / 16) .. + 3][column l % 16]. K must be a multiple of 8 (16-byte rows).
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void mfma_linear_bf16(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                 const uint16_t* __restrict__ bias, uint16_t* __restrict__ out,
+                                                 uint32_t m_total, uint32_t n_total, uint32_t k_total) {
+    constexpr int BM = 128, BN = 128, BK = 32, PAD = 8, LD = BK + PAD;
+    __shared__ __attribute__((aligned(16))) uint16_t as[2][BM * LD];
+    __shared__ __attribute__((aligned(16))) uint16_t bs[2][BN * LD];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid % 64u, wave = tid / 64u;
+    const uint32_t wm = wave / 2u, wn = wave % 2u;
+    const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+
+    // Global -> register staging: 512 chunks of 8 elements per operand tile, two per thread.
+    uint4 ra[2], rb[2];
+    auto fetch = [&](uint32_t k0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t chunk = tid + i * 256u;
+            const uint32_t row = chunk / 4u, kc = (chunk % 4u) * 8u;
+            const uint32_t gk = k0 + kc;
+            const uint32_t gm = m0 + row, gn = n0 + row;
+            ra[i] = (gm < m_total && gk < k_total) ? *reinterpret_cast<const uint4*>(x + size_t(gm) * k_total + gk) : uint4{0, 0, 0, 0};
+            rb[i] = (gn < n_total && gk < k_total) ? *reinterpret_cast<const uint4*>(w + size_t(gn) * k_total + gk) : uint4{0, 0, 0, 0};
+        }
+    };
+    auto stash = [&](int buffer) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t chunk = tid + i * 256u;
+            const uint32_t row = chunk / 4u, kc = (chunk % 4u) * 8u;
+            *reinterpret_cast<uint4*>(&as[buffer][row * LD + kc]) = ra[i];
+            *reinterpret_cast<uint4*>(&bs[buffer][row * LD + kc]) = rb[i];
+        }
+    };
+
+    f32x4_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
+    const uint32_t steps = (k_total + BK - 1) / BK;
+    fetch(0);
+    stash(0);
+    __syncthreads();
+    for (uint32_t step = 0; step < steps; ++step) {
+        const int buffer = step & 1;
+        if (step + 1 < steps) {
+            fetch((step + 1) * BK);
+        }
+        bf16x8_t a[4], b[4];
+        const uint32_t koff = (lane / 16u) * 8u;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t arow = wm * 64u + t * 16u + lane % 16u;
+            const uint32_t brow = wn * 64u + t * 16u + lane % 16u;
+            a[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(&as[buffer][arow * LD + koff]));
+            b[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(&bs[buffer][brow * LD + koff]));
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+            }
+        }
+        if (step + 1 < steps) {
+            stash(buffer ^ 1);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t gn = n0 + wn * 64u + j * 16u + lane % 16u;
+            if (gn >= n_total) {
+                continue;
+            }
+            const float b = bias ? bf16_to_f32(bias[gn]) : 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t gm = m0 + wm * 64u + i * 16u + (lane / 16u) * 4u + r;
+                if (gm < m_total) {
+                    out[size_t(gm) * n_total + gn] = f32_to_bf16(acc[i][j][r] + b);
+                }
+            }
+        }
+    }
+}
+
+// Matrix-core product for float32 (v_mfma_f32_16x16x4_f32): same tiling as the bfloat16 kernel with K
+// staged 16 at a time; lane l supplies A[row l % 16][k l / 16] and B[k l / 16][column l % 16] of each
+// 4-deep step. K must be a multiple of 4 (16-byte rows). The bias is added to the finished sum, as the
+// reference's float linear does after its GEMM (chroma/_src/codegen/cpu/kernels.h:46-61).
+__device__ __forceinline__ void mfma_linear_f32(const float* __restrict__ x, const float* __restrict__ w,
+                                                const float* __restrict__ bias, float* __restrict__ out,
+                                                uint32_t m_total, uint32_t n_total, uint32_t k_total) {
+    constexpr int BM = 128, BN = 128, BK = 16, PAD = 4, LD = BK + PAD;
+    __shared__ __attribute__((aligned(16))) float as[2][BM * LD];
+    __shared__ __attribute__((aligned(16))) float bs[2][BN * LD];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid % 64u, wave = tid / 64u;
+    const uint32_t wm = wave / 2u, wn = wave % 2u;
+    const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+
+    float4 ra[2], rb[2];
+    auto fetch = [&](uint32_t k0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t chunk = tid + i * 256u;
+            const uint32_t row = chunk / 4u, kc = (chunk % 4u) * 4u;
+            const uint32_t gk = k0 + kc;
+            const uint32_t gm = m0 + row, gn = n0 + row;
+            ra[i] = (gm < m_total && gk < k_total) ? *reinterpret_cast<const float4*>(x + size_t(gm) * k_total + gk) : float4{0, 0, 0, 0};
+            rb[i] = (gn < n_total && gk < k_total) ? *reinterpret_cast<const float4*>(w + size_t(gn) * k_total + gk) : float4{0, 0, 0, 0};
+        }
+    };
+    auto stash = [&](int buffer) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t chunk = tid + i * 256u;
+            const uint32_t row = chunk / 4u, kc = (chunk % 4u) * 4u;
+            *reinterpret_cast<float4*>(&as[buffer][row * LD + kc]) = ra[i];
+            *reinterpret_cast<float4*>(&bs[buffer][row * LD + kc]) = rb[i];
+        }
+    };
+
+    f32x4_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
+    const uint32_t steps = (k_total + BK - 1) / BK;
+    fetch(0);
+    stash(0);
+    __syncthreads();
+    for (uint32_t step = 0; step < steps; ++step) {
+        const int buffer = step & 1;
+        if (step + 1 < steps) {
+            fetch((step + 1) * BK);
+        }
+#pragma unroll
+        for (int s = 0; s < BK / 4; ++s) {
+            const uint32_t k = s * 4u + lane / 16u;
+            float a[4], b[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                a[t] = as[buffer][(wm * 64u + t * 16u + lane % 16u) * LD + k];
+                b[t] = bs[buffer][(wn * 64u + t * 16u + lane % 16u) * LD + k];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+        if (step + 1 < steps) {
+            stash(buffer ^ 1);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t gn = n0 + wn * 64u + j * 16u + lane % 16u;
+            if (gn >= n_total) {
+                continue;
+            }
+            const float b = bias ? bias[gn] : 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t gm = m0 + wm * 64u + i * 16u + (lane / 16u) * 4u + r;
+                if (gm < m_total) {
+                    out[size_t(gm) * n_total + gn] = acc[i][j][r] + b;
+                }
+            }
+        }
+    }
+}
+
 }  // namespace chroma

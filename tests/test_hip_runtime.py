@@ -56,7 +56,7 @@ def check(tmp_path, module, *inputs, blas=True, eager=True, second=True):
         saved = [np.array(a, copy=True) for a in leaves(actual)]
         model(*sets[-1])
         for got, want in zip(leaves(actual), saved):
-            np.testing.assert_array_equal(got.view(np.uint8), want.view(np.uint8))
+            np.testing.assert_array_equal(np.atleast_1d(got).view(np.uint8), np.atleast_1d(want).view(np.uint8))
     with Program(tmp_path / "hip") as loaded:
         compare(loaded(*inputs), oracle(*[numpy_of(v) for v in inputs]))
     return oracle
@@ -130,6 +130,25 @@ def test_linear_kernels(tmp_path, blas):
     check(tmp_path / "b", torch.nn.Linear(16, 7).eval(), torch.randn(16), blas=blas)
     check(tmp_path / "c", torch.nn.Linear(64, 300, bias=False).eval(), torch.randn(2, 3, 64), blas=blas)
     check(tmp_path / "d", torch.nn.Linear(128, 96).eval(), torch.randn(100, 128), blas=blas)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows, inner, columns", [(300, 200, 384), (129, 64, 130), (17, 2888, 96)])
+def test_matrix_core_linear(tmp_path, dtype, rows, inner, columns):
+    """MFMA products with partial 128 x 128 tiles and a partial last K step, against the oracle."""
+    generator = torch.Generator().manual_seed(rows + inner)
+    layer = torch.nn.Linear(inner, columns).eval()
+    with torch.no_grad():
+        layer.weight.copy_(torch.randn(columns, inner, generator=generator) * 0.05)
+        layer.bias.copy_(torch.randn(columns, generator=generator))
+    layer = layer.to(dtype)
+    x = torch.randn(rows, inner, generator=generator).to(dtype)
+    exported = torch.export.export(layer, (x,))
+    with chroma_amd.compile(exported, tmp_path / "hip") as model:
+        assert model.stats["mfma_matmuls"] == 1
+        got = model(x)
+    want = compile_cpu(exported, tmp_path / "cpu")(numpy_of(x))
+    assert_close(got, want, **tolerance(want))
 
 
 def test_aliases_and_live_workspace_across_linear_layers(tmp_path):
