@@ -46,7 +46,9 @@ STREAMING_STORES = True
 STREAMING_BYTES = 64 << 20
 FUSED_CONCAT_ELEMENTS = 1 << 16  # smaller concatenations are fused into their consumers
 DEFERRED_ELEMENTS = 1 << 16  # smaller expressions the front end asks to store stay fused instead
-REUSED_EVALUATIONS = 1 << 18  # a contraction operand is stored when (elements x reuse) reaches this  # below this a result may stay in the 4 MiB-per-XCD L2 for its consumer
+REUSED_EVALUATIONS = 1 << 18  # a contraction operand is stored when (elements x reuse) reaches this
+MATRIX_MIN_WORK = 1 << 18  # smaller batched products stay on the generic contraction kernel
+GROUPED_SLOTS = 64  # from this many (token, expert) slots on, expert products are grouped by expert  # below this a result may stay in the 4 MiB-per-XCD L2 for its consumer
 
 UNARY_OPS = {
     "reciprocal": "reciprocal",
@@ -101,6 +103,7 @@ class HIPCodegen(Codegen):
         self.kernel_sources: List[str] = []
         self.launches: List[Launch] = []
         self.gathers: Dict[str, Tuple[Value, Value]] = {}
+        self.routes: Dict[Tuple[str, int], Value] = {}
         self.extents: Dict[str, int] = {}
         self.parallel_reductions = 0
         self.expert_contractions = 0
@@ -310,7 +313,15 @@ class HIPCodegen(Codegen):
         return self.bindings[buffer]
 
     def launch(
-        self, k: Kernel, grid: Union[int, Tuple[int, int, int]], block: int, inputs: Sequence[Value], *, kind: str, prologue: Sequence[str] = ()
+        self,
+        k: Kernel,
+        grid: Union[int, Tuple[int, int, int]],
+        block: int,
+        inputs: Sequence[Value],
+        *,
+        kind: str,
+        prologue: Sequence[str] = (),
+        shared: int = 0,
     ) -> None:
         """Record one launch of ``k``; identical kernels (same code, same parameter types) are emitted once.
 
@@ -331,7 +342,7 @@ class HIPCodegen(Codegen):
             if allocation is not None:
                 allocation.end = max(allocation.end, self.kernels)
         self.record_usage(inputs)
-        self.launches.append(Launch(name, grid3, block, bindings))
+        self.launches.append(Launch(name, grid3, block, bindings, shared))
         self.kernels += 1
 
     def map_kernel(self, out: Value, value: Value, target: Optional[str] = None) -> None:
@@ -799,8 +810,7 @@ class HIPCodegen(Codegen):
         k = Kernel(1)
         args = [self._matrix_slot(k, x), self._matrix_slot(k, weight), self._matrix_slot(k, bias) if bias is not None else "nullptr"]
         out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
-        function = "mfma_linear_bf16" if out.dtype == torch.bfloat16 else "mfma_linear_f32"
-        k.line(f"chroma::{function}({args[0]}, {args[1]}, {args[2]}, {out_slot}, {rows}u, {columns}u, {inner}u);")
+        k.line(f"chroma::mfma_linear<{ctype_of(out.dtype)}>({args[0]}, {args[1]}, {args[2]}, {out_slot}, {rows}u, {columns}u, {inner}u);")
         self.launch(k, (-(-columns // 128), -(-rows // 128), 1), 256, [x, weight] + ([bias] if bias is not None else []), kind="linear_mfma")
 
     def _tiled_linear(self, out, x, weight, bias, rows, columns, inner) -> None:
@@ -836,6 +846,9 @@ class HIPCodegen(Codegen):
         expert = self._expert_einsum(meta, eqn, labels, sizes, values)
         if expert is not None:
             return expert
+        matrix = self._matrix_einsum(meta, labels, output, sizes, reduction, values)
+        if matrix is not None:
+            return matrix
         prepared = []
         for label, value in zip(labels, values):
             reuse = math.prod(sizes[letter] for letter in output if letter not in label)
@@ -864,6 +877,11 @@ class HIPCodegen(Codegen):
         tokens, selected, channels = out.shape
         inner = weight.shape[-1]
         experts = weight.shape[0]
+        per_slot = eqn == "beck,bek->bec"
+        if tokens * selected >= GROUPED_SLOTS and inner % (8 if meta.dtype == torch.bfloat16 else 4) == 0 and experts <= 4096:
+            self._grouped_experts(out, weight, indices, x, tokens, selected, experts, channels, inner, per_slot)
+            self.expert_contractions += 1
+            return out
         lanes_per_row = 64
         while lanes_per_row > 1 and inner % (4 * lanes_per_row):
             lanes_per_row //= 2
@@ -881,6 +899,110 @@ class HIPCodegen(Codegen):
         self.launch(k, (blocks_per_slot, tokens * selected, 1), 256, [weight, indices, x], kind="expert_linear")
         self.expert_contractions += 1
         return out
+
+    def _matrix_einsum(self, meta, labels, output, sizes, reduction, values) -> Optional[Value]:
+        """A batched matrix product on the matrix cores (the reference's ``matrix`` hook, gpu.py:426-435,
+        which its CUDA backend leaves to the scalar loop). Taken when the contraction has one row, one
+        column and one contracted label, the operands can be read in place with unit stride along the
+        contracted label (or along the column label for the right operand), and the product is large
+        enough to fill 128 x 128 tiles."""
+        found = matrix_axes(labels, output, reduction)
+        if not self.blas or found is None:
+            return None
+        batch, row, column, inner = found
+        dtype = meta.dtype
+        if any(v.dtype != dtype for v in values) or dtype not in (torch.float32, torch.bfloat16):
+            return None
+        rows, columns, depth = sizes[row], sizes[column], sizes[inner]
+        chunk = 8 if dtype == torch.bfloat16 else 4
+        if rows * columns * depth < MATRIX_MIN_WORK or depth % chunk or rows < 16 or columns < 16:
+            return None
+        out_shape = tuple(meta.shape)
+        out_strides = dict(zip(output, contiguous_strides(out_shape)))
+        if out_strides[column] != 1:
+            return None
+        operands, layouts = [], []
+        for label, value in zip(labels, values):
+            if any(value.shape[label.index(letter)] != sizes[letter] for letter in (row, column, inner) if letter in label):
+                return None
+            if not value.stored:
+                value = self.store(value)
+            strides = dict(zip(label, value.view.strides))
+            for letter, size in zip(label, value.shape):
+                if size == 1:
+                    strides[letter] = 0
+            operands.append(value)
+            layouts.append(strides)
+        left, right = layouts
+        if left[inner] != 1 or left[row] % chunk:
+            return None
+        if right[inner] == 1 and right[column] % chunk == 0:
+            k_contiguous, ldb = True, right[column]
+        elif right[column] == 1 and right[inner] % chunk == 0:
+            k_contiguous, ldb = False, right[inner]
+        else:
+            return None
+        for value, strides in zip(operands, layouts):
+            if value.view.offset % chunk or any(strides.get(letter, 0) % chunk for letter in batch):
+                return None
+        out = self.allocate(out_shape, dtype)
+        k = Kernel(1)
+        batch_sizes = tuple(sizes[letter] for letter in batch) or (1,)
+        batches = math.prod(batch_sizes)
+        coords = k.unflatten(Aff.of(k.atom("blockIdx.z", batches - 1, prefix="z")), batch_sizes) if batch else []
+        pointers, ends = [], []
+        spans = ((rows - 1) * left[row] + depth - 1, (columns - 1) * ldb + depth - 1 if k_contiguous else (depth - 1) * ldb + columns - 1)
+        for value, strides, span in zip(operands, layouts, spans):
+            offset = Aff((), value.view.offset)
+            for coord, letter in zip(coords, batch):
+                offset = offset + coord.scale(strides.get(letter, 0))
+            root = value.root
+            slot = k.slot(root.name, root.dtype, extent=self.extents[root.name])
+            k.check_bounds(slot, offset + span)
+            pointers.append(f"{slot} + ({offset.code()})")
+        out_offset = ZERO
+        for coord, letter in zip(coords, batch):
+            out_offset = out_offset + coord.scale(out_strides[letter])
+        out_slot = k.slot(out.name, dtype, writable=True, extent=self.extents[out.name])
+        k.check_bounds(out_slot, out_offset + ((rows - 1) * out_strides[row] + columns - 1))
+        k.line(
+            f"chroma::mfma_gemm<{ctype_of(dtype)}, {str(k_contiguous).lower()}>({pointers[0]}, {left[row]}u, {pointers[1]}, {ldb}u, "
+            f"nullptr, {out_slot} + ({out_offset.code()}), {out_strides[row]}u, {rows}u, {columns}u, {depth}u, nullptr, nullptr, blockIdx.y * 128u);"
+        )
+        self.launch(k, (-(-columns // 128), -(-rows // 128), batches), 256, operands, kind="matmul_mfma")
+        self.matrix_contractions += 1
+        self.mfma_matmuls += 1
+        return out
+
+    def _route(self, indices: Value, experts: int) -> Tuple[Value, int]:
+        """Group the slots of a router output by expert once; both expert contractions of a layer share it."""
+        key = (indices.name, experts)
+        slots = math.prod(indices.shape)
+        tiles = -(-slots // 128) + experts
+        if key not in self.routes:
+            words = 2 * experts + 2 + slots + 2 * tiles
+            scratch = self.allocate((-(-words // 2),), torch.int64)
+            k = Kernel(1)
+            ids = self._matrix_slot(k, indices)
+            table = k.slot(scratch.name, torch.int64, writable=True, extent=self.extents[scratch.name])
+            k.uses_error = True
+            k.line(f"chroma::route_slots({ids}, {slots}u, {experts}u, reinterpret_cast<int32_t*>({table}), error);")
+            self.launch(k, 1, 1024, [indices], kind="route", shared=4 * experts)
+            self.routes[key] = scratch
+        return self.routes[key], tiles
+
+    def _grouped_experts(self, out, weight, indices, x, tokens, selected, experts, channels, inner, per_slot) -> None:
+        scratch, tiles = self._route(indices, experts)
+        k = Kernel(1)
+        w, xs = self._matrix_slot(k, weight), self._matrix_slot(k, x)
+        table = k.slot(scratch.name, torch.int64, extent=self.extents[scratch.name])
+        out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        k.line(
+            f"chroma::grouped_expert_linear<{ctype_of(out.dtype)}, {str(per_slot).lower()}>({w}, {xs}, {out_slot}, "
+            f"reinterpret_cast<const int32_t*>({table}), {tokens * selected}u, {selected}u, {experts}u, {channels}u, {inner}u);"
+        )
+        self.launch(k, (-(-channels // 128), tiles, 1), 256, [weight, x, scratch], kind="experts_mfma")
+        self.mfma_matmuls += 1
 
     def _loop_einsum(self, meta, labels, output, sizes, reduction, values) -> Value:
         out = self.allocate(tuple(meta.shape), meta.dtype)

@@ -196,50 +196,86 @@ __device__ __forceinline__ void tiled_linear(const T* __restrict__ x, const T* _
 }
 
 // ---------------------------------------------------------------------------------------------
-// Matrix-core product for bfloat16: Y[M, N] = X[M, K] . W[N, K]^T (+ bias), float32 accumulation in
-// the MFMA accumulators, one bfloat16 rounding of (sum + bias) at the end - the reference's bf16 linear
-// numerics (chroma/_src/codegen/cpu/kernels.h:63-74) with a different summation order.
+// Matrix-core products. C[m, n] = sum_k A[m, k] B[k, n] (+ bias[n]) for one batch entry, float32
+// accumulation in the MFMA accumulators and one rounding to the storage type at the store - the
+// reference's numerics for float and bfloat16 products (chroma/_src/codegen/cpu/kernels.h:24-74) with a
+// different summation order.
 //
-// Workgroup: 256 threads = 4 waves, a 128 x 128 output tile, K staged through LDS 32 at a time
-// (rows padded by 8 elements against bank conflicts), double-buffered: the next K slice is loaded from
-// HBM into registers while the current one feeds the matrix cores. Each wave owns a 64 x 64 quadrant
-// as 4 x 4 tiles of v_mfma_f32_16x16x32_bf16. Operand layout of that instruction on gfx950: lane l
-// supplies A[row l % 16][k 8 * (l / 16) .. + 7] and B[k 8 * (l / 16) .. + 7][column l % 16]; it receives
-// D[rows 4 * (l / 16) .. + 3][column l % 16]. K must be a multiple of 8 (16-byte rows).
+// A is row-major with unit k stride: A[m, k] at a[m * lda + k]. B is either k-contiguous
+// (B[k, n] at b[n * ldb + k], a linear layer's weight) or n-contiguous (B[k, n] at b[k * ldb + n]); C is
+// row-major, C[m, n] at c[m * ldc + n]. Row strides and base addresses must keep 16-byte alignment.
+//
+// Workgroup: 256 threads = 4 waves, a 128 x 128 output tile, K staged through LDS in slices (32 for
+// bfloat16, 16 for float), double-buffered so the next slice streams from HBM while the current one
+// feeds the matrix cores. LDS rows are padded against bank conflicts. Each wave owns a 64 x 64 quadrant
+// as 4 x 4 tiles of v_mfma_f32_16x16x32_bf16 (lane l supplies A[row l % 16][k 8(l / 16) .. +7] and
+// B[k 8(l / 16) .. +7][column l % 16]) or v_mfma_f32_16x16x4_f32 (A[l % 16][l / 16], B[l / 16][l % 16]);
+// lane l receives D[rows 4(l / 16) .. +3][column l % 16].
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ void mfma_linear_bf16(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-                                                 const uint16_t* __restrict__ bias, uint16_t* __restrict__ out,
-                                                 uint32_t m_total, uint32_t n_total, uint32_t k_total) {
-    constexpr int BM = 128, BN = 128, BK = 32, PAD = 8, LD = BK + PAD;
-    __shared__ __attribute__((aligned(16))) uint16_t as[2][BM * LD];
-    __shared__ __attribute__((aligned(16))) uint16_t bs[2][BN * LD];
+template <class T> struct Mfma;
+template <> struct Mfma<uint16_t> {
+    static constexpr int BK = 32, PAD = 8, CHUNK = 8;  // a 16-byte chunk holds 8 elements
+    using Chunk = uint4;
+};
+template <> struct Mfma<float> {
+    static constexpr int BK = 16, PAD = 4, CHUNK = 4;
+    using Chunk = float4;
+};
+
+template <class T, bool B_K_CONTIGUOUS>
+__device__ __forceinline__ void mfma_gemm(const T* __restrict__ a, uint32_t lda, const T* __restrict__ b, uint32_t ldb,
+                                          const T* __restrict__ bias, T* __restrict__ c, uint32_t ldc, uint32_t m_total,
+                                          uint32_t n_total, uint32_t k_total, const int32_t* __restrict__ a_rows,
+                                          const int32_t* __restrict__ c_rows, uint32_t m_base) {
+    using M = Mfma<T>;
+    using Chunk = typename M::Chunk;
+    constexpr int BM = 128, BN = 128, BK = M::BK, LD = BK + M::PAD, CH = M::CHUNK;
+    constexpr int A_CHUNKS = BM * BK / CH / 256;  // 16-byte chunks each thread moves per slice
+    __shared__ __attribute__((aligned(16))) T as[2][BM * LD];
+    __shared__ __attribute__((aligned(16))) T bs[2][BN * LD];
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid % 64u, wave = tid / 64u;
     const uint32_t wm = wave / 2u, wn = wave % 2u;
-    const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const uint32_t m0 = m_base, n0 = blockIdx.x * BN;
 
-    // Global -> register staging: 512 chunks of 8 elements per operand tile, two per thread.
-    uint4 ra[2], rb[2];
+    Chunk ra[A_CHUNKS], rb[A_CHUNKS];
     auto fetch = [&](uint32_t k0) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < A_CHUNKS; ++i) {
             const uint32_t chunk = tid + i * 256u;
-            const uint32_t row = chunk / 4u, kc = (chunk % 4u) * 8u;
-            const uint32_t gk = k0 + kc;
-            const uint32_t gm = m0 + row, gn = n0 + row;
-            ra[i] = (gm < m_total && gk < k_total) ? *reinterpret_cast<const uint4*>(x + size_t(gm) * k_total + gk) : uint4{0, 0, 0, 0};
-            rb[i] = (gn < n_total && gk < k_total) ? *reinterpret_cast<const uint4*>(w + size_t(gn) * k_total + gk) : uint4{0, 0, 0, 0};
+            const uint32_t row = chunk / (BK / CH), kc = (chunk % (BK / CH)) * CH;
+            const uint32_t gk = k0 + kc, gm = m0 + row;
+            const size_t arow = a_rows ? size_t(a_rows[gm < m_total ? gm : 0]) : size_t(gm);
+            ra[i] = (gm < m_total && gk < k_total) ? *reinterpret_cast<const Chunk*>(a + arow * lda + gk) : Chunk{};
+            if constexpr (B_K_CONTIGUOUS) {
+                const uint32_t gn = n0 + row;
+                rb[i] = (gn < n_total && gk < k_total) ? *reinterpret_cast<const Chunk*>(b + size_t(gn) * ldb + gk) : Chunk{};
+            } else {
+                // n-contiguous B: chunk i covers CH consecutive columns of one k row.
+                const uint32_t kr = chunk / (BN / CH), nc = (chunk % (BN / CH)) * CH;
+                const uint32_t gkr = k0 + kr, gn = n0 + nc;
+                rb[i] = (gkr < k_total && gn < n_total) ? *reinterpret_cast<const Chunk*>(b + size_t(gkr) * ldb + gn) : Chunk{};
+            }
         }
     };
     auto stash = [&](int buffer) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < A_CHUNKS; ++i) {
             const uint32_t chunk = tid + i * 256u;
-            const uint32_t row = chunk / 4u, kc = (chunk % 4u) * 8u;
-            *reinterpret_cast<uint4*>(&as[buffer][row * LD + kc]) = ra[i];
-            *reinterpret_cast<uint4*>(&bs[buffer][row * LD + kc]) = rb[i];
+            const uint32_t row = chunk / (BK / CH), kc = (chunk % (BK / CH)) * CH;
+            *reinterpret_cast<Chunk*>(&as[buffer][row * LD + kc]) = ra[i];
+            if constexpr (B_K_CONTIGUOUS) {
+                *reinterpret_cast<Chunk*>(&bs[buffer][row * LD + kc]) = rb[i];
+            } else {
+                const uint32_t kr = chunk / (BN / CH), nc = (chunk % (BN / CH)) * CH;
+                const T* values = reinterpret_cast<const T*>(&rb[i]);
+#pragma unroll
+                for (int e = 0; e < CH; ++e) {
+                    bs[buffer][(nc + e) * LD + kr] = values[e];
+                }
+            }
         }
     };
 
@@ -260,20 +296,38 @@ __device__ __forceinline__ void mfma_linear_bf16(const uint16_t* __restrict__ x,
         if (step + 1 < steps) {
             fetch((step + 1) * BK);
         }
-        bf16x8_t a[4], b[4];
-        const uint32_t koff = (lane / 16u) * 8u;
+        if constexpr (sizeof(T) == 2) {
+            bf16x8_t fa[4], fb[4];
+            const uint32_t koff = (lane / 16u) * 8u;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const uint32_t arow = wm * 64u + t * 16u + lane % 16u;
-            const uint32_t brow = wn * 64u + t * 16u + lane % 16u;
-            a[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(&as[buffer][arow * LD + koff]));
-            b[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(&bs[buffer][brow * LD + koff]));
-        }
+            for (int t = 0; t < 4; ++t) {
+                fa[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(&as[buffer][(wm * 64u + t * 16u + lane % 16u) * LD + koff]));
+                fb[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(&bs[buffer][(wn * 64u + t * 16u + lane % 16u) * LD + koff]));
+            }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < 4; ++i) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < 4; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int sub = 0; sub < BK / 4; ++sub) {
+                const uint32_t k = sub * 4u + lane / 16u;
+                float fa[4], fb[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    fa[t] = as[buffer][(wm * 64u + t * 16u + lane % 16u) * LD + k];
+                    fb[t] = bs[buffer][(wn * 64u + t * 16u + lane % 16u) * LD + k];
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[i], fb[j], acc[i][j], 0, 0, 0);
+                    }
+                }
             }
         }
         if (step + 1 < steps) {
@@ -289,112 +343,111 @@ __device__ __forceinline__ void mfma_linear_bf16(const uint16_t* __restrict__ x,
             if (gn >= n_total) {
                 continue;
             }
-            const float b = bias ? bf16_to_f32(bias[gn]) : 0.0f;
+            const float offset = bias ? load1<T>(bias + gn) : 0.0f;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const uint32_t gm = m0 + wm * 64u + i * 16u + (lane / 16u) * 4u + r;
                 if (gm < m_total) {
-                    out[size_t(gm) * n_total + gn] = f32_to_bf16(acc[i][j][r] + b);
+                    const size_t crow = c_rows ? size_t(c_rows[gm]) : size_t(gm);
+                    store1<T>(c + crow * ldc + gn, acc[i][j][r] + offset);
                 }
             }
         }
     }
 }
 
-// Matrix-core product for float32 (v_mfma_f32_16x16x4_f32): same tiling as the bfloat16 kernel with K
-// staged 16 at a time; lane l supplies A[row l % 16][k l / 16] and B[k l / 16][column l % 16] of each
-// 4-deep step. K must be a multiple of 4 (16-byte rows). The bias is added to the finished sum, as the
-// reference's float linear does after its GEMM (chroma/_src/codegen/cpu/kernels.h:46-61).
-__device__ __forceinline__ void mfma_linear_f32(const float* __restrict__ x, const float* __restrict__ w,
-                                                const float* __restrict__ bias, float* __restrict__ out,
-                                                uint32_t m_total, uint32_t n_total, uint32_t k_total) {
-    constexpr int BM = 128, BN = 128, BK = 16, PAD = 4, LD = BK + PAD;
-    __shared__ __attribute__((aligned(16))) float as[2][BM * LD];
-    __shared__ __attribute__((aligned(16))) float bs[2][BN * LD];
-    const uint32_t tid = threadIdx.x;
-    const uint32_t lane = tid % 64u, wave = tid / 64u;
-    const uint32_t wm = wave / 2u, wn = wave % 2u;
-    const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+// A linear layer on the matrix cores: Y[M, N] = X[M, K] . W[N, K]^T (+ bias).
+template <class T>
+__device__ __forceinline__ void mfma_linear(const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias,
+                                            T* __restrict__ out, uint32_t m_total, uint32_t n_total, uint32_t k_total) {
+    mfma_gemm<T, true>(x, k_total, w, k_total, bias, out, n_total, m_total, n_total, k_total, nullptr, nullptr, blockIdx.y * 128u);
+}
 
-    float4 ra[2], rb[2];
-    auto fetch = [&](uint32_t k0) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint32_t chunk = tid + i * 256u;
-            const uint32_t row = chunk / 4u, kc = (chunk % 4u) * 4u;
-            const uint32_t gk = k0 + kc;
-            const uint32_t gm = m0 + row, gn = n0 + row;
-            ra[i] = (gm < m_total && gk < k_total) ? *reinterpret_cast<const float4*>(x + size_t(gm) * k_total + gk) : float4{0, 0, 0, 0};
-            rb[i] = (gn < n_total && gk < k_total) ? *reinterpret_cast<const float4*>(w + size_t(gn) * k_total + gk) : float4{0, 0, 0, 0};
-        }
-    };
-    auto stash = [&](int buffer) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint32_t chunk = tid + i * 256u;
-            const uint32_t row = chunk / 4u, kc = (chunk % 4u) * 4u;
-            *reinterpret_cast<float4*>(&as[buffer][row * LD + kc]) = ra[i];
-            *reinterpret_cast<float4*>(&bs[buffer][row * LD + kc]) = rb[i];
-        }
-    };
-
-    f32x4_t acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        }
+// ---------------------------------------------------------------------------------------------
+// Expert-grouped mixture-of-experts products.
+//
+// ``route_slots`` (one workgroup) turns the [tokens x selected] expert ids into a slot permutation grouped
+// by expert and a table of 128-slot tiles; ids are checked like every gather (negative ids wrap, an id
+// outside [-experts, experts) raises the error word and counts as expert 0). Layout of ``scratch``
+// (int32): [0, E) per-expert counts, [E, 2E+1) offsets, [2E+1] tile count, then ``slots`` permutation
+// entries, then the tile table as (expert, first row) pairs.
+// ``grouped_expert_linear`` then computes, for every tile, Y[slot, :] = W[e] . X[row(slot)]^T on the
+// matrix cores: each expert's [C, K] slab is read once per tile instead of once per slot. Every output
+// row is an independent dot product, so the order of slots inside a group changes no result bit.
+__device__ __forceinline__ void route_slots(const int64_t* __restrict__ indices, uint32_t slots, uint32_t experts,
+                                            int32_t* __restrict__ scratch, unsigned int* error) {
+    extern __shared__ int32_t shared_counts[];
+    int32_t* counts = scratch;
+    int32_t* offsets = scratch + experts;
+    int32_t* tile_count = scratch + 2 * experts + 1;
+    int32_t* permutation = tile_count + 1;
+    int32_t* tiles = permutation + slots;
+    for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) {
+        shared_counts[e] = 0;
     }
-    const uint32_t steps = (k_total + BK - 1) / BK;
-    fetch(0);
-    stash(0);
     __syncthreads();
-    for (uint32_t step = 0; step < steps; ++step) {
-        const int buffer = step & 1;
-        if (step + 1 < steps) {
-            fetch((step + 1) * BK);
-        }
-#pragma unroll
-        for (int s = 0; s < BK / 4; ++s) {
-            const uint32_t k = s * 4u + lane / 16u;
-            float a[4], b[4];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                a[t] = as[buffer][(wm * 64u + t * 16u + lane % 16u) * LD + k];
-                b[t] = bs[buffer][(wn * 64u + t * 16u + lane % 16u) * LD + k];
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
-                }
-            }
-        }
-        if (step + 1 < steps) {
-            stash(buffer ^ 1);
-        }
-        __syncthreads();
+    for (uint32_t t = threadIdx.x; t < slots; t += blockDim.x) {
+        const uint32_t e = uint32_t(checked_index(indices[t], experts, true, error));
+        atomicAdd(&shared_counts[e], 1);
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t gn = n0 + wn * 64u + j * 16u + lane % 16u;
-            if (gn >= n_total) {
-                continue;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int32_t running = 0, tile = 0;
+        for (uint32_t e = 0; e < experts; ++e) {
+            const int32_t count = shared_counts[e];
+            counts[e] = count;
+            offsets[e] = running;
+            for (int32_t first = 0; first < count; first += 128) {
+                tiles[2 * tile] = int32_t(e);
+                tiles[2 * tile + 1] = first;
+                ++tile;
             }
-            const float b = bias ? bias[gn] : 0.0f;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t gm = m0 + wm * 64u + i * 16u + (lane / 16u) * 4u + r;
-                if (gm < m_total) {
-                    out[size_t(gm) * n_total + gn] = acc[i][j][r] + b;
-                }
-            }
+            running += count;
         }
+        offsets[experts] = running;
+        *tile_count = tile;
     }
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) {
+        shared_counts[e] = offsets[e];
+    }
+    __syncthreads();
+    for (uint32_t t = threadIdx.x; t < slots; t += blockDim.x) {
+        int64_t raw = indices[t];
+        raw = raw < 0 ? raw + int64_t(experts) : raw;
+        const uint32_t e = (raw < 0 || raw >= int64_t(experts)) ? 0u : uint32_t(raw);
+        permutation[atomicAdd(&shared_counts[e], 1)] = int32_t(t);
+    }
+}
+
+// Per-slot input rows (``PER_SLOT``: X is [slots, K]) or per-token rows (X is [tokens, K], token = slot /
+// selected). ``rows`` receives the A-row of each permuted slot and is filled by the first block of each
+// tile before its product; grid = (ceil(C / 128), max tiles).
+template <class T, bool PER_SLOT>
+__device__ __forceinline__ void grouped_expert_linear(const T* __restrict__ w, const T* __restrict__ x, T* __restrict__ out,
+                                                      const int32_t* __restrict__ scratch, uint32_t slots, uint32_t selected,
+                                                      uint32_t experts, uint32_t channels, uint32_t inner) {
+    __shared__ int32_t a_rows[128], c_rows[128];
+    const int32_t* offsets = scratch + experts;
+    const int32_t tile_count = scratch[2 * experts + 1];
+    const int32_t* permutation = scratch + 2 * experts + 2;
+    const int32_t* tiles = permutation + slots;
+    const int32_t tile = int32_t(blockIdx.y);
+    if (tile >= tile_count) {
+        return;
+    }
+    const uint32_t expert = uint32_t(tiles[2 * tile]);
+    const uint32_t first = uint32_t(tiles[2 * tile + 1]);
+    const uint32_t count = uint32_t(offsets[expert + 1] - offsets[expert]);
+    const uint32_t rows = count - first < 128u ? count - first : 128u;
+    for (uint32_t r = threadIdx.x; r < 128u; r += blockDim.x) {
+        const int32_t slot = r < rows ? permutation[offsets[expert] + first + r] : 0;
+        a_rows[r] = PER_SLOT ? slot : slot / int32_t(selected);
+        c_rows[r] = slot;
+    }
+    __syncthreads();
+    mfma_gemm<T, true>(x, inner, w + size_t(expert) * channels * inner, inner, nullptr, out, channels, rows, channels, inner,
+                       a_rows, c_rows, 0u);
 }
 
 }  // namespace chroma

@@ -69,7 +69,7 @@ def test_linear_kernel_selection():
         assert kind in generated.files["model.hip"], kind
         assert generated.stats["workspace_bytes"] == 0  # the result is written straight into the output
     assert "linear_tiled" in lower(torch.nn.Linear(17, 7).eval(), torch.ones(40, 17)).files["model.hip"]
-    assert "mfma_linear_bf16" in lower(torch.nn.Linear(64, 7).bfloat16().eval(), torch.ones(40, 64, dtype=torch.bfloat16)).files["model.hip"]
+    assert "mfma_linear<uint16_t>" in lower(torch.nn.Linear(64, 7).bfloat16().eval(), torch.ones(40, 64, dtype=torch.bfloat16)).files["model.hip"]
     # bfloat16 keeps float accumulation in both paths
     generated = lower(torch.nn.Linear(17, 7).bfloat16().eval(), torch.ones(3, 5, 17, dtype=torch.bfloat16))
     assert generated.inputs[0]["dtype"] == "bfloat16" and generated.outputs[0]["dtype"] == "bfloat16"

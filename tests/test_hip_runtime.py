@@ -151,6 +151,63 @@ def test_matrix_core_linear(tmp_path, dtype, rows, inner, columns):
     assert_close(got, want, **tolerance(want))
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_matrix_core_contractions(tmp_path, dtype):
+    """Attention-shaped einsums on the batched MFMA path: k-contiguous and n-contiguous right operands,
+    a grouped-query operand broadcast along a batch label, and partial tiles."""
+    generator = torch.Generator().manual_seed(11)
+
+    def rand(*shape):
+        return (torch.randn(*shape, generator=generator) * 0.5).to(dtype)
+
+    def scores(q, k):
+        return torch.einsum("qhmd,khmd->hmqk", q, k[:, :, None, :].expand(-1, -1, 4, -1))
+
+    def attend(w, v):
+        return torch.einsum("hmqk,khmd->qhmd", w, v[:, :, None, :].expand(-1, -1, 4, -1))
+
+    cases = [
+        ("qhd", Function(lambda a, b: torch.einsum("qhd,khd->hqk", a, b)), (rand(135, 3, 64), rand(167, 3, 64))),
+        ("hqk", Function(lambda a, b: torch.einsum("hqk,khd->qhd", a, b)), (rand(3, 135, 168), rand(168, 3, 40))),
+        ("gqa-scores", Function(scores), (rand(130, 2, 4, 64), rand(140, 2, 64))),
+        ("gqa-attend", Function(attend), (rand(2, 4, 130, 144), rand(144, 2, 64))),
+    ]
+    for name, module, inputs in cases:
+        exported = torch.export.export(module, inputs)
+        with chroma_amd.compile(exported, tmp_path / name) as model:
+            assert model.stats["mfma_matmuls"] == 1, name
+            got = model(*inputs)
+        compare(got, compile_cpu(exported, tmp_path / f"{name}-cpu")(*[numpy_of(v) for v in inputs]))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_grouped_expert_products(tmp_path, dtype):
+    """Many-token selected-expert contractions take the routed, expert-grouped MFMA path; negative ids wrap
+    and an out-of-range id raises IndexError without poisoning the next call."""
+
+    class Experts(torch.nn.Module):
+        def forward(self, weights, indices, x, per_slot):
+            selected = weights[indices]
+            return torch.einsum("beck,bk->bec", selected, x), torch.einsum("beck,bek->bec", selected, per_slot)
+
+    generator = torch.Generator().manual_seed(3)
+    weights = (torch.randn(6, 160, 72, generator=generator) * 0.2).to(dtype)
+    indices = torch.randint(-6, 6, (40, 3), generator=generator)
+    x = torch.randn(40, 72, generator=generator).to(dtype)
+    per_slot = torch.randn(40, 3, 72, generator=generator).to(dtype)
+    inputs = (weights, indices, x, per_slot)
+    exported = torch.export.export(Experts(), inputs)
+    oracle = compile_cpu(exported, tmp_path / "cpu")
+    with chroma_amd.compile(exported, tmp_path / "hip") as model:
+        assert model.stats["expert_contractions"] == 2 and model.stats["mfma_matmuls"] == 2
+        compare(model(*inputs), oracle(*[numpy_of(v) for v in inputs]))
+        bad = indices.clone()
+        bad[7, 1] = 6
+        with pytest.raises(IndexError):
+            model(weights, bad, x, per_slot)
+        compare(model(*inputs), oracle(*[numpy_of(v) for v in inputs]))
+
+
 def test_aliases_and_live_workspace_across_linear_layers(tmp_path):
     def fn(x, w):
         first = torch.nn.functional.linear(x, w)
