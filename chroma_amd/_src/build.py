@@ -104,7 +104,7 @@ def build(generated: GeneratedCode, output, *, load: bool = True):
 
     inputs, outputs, weights = generated.inputs, generated.outputs, generated.weights
     library = f"_chroma_{uuid.uuid4().hex}.hsaco"
-    weights_name = f"weights-{hashlib.sha256(weights).hexdigest()[:20]}.bin"
+    weights_name = f"weights-{weights.hexdigest()[:20]}.bin"
     output = Path(output).resolve()
     output.mkdir(parents=True, exist_ok=True)
     stale = _artifact_files(output)
@@ -118,7 +118,7 @@ def build(generated: GeneratedCode, output, *, load: bool = True):
         for name, text in files.items():
             (stage / name).write_text(text)
         compile_code_object(files[generated.source_name], stage / library)
-        (stage / weights_name).write_bytes(weights)
+        weights.write_to(stage / weights_name)
         manifest = {
             "version": MANIFEST_VERSION,
             "python_abi": sysconfig.get_config_var("SOABI"),

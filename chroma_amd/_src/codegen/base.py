@@ -16,7 +16,10 @@ from __future__ import annotations
 import hashlib
 import itertools
 import math
+import shutil
+import tempfile
 from dataclasses import dataclass
+from pathlib import Path
 from typing import Dict, List, Optional, Sequence, Tuple
 
 import torch
@@ -24,6 +27,54 @@ import torch
 from chroma_amd._src.memory import Allocation, plan_memory
 from chroma_amd._src.spec import Stats, TensorSpec, nbytes
 from chroma_amd._src.value import ITEMSIZE, Shape, Value, View, contiguous_strides
+
+
+class WeightBlob:
+    """The constant blob: appended in 64-byte aligned pieces, hashed as it grows, spilled to a temporary
+    file once it exceeds ``spill_bytes`` so that multi-gigabyte models never need a host copy of their
+    size in memory."""
+
+    def __init__(self, spill_bytes: int = 1 << 30) -> None:
+        self._memory = bytearray()
+        self._file = None
+        self._size = 0
+        self._digest = hashlib.sha256()
+        self._spill_bytes = spill_bytes
+
+    def __len__(self) -> int:
+        return self._size
+
+    def append(self, data) -> None:
+        view = memoryview(data).cast("B")
+        if self._file is None and self._size + len(view) > self._spill_bytes:
+            self._file = tempfile.NamedTemporaryFile(prefix="chroma-weights-", suffix=".bin")
+            self._file.write(self._memory)
+            self._memory = bytearray()
+        if self._file is None:
+            self._memory += view
+        else:
+            self._file.write(view)
+        self._digest.update(view)
+        self._size += len(view)
+
+    def pad(self, alignment: int) -> None:
+        self.append(bytes(-self._size % alignment))
+
+    def hexdigest(self) -> str:
+        return self._digest.copy().hexdigest()
+
+    def write_to(self, path: Path) -> None:
+        if self._file is None:
+            Path(path).write_bytes(self._memory)
+            return
+        self._file.flush()
+        shutil.copyfile(self._file.name, path)
+
+    def __bytes__(self) -> bytes:
+        if self._file is None:
+            return bytes(self._memory)
+        self._file.flush()
+        return Path(self._file.name).read_bytes()
 
 
 @dataclass
@@ -34,14 +85,15 @@ class GeneratedCode:
     stats: Stats
     inputs: List[TensorSpec]
     outputs: List[TensorSpec]
-    weights: bytes
+    weights: WeightBlob
 
 
-def tensor_bytes(tensor: torch.Tensor) -> bytes:
+def tensor_bytes(tensor: torch.Tensor) -> memoryview:
+    """The tensor's bytes without a copy when it is already contiguous (bfloat16 as its bit patterns)."""
     tensor = tensor.detach().contiguous()
     if tensor.dtype == torch.bfloat16:
-        return tensor.view(torch.uint16).numpy().tobytes()
-    return tensor.numpy().tobytes()
+        tensor = tensor.view(torch.uint16)
+    return memoryview(tensor.numpy().reshape(-1)).cast("B")
 
 
 class Codegen:
@@ -50,7 +102,7 @@ class Codegen:
     def __init__(self) -> None:
         self.materialized: Dict[str, Value] = {}
         self.allocations: Dict[str, Allocation] = {}
-        self.weights = bytearray()
+        self.weights = WeightBlob()
         self.weight_cache: Dict[Tuple[torch.dtype, Shape, bytes], Value] = {}
         self.output_buffers: Dict[str, int] = {}
         self.counter = itertools.count()
@@ -70,8 +122,8 @@ class Codegen:
         if cached is not None:
             return cached
         offset = len(self.weights)
-        self.weights += data
-        self.weights += bytes(-len(self.weights) % 64)
+        self.weights.append(data)
+        self.weights.pad(64)
         value = self.extern(tensor, "weight", offset)
         self.weight_cache[key] = value
         return value

@@ -1112,4 +1112,4 @@ class HIPCodegen(Codegen):
         )
         source = "#include <chroma_hip/kernels.h>\n\n" + "\n\n".join(self.kernel_sources) + "\n"
         plan = "\n".join(lines) + "\n"
-        return GeneratedCode({"model.hip": source, "model.plan": plan}, "model.hip", [], stats, inputs, outputs, bytes(self.weights))
+        return GeneratedCode({"model.hip": source, "model.plan": plan}, "model.hip", [], stats, inputs, outputs, self.weights)

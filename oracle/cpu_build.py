@@ -125,5 +125,5 @@ def build_cpu(generated: GeneratedCode, output: os.PathLike, include_root: Path 
     if not library.exists():
         compile_library(source, library, generated.flags, include_root)
     weights = directory / "weights.bin"
-    weights.write_bytes(generated.weights)
+    generated.weights.write_to(weights)
     return OracleProgram(library, weights, generated.inputs, generated.outputs, generated.stats)

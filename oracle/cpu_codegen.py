@@ -342,7 +342,7 @@ class CPUCodegen(Codegen):
         stats = dict(stats, expert_contractions=self.expert_contractions, backend="cpu", math_library="cblas" if self.blas else "portable")
         body = "\n".join(self.render(line) for line in self.lines)
         source = TEMPLATE.format(weight_bytes=stats["weight_bytes"], workspace_bytes=stats["workspace_bytes"], body=body)
-        return GeneratedCode({"model.cc": source}, "model.cc", flags, stats, inputs, outputs, bytes(self.weights))
+        return GeneratedCode({"model.cc": source}, "model.cc", flags, stats, inputs, outputs, self.weights)
 
 
 # C ABI around the generated program; the oracle runner binds it with ctypes.

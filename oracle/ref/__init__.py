@@ -140,7 +140,7 @@ def build_reference_fixtures(force: bool = False) -> bool:
             stage = Path(stage)
             (stage / "model.cc").write_text(generated.files["model.cc"])
             compile_library(stage / "model.cc", stage / "model.so", generated.flags, REFERENCE_HEADERS)
-            (stage / "weights.bin").write_bytes(generated.weights)
+            generated.weights.write_to(stage / "weights.bin")
             (stage / "spec.json").write_text(json.dumps({"inputs": generated.inputs, "outputs": generated.outputs, "stats": generated.stats}))
             if target.exists():
                 shutil.rmtree(target)
