@@ -21,7 +21,7 @@ from __future__ import annotations
 import hashlib
 import math
 from dataclasses import dataclass, field
-from typing import Callable, Dict, List, Optional, Sequence, Tuple, Union
+from typing import Callable, Dict, Iterator, List, Optional, Sequence, Tuple, Union
 
 import torch
 
@@ -37,18 +37,21 @@ MAX_DEPTH = 24
 MAX_SOURCES = 24
 MAP_THREADS = 256
 MAX_GRID = 16384
+# Elementwise (map and concatenation) kernels launch one thread per vector up to this many workgroups,
+# so no thread walks a grid-stride loop and every load of the launch can be in flight at once.
+MAP_GRID = 1 << 20
 # Row kernels: threads per row for rows of at least 2048 elements (smaller rows use one wave), the most
 # elements a thread keeps in registers for a single-pass row, and whether results that nothing in the
 # same kernel reads again are written with non-temporal (streaming) stores.
 ROW_THREADS = 256
 ROW_RESIDENT = 32
 STREAMING_STORES = True
-STREAMING_BYTES = 64 << 20
+STREAMING_BYTES = 64 << 20  # smaller operands and results may stay in L2 / the last-level cache
 FUSED_CONCAT_ELEMENTS = 1 << 16  # smaller concatenations are fused into their consumers
 DEFERRED_ELEMENTS = 1 << 16  # smaller expressions the front end asks to store stay fused instead
 REUSED_EVALUATIONS = 1 << 18  # a contraction operand is stored when (elements x reuse) reaches this
 MATRIX_MIN_WORK = 1 << 18  # smaller batched products stay on the generic contraction kernel
-GROUPED_SLOTS = 64  # from this many (token, expert) slots on, expert products are grouped by expert  # below this a result may stay in the 4 MiB-per-XCD L2 for its consumer
+GROUPED_SLOTS = 64  # from this many (token, expert) slots on, expert products are grouped by expert
 
 UNARY_OPS = {
     "reciprocal": "reciprocal",
@@ -352,6 +355,7 @@ class HIPCodegen(Codegen):
         lanes = choose_lanes(shape[-1], value.dtype)
         k = Kernel(lanes)
         k.streaming = STREAMING_STORES and count * ITEMSIZE[value.dtype] >= STREAMING_BYTES
+        k.streaming_loads = STREAMING_BYTES if k.streaming else 0
         slot = k.slot(target or out.name, value.dtype, writable=True, extent=self.extents[target or out.name])
         vectors = count // lanes
         wide = vectors > 2**31 - 1
@@ -365,7 +369,7 @@ class HIPCodegen(Codegen):
                 coords[-1] = Aff.of(k.vector_atom(f"({coords[-1].code()}) * {lanes}u", shape[-1] - 1))
             node = self.read(k, value, coords if value.shape else coords[:0])
             k.store(slot, value.dtype, Kernel.flatten(coords, shape), node)
-        grid = max(1, min(-(-vectors // MAP_THREADS), MAX_GRID))
+        grid = max(1, min(-(-vectors // MAP_THREADS), MAP_GRID))
         self.launch(k, grid, MAP_THREADS, [value], kind="map")
 
     # ==================================================================================== outputs
@@ -424,7 +428,7 @@ class HIPCodegen(Codegen):
                 k.indent -= 1
                 start = end
             k.line("}")
-        grid = max(1, min(-(-vectors // MAP_THREADS), MAX_GRID))
+        grid = max(1, min(-(-vectors // MAP_THREADS), MAP_GRID))
         self.launch(k, grid, MAP_THREADS, values, kind="concat")
         return out
 
@@ -487,6 +491,7 @@ class HIPCodegen(Codegen):
         waves = threads // 64
         k = Kernel(lanes)
         k.streaming = STREAMING_STORES and math.prod(shape) * ITEMSIZE[out.dtype] >= STREAMING_BYTES
+        k.streaming_loads = STREAMING_BYTES if k.streaming else 0
         slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
         row_atom = k.atom("blockIdx.x", rows - 1, prefix="r")
         row = Aff.of(row_atom)
@@ -507,6 +512,8 @@ class HIPCodegen(Codegen):
         if resident:
             k.line(f"float vals[{chunks}][{lanes}];")
             k.line(f"float peak = {neg_inf};")
+            if not ragged:
+                k.load_replay = self._hoist_loads(k, chunks, lambda: lane_names(element(Aff.of(k.vector_atom(f"c * {step}u + threadIdx.x * {lanes}u", width - 1)))))
             k.line("#pragma unroll")
             with k.block(f"for (uint32_t c = 0; c < {chunks}u; ++c) {{"):
                 j = Aff.of(k.vector_atom(f"c * {step}u + threadIdx.x * {lanes}u", width - 1))
@@ -522,6 +529,7 @@ class HIPCodegen(Codegen):
                     k.line("} else {")
                     k.line("    " + " ".join(f"vals[c][{lane}] = {neg_inf};" for lane in range(lanes)))
                     k.line("}")
+            k.load_replay = None
             k.line(f"peak = chroma::block_max<{waves}>(peak, scratch);")
             k.line("float total = 0.0f;")
             k.line("#pragma unroll")
@@ -559,6 +567,28 @@ class HIPCodegen(Codegen):
                 result = self._lane_values(k, [f"chroma::fast_exp({name} - row_peak) * inverse" for name in names])
                 k.store(slot, out.dtype, out_address(j), result)
         self.launch(k, rows, threads, [x], kind="softmax_rows", prologue=[f"__shared__ float scratch[{max(waves, 1)}];"])
+
+    @staticmethod
+    def _hoist_loads(k: Kernel, chunks: int, body: Callable[[], object]) -> Optional[Iterator[str]]:
+        """Issue every chunk's vector loads before any arithmetic: ``body`` (one chunk of a row, indexed by
+        ``c``) is emitted once in a loop that keeps its vector loads in per-chunk register arrays (the
+        arithmetic it also emits has no use and is dropped by the compiler). Returns the replay that makes
+        the real pass read those arrays, or None (nothing emitted) when the body has side effects or
+        no vector loads."""
+        mark, uses_error = len(k.lines), k.uses_error
+        k.load_log = []
+        k.line("#pragma unroll")
+        with k.block(f"for (uint32_t {k.load_index} = 0; {k.load_index} < {chunks}u; ++{k.load_index}) {{"):
+            body()
+        log, k.load_log = k.load_log, None
+        if not log or k.uses_error != uses_error:
+            del k.lines[mark:]
+            k.uses_error = uses_error
+            return None
+        k.lines[mark:mark] = ["    " * k.indent + f"{vtype} {array}[{chunks}];" for array, vtype in log]
+        # Keep the instruction scheduler from sinking the loads back to their uses.
+        k.line("__builtin_amdgcn_sched_barrier(0);")
+        return iter([array for array, _ in log])
 
     def _lane_values(self, k: Kernel, codes: Sequence[str]) -> tuple:
         """A varying node whose lane l is the C expression ``codes[l]`` (declared now)."""
@@ -926,7 +956,8 @@ class HIPCodegen(Codegen):
             if any(value.shape[label.index(letter)] != sizes[letter] for letter in (row, column, inner) if letter in label):
                 return None
             if not value.stored:
-                value = self.store(value)
+                # A strided view (a GQA expand, a head slice) is read in place through its strides.
+                value = self.materialize(value) if value.view is not None and value.view.base is not None else self.store(value)
             strides = dict(zip(label, value.view.strides))
             for letter, size in zip(label, value.shape):
                 if size == 1:

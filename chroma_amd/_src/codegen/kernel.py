@@ -182,6 +182,15 @@ class Kernel:
         self.definitions: Dict[str, Tuple[str, "Aff", int]] = {}  # opaque atom -> (op, operand, constant)
         self.uses_error = False
         self.streaming = False  # vector float stores bypass the caches (results read by later kernels only)
+        # Vector loads from buffers of at least this many bytes bypass the caches too (0: never). Set on
+        # kernels that read each element of their large operands once.
+        self.streaming_loads = 0
+        # Load hoisting for unrolled chunk loops: while ``load_log`` is a list, every vector load is also
+        # kept in ``array[load_index]`` and logged as (array, C type); while ``load_replay`` is set, the
+        # same vector loads (met in the same order) read those arrays instead of memory.
+        self.load_log: Optional[List[Tuple[str, str]]] = None
+        self.load_replay: Optional[Iterator[str]] = None
+        self.load_index = "c"
         self.shared: List[str] = []
 
     # -- parameters ------------------------------------------------------------------------------
@@ -420,15 +429,35 @@ class Kernel:
         if vector is not None and self.lanes > 1 and not is_int(dtype) and self._vector_aligned(aff, vector):
             base = aff.code(0, wide)
             raw = self.fresh("v")
+            itemsize = 4 if dtype == torch.float32 else 2
+            streaming = 0 < self.streaming_loads <= self.extents.get(slot, 0) * itemsize
             if dtype == torch.float32:
                 vtype = {2: "float2", 4: "float4"}[self.lanes]
-                self.line(f"const {vtype} {raw} = *reinterpret_cast<const {vtype}*>({slot} + {base});")
+                if streaming:
+                    vtype = f"chroma::{vtype}_nt"
+                    load = f"chroma::load_streaming{self.lanes}({slot} + {base})"
+                else:
+                    load = f"*reinterpret_cast<const {vtype}*>({slot} + {base})"
+            else:
+                vtype = {2: "uint32_t", 4: "uint2"}[self.lanes]
+                if streaming:
+                    vtype = {2: "uint32_t", 4: "chroma::uint2_nt"}[self.lanes]
+                    load = f"chroma::load_streaming_bf16x{self.lanes}({slot} + {base})"
+                else:
+                    load = f"*reinterpret_cast<const {vtype}*>({slot} + {base})"
+            if self.load_replay is not None:
+                self.line(f"const {vtype} {raw} = {next(self.load_replay)}[{self.load_index}];")
+            else:
+                self.line(f"const {vtype} {raw} = {load};")
+                if self.load_log is not None:
+                    array = self.fresh("pre")
+                    self.load_log.append((array, vtype))
+                    self.line(f"{array}[{self.load_index}] = {raw};")
+            if dtype == torch.float32:
                 fields = "xyzw"
                 for lane, name in enumerate(names):
                     self.line(f"const float {name} = {raw}.{fields[lane]};")
             else:
-                vtype = {2: "uint32_t", 4: "uint2"}[self.lanes]
-                self.line(f"const {vtype} {raw} = *reinterpret_cast<const {vtype}*>({slot} + {base});")
                 words = [f"{raw}"] if self.lanes == 2 else [f"{raw}.x", f"{raw}.y"]
                 for lane, name in enumerate(names):
                     word = words[lane // 2]

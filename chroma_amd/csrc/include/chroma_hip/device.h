@@ -83,6 +83,26 @@ __device__ __forceinline__ void store_streaming2(float* p, float a, float b) {
     __builtin_nontemporal_store(float2_nt{a, b}, reinterpret_cast<float2_nt*>(p));
 }
 
+// Streaming (non-temporal) vector loads for operands a kernel reads once: they are not kept in L2 or the
+// last-level cache, which leaves those to the data that is reused.
+typedef unsigned int uint2_nt __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float4_nt load_streaming4(const float* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const float4_nt*>(p));
+}
+
+__device__ __forceinline__ float2_nt load_streaming2(const float* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const float2_nt*>(p));
+}
+
+__device__ __forceinline__ uint2_nt load_streaming_bf16x4(const uint16_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint2_nt*>(p));
+}
+
+__device__ __forceinline__ uint32_t load_streaming_bf16x2(const uint16_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+}
+
 // ---------------------------------------------------------------------------------------------
 // Wave64 reductions (butterfly over all 64 lanes; every lane receives the result).
 __device__ __forceinline__ float wave_sum(float v) {
