@@ -35,6 +35,7 @@ METRIC = "dev-model 8-tok fwd ms; 256-KV decode ms; fused-kernel HBM GB/s"
 C2_SHAPE = (16384, 8192)
 C2_BYTES = 3 * C2_SHAPE[0] * C2_SHAPE[1] * 4
 HBM_PEAK_GBS = 8000.0
+BF16_MFMA_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = ROOT / "profiles" / "c2_fused_softmax_traffic.txt"
 
 
@@ -239,6 +240,98 @@ def bench_decode(work: Path, steps: int) -> dict:
     return results
 
 
+C5_CONTEXT, C5_PREFILL = 4096, 2048
+
+
+def c5_flops(config, tokens: int, context: int) -> dict:
+    """Multiply-add work (2 flops each) of one pass of ``export_cached(m, context, tokens)``, per kind of
+    product, as the graph computes it (every score over the whole padded cache; one row unembedded)."""
+    d, hd, heads, kv = config.hidden_size, config.head_dim, config.num_attention_heads, config.num_key_value_heads
+    inter, top, layers = config.intermediate_size, config.experts_per_token, config.num_hidden_layers
+    keys = context + tokens
+    per_layer = {
+        "qkv": 2 * tokens * d * hd * (heads + 2 * kv),
+        "out": 2 * tokens * hd * heads * d,
+        "router": 2 * tokens * d * config.num_experts,
+        "experts_up": 2 * tokens * top * 2 * inter * d,
+        "experts_down": 2 * tokens * top * d * inter,
+        "scores": 2 * heads * tokens * keys * hd,
+        "attend": 2 * heads * tokens * keys * hd,
+    }
+    flops = {name: value * layers for name, value in per_layer.items()}
+    flops["unembedding"] = 2 * d * config.vocab_size
+    flops["total"] = sum(flops.values())
+    return flops
+
+
+def c5_decode_bytes(config, context: int) -> int:
+    """HBM bytes one decode step must read at least: every dense weight, the four selected experts of
+    every layer, the K/V cache, the unembedding, in bfloat16 (norm scales and biases ignored)."""
+    d, hd, heads, kv = config.hidden_size, config.head_dim, config.num_attention_heads, config.num_key_value_heads
+    inter, top = config.intermediate_size, config.experts_per_token
+    per_layer = d * hd * (heads + 2 * kv) + hd * heads * d + d * config.num_experts + top * (2 * inter * d + d * inter)
+    cache = 2 * context * kv * hd
+    return 2 * (config.num_hidden_layers * (per_layer + cache) + d * config.vocab_size)
+
+
+def bench_c5(work: Path, steps: int) -> dict:
+    """C5: the GPT-OSS-20B-shaped bfloat16 model (24 layers, hidden 2880, 64/8 heads of 64, 32 experts
+    top-4, vocabulary 201,088; weights N(0, 0.02) seed 2 drawn on the GPU), a 2048-token prefill through
+    ``export_cached(m, 4096, 2048)`` and single-token steps through ``export_cached(m, 4096, 1)``. Device
+    times run on device-resident inputs; the ``Decoder`` times are end to end (host cache and masks)."""
+    import numpy as np
+    import torch
+
+    import chroma_amd
+    from chroma_amd import Decoder
+    from chroma_amd.models.cached import export_cached
+    from chroma_amd.models.dev import make_gpt_oss_20b
+    from chroma_amd.models.variants import gpt_oss_20b
+
+    started = time.perf_counter()
+    model = make_gpt_oss_20b(2, generator_device="cuda")
+    torch.cuda.empty_cache()
+    log(f"C5 weights drawn in {time.perf_counter() - started:.1f} s")
+    programs = {}
+    for name, steps_ in (("prefill", C5_PREFILL), ("decode", 1)):
+        start = time.perf_counter()
+        programs[name] = chroma_amd.compile(export_cached(model, C5_CONTEXT, steps_), work / f"c5_{name}")
+        log(f"C5 {name} compiled and loaded in {time.perf_counter() - start:.1f} s ({programs[name].stats['launches']} launches)")
+    del model
+    tokens = torch.randint(0, 201088, (C5_PREFILL + steps,), generator=torch.Generator().manual_seed(2)).numpy()
+    result = {"workload": "GPT-OSS-20B-shaped bf16 MoE (24 layers, hidden 2880, 64/8 heads of 64, 32 experts top-4, vocab 201088), "
+              "weights N(0,0.02) seed 2; 2048-token prefill then decode, cache 4096 positions",
+              "weight_bytes": programs["prefill"].stats["weight_bytes"]}
+    flops = c5_flops(gpt_oss_20b, C5_PREFILL, C5_CONTEXT)
+    with Decoder(programs["prefill"], programs["decode"], sliding_window=gpt_oss_20b.sliding_window) as decoder:
+        start = time.perf_counter()
+        logits = decoder.append(tokens[:C5_PREFILL])
+        result["prefill_decoder_ms"] = round((time.perf_counter() - start) * 1e3, 3)
+        if not np.isfinite((logits.view(np.uint16).astype(np.uint32) << 16).view(np.float32)).all():
+            raise RuntimeError("C5 prefill logits are not finite")
+        samples = []
+        for i in range(C5_PREFILL, C5_PREFILL + steps):
+            start = time.perf_counter()
+            decoder.append(tokens[i : i + 1])
+            samples.append((time.perf_counter() - start) * 1e3)
+        result["decode_decoder_ms"] = round(statistics.median(samples), 3)
+        result["decode_cache_on_device"] = decoder.stats["cache_on_device"]
+        # Device-only times: the plans re-run on what their staging regions hold after the Decoder calls.
+        for name, runs in (("prefill", 5), ("decode", 20)):
+            native = programs[name].native
+            native.execute(2)
+            device_ms = native.execute(runs, timed=True) / runs
+            result[f"{name}_device_ms"] = round(device_ms, 4)
+    result["prefill_flops"] = flops["total"]
+    result["prefill_tflops"] = round(flops["total"] / (result["prefill_device_ms"] * 1e-3) / 1e12, 1)
+    result["prefill_mfma_frac"] = round(result["prefill_tflops"] / BF16_MFMA_PEAK_TFLOPS, 4)
+    decode_bytes = c5_decode_bytes(gpt_oss_20b, C5_CONTEXT)
+    result["decode_algorithmic_bytes"] = decode_bytes
+    result["decode_gbs"] = round(decode_bytes / (result["decode_device_ms"] * 1e-3) / 1e9, 1)
+    result["decode_hbm_frac"] = round(result["decode_gbs"] / HBM_PEAK_GBS, 4)
+    return result
+
+
 def counters(work: Path) -> None:
     """For rocprofv3 --pmc: three launches of the C2 kernel and of a plain copy kernel of known size
     (``x * 1.0`` over the same [16384, 8192] fp32 input: 512 MiB read, 512 MiB written), which calibrates
@@ -277,6 +370,8 @@ def main() -> None:
     parser.add_argument("--no-extras", action="store_true", help="skip the dev-model forward and decode measurements")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--counters", action="store_true", help="only run the C2 and copy kernels (for rocprofv3 --pmc)")
+    parser.add_argument("--c5", action="store_true", help="also measure the GPT-OSS-20B-shaped bf16 model (minutes: 42 GB of weights)")
+    parser.add_argument("--c5-only", action="store_true", help="only measure the GPT-OSS-20B-shaped model")
     args = parser.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the hip backend is single-device (every GPU box here has one GPU)", file=sys.stderr)
@@ -286,6 +381,9 @@ def main() -> None:
         work = Path(directory)
         if args.counters:
             counters(work)
+            return
+        if args.c5_only:
+            print(json.dumps({"c5": bench_c5(work, 16)}), flush=True)
             return
         c2 = bench_c2(args, work)
         log(f"C2 {c2['value']:.1f} GB/s wall, kernel {c2['kernel_ms']:.4f} ms ({c2['roofline']['achieved']:.1f} GB/s)")
@@ -315,6 +413,8 @@ def main() -> None:
             log(f"dev forward {line['dev_forward']['hip_fresh']['median_ms']} ms (oracle {line['dev_forward']['cpu_oracle']['median_ms']} ms)")
             line["decode"] = bench_decode(work, 32)
             log(f"decode step {line['decode']['hip']['decode_step']['median_ms']} ms")
+        if args.c5:
+            line["c5"] = bench_c5(work, 16)
         print(json.dumps(line), flush=True)
 
 

@@ -7,7 +7,7 @@ the artifact it replaces are deleted afterwards. The ``nvcc`` branch (build.py:2
 prebuilt ``libchroma_hip.so`` runs it.
 
 Artifact contents: ``model.json`` (manifest version 2), ``_chroma_<id>.hsaco`` (code object),
-``weights-<sha256[:20]>.bin``, ``model.plan`` (launch plan read by the runtime) and the generated
+``weights-<XXH3-128 of the blob [:20]>.bin``, ``model.plan`` (launch plan read by the runtime) and the generated
 ``model.hip``.
 """
 
@@ -23,7 +23,7 @@ import sysconfig
 import tempfile
 import uuid
 from pathlib import Path
-from typing import List, Optional, Set
+from typing import Dict, List, Optional, Set
 
 from chroma_amd._src.codegen.base import GeneratedCode
 from chroma_amd._src.native import DEVICE_INCLUDE
@@ -97,6 +97,23 @@ def _artifact_files(directory: Path) -> Set[str]:
     return {name for name in names if isinstance(name, str) and name == Path(name).name}
 
 
+# Weights files this process has published, by blob digest: a later artifact with the same blob (the
+# prefill and decode graphs of one model) hard-links the file instead of writing gigabytes again.
+_published_weights: Dict[str, Path] = {}
+
+
+def _write_weights(weights, digest: str, destination: Path) -> None:
+    existing = _published_weights.get(digest)
+    if existing is not None:
+        try:
+            if existing.stat().st_size == len(weights):
+                os.link(existing, destination)
+                return
+        except OSError:
+            pass
+    weights.write_to(destination)
+
+
 def build(generated: GeneratedCode, output, *, load: bool = True):
     """Write the artifact for ``generated`` into ``output`` and return the loaded ``Program``
     (``load=False`` publishes without touching a GPU and returns the directory)."""
@@ -104,7 +121,8 @@ def build(generated: GeneratedCode, output, *, load: bool = True):
 
     inputs, outputs, weights = generated.inputs, generated.outputs, generated.weights
     library = f"_chroma_{uuid.uuid4().hex}.hsaco"
-    weights_name = f"weights-{weights.hexdigest()[:20]}.bin"
+    digest = weights.hexdigest()
+    weights_name = f"weights-{digest[:20]}.bin"
     output = Path(output).resolve()
     output.mkdir(parents=True, exist_ok=True)
     stale = _artifact_files(output)
@@ -118,7 +136,7 @@ def build(generated: GeneratedCode, output, *, load: bool = True):
         for name, text in files.items():
             (stage / name).write_text(text)
         compile_code_object(files[generated.source_name], stage / library)
-        weights.write_to(stage / weights_name)
+        _write_weights(weights, digest, stage / weights_name)
         manifest = {
             "version": MANIFEST_VERSION,
             "python_abi": sysconfig.get_config_var("SOABI"),
@@ -137,6 +155,7 @@ def build(generated: GeneratedCode, output, *, load: bool = True):
             if model is not None:
                 model.close()
             raise
+    _published_weights[digest] = output / weights_name
     # The loaded program holds its code object and weights on the device, so replaced files can go.
     for name in stale - {library, weights_name}:
         (output / name).unlink(missing_ok=True)

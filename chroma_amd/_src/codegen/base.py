@@ -4,7 +4,7 @@ A backend receives one call per lowered operation (``extern``, ``weight``, ``ele
 and returns ``Value`` objects. The base class owns what is backend-independent, following the reference
 (chroma/_src/codegen/base.py:39-113):
 
-* the weight blob: constants deduplicated by (dtype, shape, sha256 of bytes), each padded to 64 bytes;
+* the weight blob: constants deduplicated by (dtype, shape, bytes), each padded to 64 bytes;
 * arena allocations: sizes rounded up to 64 bytes, lifetimes as inclusive kernel-index ranges that
   ``record_usage`` extends to the kernel that last reads them;
 * output promotion: a temporary that is also a graph output is written straight into the output buffer;
@@ -13,16 +13,15 @@ and returns ``Value`` objects. The base class owns what is backend-independent, 
 
 from __future__ import annotations
 
-import hashlib
 import itertools
 import math
-import shutil
-import tempfile
 from dataclasses import dataclass
 from pathlib import Path
 from typing import Dict, List, Optional, Sequence, Tuple
 
+import numpy as np
 import torch
+import xxhash
 
 from chroma_amd._src.memory import Allocation, plan_memory
 from chroma_amd._src.spec import Stats, TensorSpec, nbytes
@@ -30,51 +29,48 @@ from chroma_amd._src.value import ITEMSIZE, Shape, Value, View, contiguous_strid
 
 
 class WeightBlob:
-    """The constant blob: appended in 64-byte aligned pieces, hashed as it grows, spilled to a temporary
-    file once it exceeds ``spill_bytes`` so that multi-gigabyte models never need a host copy of their
-    size in memory."""
+    """The constant blob as a list of borrowed pieces: each appended buffer is kept by reference (a
+    model's parameters are not copied), hashed once with XXH3-128 as it arrives, and only streamed out
+    when the artifact is written. A multi-gigabyte model therefore never needs a second host copy of its
+    weights, a temporary file, or a cryptographic hash over every byte.
 
-    def __init__(self, spill_bytes: int = 1 << 30) -> None:
-        self._memory = bytearray()
-        self._file = None
+    ``piece_digest`` (XXH3-128 of one buffer) is the deduplication key of a constant; ``hexdigest`` names
+    the blob's content as the XXH3-128 of the sequence of (piece digest, piece length), so every byte is
+    hashed exactly once."""
+
+    def __init__(self) -> None:
+        self._pieces: List[memoryview] = []
         self._size = 0
-        self._digest = hashlib.sha256()
-        self._spill_bytes = spill_bytes
+        self._digest = xxhash.xxh3_128()
 
     def __len__(self) -> int:
         return self._size
 
-    def append(self, data) -> None:
+    def append(self, data, digest: Optional[bytes] = None) -> None:
         view = memoryview(data).cast("B")
-        if self._file is None and self._size + len(view) > self._spill_bytes:
-            self._file = tempfile.NamedTemporaryFile(prefix="chroma-weights-", suffix=".bin")
-            self._file.write(self._memory)
-            self._memory = bytearray()
-        if self._file is None:
-            self._memory += view
-        else:
-            self._file.write(view)
-        self._digest.update(view)
+        if not len(view):
+            return
+        self._pieces.append(view)
+        self._digest.update((digest or self.piece_digest(view)) + len(view).to_bytes(8, "little"))
         self._size += len(view)
 
     def pad(self, alignment: int) -> None:
         self.append(bytes(-self._size % alignment))
 
     def hexdigest(self) -> str:
-        return self._digest.copy().hexdigest()
+        return self._digest.hexdigest()
+
+    @staticmethod
+    def piece_digest(data: memoryview) -> bytes:
+        return xxhash.xxh3_128(data).digest()
 
     def write_to(self, path: Path) -> None:
-        if self._file is None:
-            Path(path).write_bytes(self._memory)
-            return
-        self._file.flush()
-        shutil.copyfile(self._file.name, path)
+        with open(path, "wb") as stream:
+            for piece in self._pieces:
+                stream.write(piece)
 
     def __bytes__(self) -> bytes:
-        if self._file is None:
-            return bytes(self._memory)
-        self._file.flush()
-        return Path(self._file.name).read_bytes()
+        return b"".join(self._pieces)
 
 
 @dataclass
@@ -104,6 +100,7 @@ class Codegen:
         self.allocations: Dict[str, Allocation] = {}
         self.weights = WeightBlob()
         self.weight_cache: Dict[Tuple[torch.dtype, Shape, bytes], Value] = {}
+        self.weight_data: Dict[Tuple[torch.dtype, Shape, bytes], memoryview] = {}
         self.output_buffers: Dict[str, int] = {}
         self.counter = itertools.count()
         self.kernels = 0
@@ -116,13 +113,17 @@ class Codegen:
         raise NotImplementedError
 
     def weight(self, tensor: torch.Tensor) -> Value:
+        """Store a constant once per distinct (dtype, shape, bytes): the key carries a 128-bit content
+        digest and a hit is confirmed byte for byte before the stored copy is reused."""
         data = tensor_bytes(tensor)
-        key = (tensor.dtype, tuple(tensor.shape), hashlib.sha256(data).digest())
+        digest = WeightBlob.piece_digest(data)
+        key = (tensor.dtype, tuple(tensor.shape), digest)
         cached = self.weight_cache.get(key)
-        if cached is not None:
+        if cached is not None and np.array_equal(np.frombuffer(self.weight_data[key], np.uint8), np.frombuffer(data, np.uint8)):
             return cached
+        self.weight_data[key] = data
         offset = len(self.weights)
-        self.weights.append(data)
+        self.weights.append(data, digest)
         self.weights.pad(64)
         value = self.extern(tensor, "weight", offset)
         self.weight_cache[key] = value

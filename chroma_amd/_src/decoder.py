@@ -7,13 +7,25 @@ return (logits, new K rows, new V rows); the cache is a rolling host buffer inde
 elsewhere; one remaining token runs the decode graph, longer inputs run prefill in chunks; the cache
 commits only after the native call returned, so an interrupted ``append`` leaves the last committed
 state in place.
+
+When both programs are hip programs the cache stays on the device (an extension: the reference keeps
+it on the host and uploads all of it every step, decoder.py:68-76). Each program's own input staging
+regions for the K and V caches hold a device copy; ``owner`` names the program whose copy is the
+committed cache. A step uploads only tokens, positions, masks and the logit row, leaves the new K/V
+rows in the program's output staging, and commits by copying those rows into the owner's cache rows
+on the device; switching between prefill and decode first copies the committed cache across. The
+device copy and the state update form one critical section that defers SIGINT, so an interrupt lands
+either before the commit (state and device cache untouched) or after it.
 """
 
 from __future__ import annotations
 
+import contextlib
+import os
+import signal
 import threading
 from dataclasses import dataclass
-from typing import Any, List, Sequence, Tuple
+from typing import Any, Iterator, List, Optional, Sequence, Tuple
 
 import numpy as np
 
@@ -23,10 +35,27 @@ from chroma_amd._src.program import Program
 
 @dataclass(frozen=True)
 class CacheState:
-    keys: np.ndarray
-    values: np.ndarray
+    keys: Optional[np.ndarray]  # host cache (None when the cache lives on the device)
+    values: Optional[np.ndarray]
     slots: np.ndarray  # absolute position held by each cache row, or -1
     position: int
+    owner: Optional[int] = None  # device mode: the program whose staging holds the committed cache
+
+
+@contextlib.contextmanager
+def _interrupts_deferred() -> Iterator[None]:
+    """Hold SIGINT until the block ends (main thread only; other threads never receive it)."""
+    if threading.current_thread() is not threading.main_thread():
+        yield
+        return
+    pending: List[int] = []
+    previous = signal.signal(signal.SIGINT, lambda number, frame: pending.append(number))
+    try:
+        yield
+    finally:
+        signal.signal(signal.SIGINT, previous)
+        if pending:
+            os.kill(os.getpid(), signal.SIGINT)
 
 
 def _fill_mask(mask: np.ndarray, allowed: np.ndarray) -> None:
@@ -69,25 +98,62 @@ class Decoder:
         self.vocab_size = logits["shape"][1]
         self.device = decode.device
         self._window = min(sliding_window or self.context, self.context)
-        self._buffers: List[Tuple[List[np.ndarray], List[np.ndarray]]] = [
+        self._on_device = all(isinstance(model, Program) for model in self._models) and prefill.device == decode.device
+        # Per program: the seven input arrays (the caches are bound at commit time, or stay on the
+        # device) and the host arrays for the new K/V rows (device mode leaves those on the device).
+        self._buffers: List[Tuple[List[Optional[np.ndarray]], List[Optional[np.ndarray]]]] = [
             (
-                [np.empty(spec["shape"], dtype=numpy_dtype(spec["dtype"])) for spec in model.inputs],
-                [np.empty(spec["shape"], dtype=numpy_dtype(spec["dtype"])) for spec in model.outputs[1:]],
+                [None if i in (2, 3) else np.empty(spec["shape"], dtype=numpy_dtype(spec["dtype"])) for i, spec in enumerate(model.inputs)],
+                [None if self._on_device else np.empty(spec["shape"], dtype=numpy_dtype(spec["dtype"])) for spec in model.outputs[1:]],
             )
             for model in self._models
         ]
+        self._row_bytes = int(np.prod(self._shape[2:])) * self._cache_dtype.itemsize
         self._lock = threading.Lock()
         self._closed = False
         self._commit(self._empty())
 
     def _empty(self) -> CacheState:
+        slots = np.full(self.context, -1, dtype=np.int64)
+        if self._on_device:
+            return CacheState(None, None, slots, 0)
         keys = np.zeros(self._shape, dtype=self._cache_dtype)
-        return CacheState(keys, np.zeros_like(keys), np.full(self.context, -1, dtype=np.int64), 0)
+        return CacheState(keys, np.zeros_like(keys), slots, 0)
 
     def _commit(self, state: CacheState) -> None:
         self._state = state
-        for args, _ in self._buffers:
-            args[2], args[3] = state.keys, state.values
+        if not self._on_device:
+            for args, _ in self._buffers:
+                args[2], args[3] = state.keys, state.values
+
+    # ---------------------------------------------------------------------------- device-resident cache
+    def _device_cache(self, which: int, args: List[Any]) -> None:
+        """Make program ``which``'s device copy of the cache the committed cache: upload zeros to a fresh
+        cache, copy from the owner's staging when another program owns it, or leave it (args None)."""
+        owner = self._state.owner
+        if owner is None:
+            zeros = np.zeros(self._shape, dtype=self._cache_dtype)
+            args[2], args[3] = zeros, zeros
+            return
+        args[2] = args[3] = None
+        if owner != which:
+            target, source = self._models[which].native, self._models[owner].native
+            size = int(np.prod(self._shape)) * self._cache_dtype.itemsize
+            for index in (2, 3):
+                target.copy_2d(target.input_pointer(index), size, source.input_pointer(index), size, size, 1)
+
+    def _device_commit(self, which: int, start: int, count: int, steps: int) -> None:
+        """Copy the first ``count`` new K/V rows of program ``which`` (its outputs 1 and 2, [layers, steps,
+        ...]) into its cache inputs (2 and 3, [layers, context, ...]) at rows (start + i) % context."""
+        program = self._models[which].native
+        row, layers = self._row_bytes, self._shape[0]
+        first = start % self.context
+        head = min(count, self.context - first)
+        for output, cache in ((1, 2), (2, 3)):
+            src, dst = program.output_pointer(output), program.input_pointer(cache)
+            program.copy_2d(dst + first * row, self.context * row, src, steps * row, head * row, layers)
+            if count > head:
+                program.copy_2d(dst, self.context * row, src + head * row, steps * row, (count - head) * row, layers)
 
     @property
     def position(self) -> int:
@@ -96,7 +162,8 @@ class Decoder:
     @property
     def stats(self) -> dict:
         return {
-            "cache_bytes": self._state.keys.nbytes + self._state.values.nbytes,
+            "cache_bytes": 2 * int(np.prod(self._shape)) * self._cache_dtype.itemsize,
+            "cache_on_device": self._on_device,
             "prefill": self._models[0].stats,
             "decode": self._models[1].stats,
         }
@@ -139,13 +206,21 @@ class Decoder:
                     _fill_mask(mask, causal & (key_times[None, :] > times[:, None] - window))
                 logit_index[0] = count - 1
                 logits = np.empty((1, self.vocab_size), dtype=self._logit_dtype)
-                self._models[which](*args, out=[logits, *updates])
                 rows = times[:count] % self.context
-                keys, values, slots = state.keys.copy(), state.values.copy(), state.slots.copy()
-                keys[:, rows] = updates[0][:, :count]
-                values[:, rows] = updates[1][:, :count]
+                slots = state.slots.copy()
                 slots[rows] = times[:count]
-                self._commit(CacheState(keys, values, slots, state.position + count))
+                if self._on_device:
+                    self._device_cache(which, args)
+                    self._models[which].run_resident(args, [logits, *updates])
+                    with _interrupts_deferred():
+                        self._device_commit(which, state.position, count, steps)
+                        self._commit(CacheState(None, None, slots, state.position + count, which))
+                else:
+                    self._models[which](*args, out=[logits, *updates])
+                    keys, values = state.keys.copy(), state.values.copy()
+                    keys[:, rows] = updates[0][:, :count]
+                    values[:, rows] = updates[1][:, :count]
+                    self._commit(CacheState(keys, values, slots, state.position + count))
                 offset += count
             return logits
 

@@ -81,6 +81,10 @@ def library() -> ctypes.CDLL:
         lib.chroma_hip_launch_count.argtypes = [c.c_void_p]
         lib.chroma_hip_device_base.argtypes = [c.c_void_p]
         lib.chroma_hip_device_base.restype = c.c_void_p
+        for name in ("chroma_hip_input_pointer", "chroma_hip_output_pointer"):
+            getattr(lib, name).argtypes = [c.c_void_p, c.c_int]
+            getattr(lib, name).restype = c.c_void_p
+        lib.chroma_hip_copy_2d.argtypes = [c.c_void_p, c.c_void_p, c.c_size_t, c.c_void_p, c.c_size_t, c.c_size_t, c.c_size_t, c.c_char_p, c.c_size_t]
         _library = lib
         return lib
 
@@ -97,6 +101,9 @@ EXPORTED = (
     "chroma_hip_set_graph",
     "chroma_hip_launch_count",
     "chroma_hip_device_base",
+    "chroma_hip_input_pointer",
+    "chroma_hip_output_pointer",
+    "chroma_hip_copy_2d",
 )
 
 

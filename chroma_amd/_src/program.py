@@ -51,16 +51,22 @@ class NativeModel:
         self.device = self._lib.chroma_hip_device_name(handle).decode()
         self.signature = self._lib.chroma_hip_signature(handle).decode()
 
-    def run(self, inputs: List[np.ndarray], outputs: List[np.ndarray]) -> None:
+    def run(self, inputs: List[np.ndarray], outputs: List[np.ndarray], *, resident: bool = False) -> None:
+        """The extension's ``Model.run``. With ``resident`` an input given as None keeps what its device
+        staging region holds and an output given as None stays on the device."""
         if not isinstance(inputs, list) or not isinstance(outputs, list):
             raise TypeError("run takes two lists of arrays")
         if len(inputs) != len(self._inputs) or len(outputs) != len(self._outputs):
             raise ValueError("wrong number of arrays")
         regions: List[Tuple[int, int]] = []
         for value, spec in zip(inputs, self._inputs):
+            if value is None and resident:
+                continue
             array = _checked(value, spec, False)
             regions.append((array.ctypes.data, array.ctypes.data + array.nbytes))
         for value, spec in zip(outputs, self._outputs):
+            if value is None and resident:
+                continue
             array = _checked(value, spec, True)
             begin, end = array.ctypes.data, array.ctypes.data + array.nbytes
             if any(begin < last and first < end for first, last in regions):
@@ -69,12 +75,23 @@ class NativeModel:
         error = ctypes.create_string_buffer(1024)
         status = self._lib.chroma_hip_run(
             self._handle,
-            native.pointer_array(a.ctypes.data for a in inputs),
-            native.pointer_array(a.ctypes.data for a in outputs),
+            native.pointer_array(None if a is None else a.ctypes.data for a in inputs),
+            native.pointer_array(None if a is None else a.ctypes.data for a in outputs),
             error,
             len(error),
         )
         native.check(status, error)
+
+    def input_pointer(self, index: int) -> int:
+        return int(self._lib.chroma_hip_input_pointer(self._handle, index) or 0)
+
+    def output_pointer(self, index: int) -> int:
+        return int(self._lib.chroma_hip_output_pointer(self._handle, index) or 0)
+
+    def copy_2d(self, dst: int, dst_pitch: int, src: int, src_pitch: int, width: int, height: int) -> None:
+        """Device-to-device copy of ``height`` rows of ``width`` bytes on this program's stream."""
+        error = ctypes.create_string_buffer(1024)
+        native.check(self._lib.chroma_hip_copy_2d(self._handle, dst, dst_pitch, src, src_pitch, width, height, error, len(error)), error)
 
     # Device-resident helpers (benchmarks and tests): upload once, execute many times, download.
     def upload(self, inputs: Sequence[np.ndarray]) -> None:
@@ -179,6 +196,16 @@ class Program:
                 raise RuntimeError("Model is closed")
             self._model.run(arrays, results)
         return results[0] if len(results) == 1 else tuple(results)
+
+    def run_resident(self, inputs: Sequence[Optional[Array]], outputs: Sequence[Optional[Array]]) -> None:
+        """A call that leaves chosen data on the device: an input given as None keeps what the program's
+        device copy of it already holds (an earlier upload or device copy), an output given as None is
+        not downloaded. The KV-cached ``Decoder`` keeps its cache on the device this way."""
+        arrays = [None if value is None else self._array(value) for value in inputs]
+        with self._lock:
+            if self._model is None:
+                raise RuntimeError("Model is closed")
+            self._model.run(arrays, list(outputs), resident=True)
 
     @property
     def native(self) -> NativeModel:

@@ -234,10 +234,12 @@ public:
         }
     }
 
+    // A null input pointer leaves that input's staging region as it is (device-resident data from an
+    // earlier upload or device copy); a null output pointer skips that output's download.
     void upload(const void* const* inputs) {
         DeviceGuard guard(device_);
         for (size_t i = 0; i < plan_.inputs.size(); ++i) {
-            if (plan_.inputs[i].bytes) {
+            if (plan_.inputs[i].bytes && inputs[i]) {
                 check(hipMemcpyAsync(static_cast<char*>(base_) + plan_.inputs[i].offset, inputs[i], plan_.inputs[i].bytes,
                                      hipMemcpyHostToDevice, stream_),
                       "Upload input");
@@ -248,7 +250,7 @@ public:
     void download(void* const* outputs) {
         DeviceGuard guard(device_);
         for (size_t i = 0; i < plan_.outputs.size(); ++i) {
-            if (plan_.outputs[i].bytes) {
+            if (plan_.outputs[i].bytes && outputs[i]) {
                 check(hipMemcpyAsync(outputs[i], static_cast<char*>(base_) + plan_.outputs[i].offset, plan_.outputs[i].bytes,
                                      hipMemcpyDeviceToHost, stream_),
                       "Download output");
@@ -257,6 +259,27 @@ public:
     }
 
     void finish_download() { check(hipStreamSynchronize(stream_), "Download output"); }
+
+    void* input_pointer(size_t index) const {
+        return index < plan_.inputs.size() ? static_cast<char*>(base_) + plan_.inputs[index].offset : nullptr;
+    }
+    void* output_pointer(size_t index) const {
+        return index < plan_.outputs.size() ? static_cast<char*>(base_) + plan_.outputs[index].offset : nullptr;
+    }
+
+    // Device-to-device rectangle copy on this program's stream (``height`` rows of ``width`` bytes),
+    // finished before returning.
+    void copy_2d(void* dst, size_t dst_pitch, const void* src, size_t src_pitch, size_t width, size_t height) {
+        DeviceGuard guard(device_);
+        if (!width || !height) {
+            return;
+        }
+        if (dst_pitch < width || src_pitch < width) {
+            throw std::runtime_error("copy_2d pitch smaller than the row width");
+        }
+        check(hipMemcpy2DAsync(dst, dst_pitch, src, src_pitch, width, height, hipMemcpyDeviceToDevice, stream_), "hipMemcpy2DAsync");
+        check(hipStreamSynchronize(stream_), "Device copy");
+    }
 
     float execute(int iterations, bool timed) {
         DeviceGuard guard(device_);
@@ -437,4 +460,17 @@ __attribute__((visibility("default"))) int chroma_hip_set_graph(void* handle, in
 __attribute__((visibility("default"))) int chroma_hip_launch_count(void* handle) { return program(handle)->launch_count(); }
 
 __attribute__((visibility("default"))) void* chroma_hip_device_base(void* handle) { return program(handle)->base(); }
+
+__attribute__((visibility("default"))) void* chroma_hip_input_pointer(void* handle, int index) {
+    return index < 0 ? nullptr : program(handle)->input_pointer(size_t(index));
+}
+
+__attribute__((visibility("default"))) void* chroma_hip_output_pointer(void* handle, int index) {
+    return index < 0 ? nullptr : program(handle)->output_pointer(size_t(index));
+}
+
+__attribute__((visibility("default"))) int chroma_hip_copy_2d(void* handle, void* dst, size_t dst_pitch, const void* src, size_t src_pitch,
+                                                              size_t width, size_t height, char* error, size_t error_size) {
+    return guarded(error, error_size, [&] { program(handle)->copy_2d(dst, dst_pitch, src, src_pitch, width, height); });
+}
 }

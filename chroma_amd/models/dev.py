@@ -45,3 +45,35 @@ def weights_digest(model: torch.nn.Module) -> str:
         digest.update(name.encode())
         digest.update(value.numpy().tobytes())
     return digest.hexdigest()
+
+
+def make_gpt_oss_20b(seed: int = 2, *, std: float = 0.02, generator_device: str = "cpu", **changes) -> Transformer:
+    """The GPT-OSS-20B-shaped bfloat16 workload with seeded random weights: norm scales 1, biases and
+    sinks 0, every other parameter N(0, ``std``) drawn in ``named_parameters`` order from one generator
+    seeded with ``seed`` on ``generator_device`` ("cpu", or "cuda" to draw 21 billion values in seconds).
+    ``changes`` override configuration fields (a reduced slice keeps the widths and drops layers or
+    experts). The module is built without initialisers, so no float32 copy of the model ever exists."""
+    import dataclasses
+
+    from chroma_amd.models.variants import gpt_oss_20b
+
+    config = dataclasses.replace(gpt_oss_20b, **changes)
+    with torch.device("meta"):
+        model = Transformer(config)
+    model = model.to_empty(device="cpu")
+    generator = torch.Generator(device=generator_device).manual_seed(seed)
+    chunk = 1 << 26
+    with torch.no_grad():
+        for name, parameter in model.named_parameters():
+            if name.endswith(".scale"):
+                parameter.fill_(1.0)
+            elif name.endswith(("bias", ".sinks")):
+                parameter.zero_()
+            else:
+                flat = parameter.view(-1)
+                for start in range(0, flat.numel(), chunk):
+                    piece = flat[start : start + chunk]
+                    drawn = torch.empty(piece.numel(), dtype=torch.float32, device=generator_device)
+                    drawn.normal_(mean=0.0, std=std, generator=generator)
+                    piece.copy_(drawn)
+    return model.eval().requires_grad_(False)

@@ -31,7 +31,10 @@ int chroma_hip_create(const char* artifact_dir, void** handle, char* error, size
 /* One synchronous call: copy every input from host memory, run the plan, copy every output back.
  * Replaces ``ModelProgram::run(const void* const* inputs, void* const* outputs)`` /
  * ``Runner::run`` (chroma/_src/codegen/cuda/codegen.py:29-33, runtime.h:147-173). Input and output
- * pointers are host buffers with exactly the manifest's byte sizes. */
+ * pointers are host buffers with exactly the manifest's byte sizes. A null input pointer (an extension:
+ * the reference has no such case) keeps what that input's device staging region already holds, and a
+ * null output pointer leaves that output on the device; the KV-cached decoder uses both to keep its
+ * cache device-resident. */
 int chroma_hip_run(void* handle, const void* const* inputs, void* const* outputs, char* error, size_t error_size);
 
 /* Device name for ``Program.device`` (the reference's ``Runner::device_name``, runtime.h:182). */
@@ -65,6 +68,18 @@ int chroma_hip_set_graph(void* handle, int enabled);
  * inspect device memory through another API). */
 int chroma_hip_launch_count(void* handle);
 void* chroma_hip_device_base(void* handle);
+
+/* Device addresses of input ``index``'s and output ``index``'s staging regions (null when out of range).
+ * They stay valid until ``chroma_hip_destroy``. */
+void* chroma_hip_input_pointer(void* handle, int index);
+void* chroma_hip_output_pointer(void* handle, int index);
+
+/* Device-to-device copy of ``height`` rows of ``width`` bytes (row pitches ``dst_pitch`` and
+ * ``src_pitch``) on the program's stream, complete on return. Both addresses must lie in device memory
+ * of the program's device, for example staging regions of two programs; the KV-cached decoder commits
+ * new cache rows and hands its cache between its prefill and decode programs with it. */
+int chroma_hip_copy_2d(void* handle, void* dst, size_t dst_pitch, const void* src, size_t src_pitch, size_t width, size_t height,
+                       char* error, size_t error_size);
 
 #ifdef __cplusplus
 }
