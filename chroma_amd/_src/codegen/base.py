@@ -94,6 +94,8 @@ def tensor_bytes(tensor: torch.Tensor) -> memoryview:
 
 class Codegen:
     backend = "abstract"
+    # Graph rewrites (functions of the imported ExportedProgram) this backend wants before lowering.
+    graph_passes: Tuple = ()
 
     def __init__(self) -> None:
         self.materialized: Dict[str, Value] = {}

@@ -26,6 +26,7 @@ from typing import Callable, Dict, Iterator, List, Optional, Sequence, Tuple, Un
 import torch
 
 from chroma_amd._src.codegen.base import Codegen, GeneratedCode
+from chroma_amd._src.graph import fuse_attention
 from chroma_amd._src.codegen.kernel import ZERO, Aff, Atom, Kernel, choose_lanes, ctype_of, float_literal, is_int
 from chroma_amd._src.spec import Stats, TensorSpec, nbytes
 from chroma_amd._src.value import ITEMSIZE, Value, View, contiguous_strides, contraction, matrix_axes
@@ -52,6 +53,8 @@ DEFERRED_ELEMENTS = 1 << 16  # smaller expressions the front end asks to store s
 REUSED_EVALUATIONS = 1 << 18  # a contraction operand is stored when (elements x reuse) reaches this
 MATRIX_MIN_WORK = 1 << 18  # smaller batched products stay on the generic contraction kernel
 GROUPED_SLOTS = 64  # from this many (token, expert) slots on, expert products are grouped by expert
+MATRIX_ATTENTION_TOKENS = 64  # bfloat16 attention over at least this many queries runs on the matrix cores
+SPLIT_KEYS = 256  # keys per workgroup when an attention row's keys are split over workgroups
 
 UNARY_OPS = {
     "reciprocal": "reciprocal",
@@ -94,6 +97,7 @@ def _shape(value_shape: Sequence[int]) -> Tuple[int, ...]:
 
 class HIPCodegen(Codegen):
     backend = "hip"
+    graph_passes = (fuse_attention,)
 
     def __init__(self, *, blas: bool = True) -> None:
         super().__init__()
@@ -113,6 +117,7 @@ class HIPCodegen(Codegen):
         self.tiled_matmuls = 0
         self.skinny_matmuls = 0
         self.mfma_matmuls = 0
+        self.fused_attentions = 0
 
     # ===================================================================================== storage
     def extern(self, tensor: torch.Tensor, kind: str, offset: int) -> Value:
@@ -869,6 +874,185 @@ class HIPCodegen(Codegen):
             k.store(slot, out.dtype, Aff.of(o), self._lane_values(k, ["sum"]))
         self.launch(k, max(1, min(-(-total // 256), MAX_GRID)), 256, [x, weight] + ([bias] if bias is not None else []), kind="linear_scalar")
 
+    # ============================================================================== attention
+    def attention(self, meta, q: Value, k_past: Optional[Value], k_new: Value, v_past: Optional[Value], v_new: Value,
+                  mask: Value, sinks: Value, scale: float) -> Value:
+        """Grouped-query attention with sinks in one launch (the ``_attention`` node that the graph pass
+        substitutes for einsum / scale / mask / cat / softmax / slice / einsum): one workgroup per (query
+        row, key-value head), operands read through generated loaders, so views and fused expressions
+        (the rotary embedding of q and of the new keys) are evaluated in place."""
+        tokens, kv_heads, group, dim = q.shape
+        past = k_past.shape[0] if k_past is not None else 0
+        keys = past + k_new.shape[0]
+        out = self.allocate(tuple(meta.shape), meta.dtype)
+        bf16 = meta.dtype == torch.bfloat16
+        if self.blas and bf16 and dim % 32 == 0 and dim <= 128 and tokens >= MATRIX_ATTENTION_TOKENS:
+            if self._matrix_attention(out, q, k_past, k_new, v_past, v_new, mask, sinks, scale):
+                return out
+        splits = -(-keys // SPLIT_KEYS) if keys > 4 * SPLIT_KEYS and tokens * kv_heads < 64 else 1
+        inputs = [v for v in (q, k_past, k_new, v_past, v_new, mask, sinks) if v is not None]
+        if splits == 1:
+            k, split, _ = self._attention_kernel(out, q, k_past, k_new, v_past, v_new, mask, sinks, None)
+            k.line(f"chroma::attention_rows<0, {dim}, {group}, 256, {str(bf16).lower()}>(0u, {keys}u, {float_literal(scale)}, "
+                   "load_q, load_k, load_v, load_mask, load_sink, store, chroma::AttentionSplit{nullptr, nullptr, 1u, 0u});")
+            self.launch(k, (tokens, kv_heads, 1), 256, inputs, kind="attention")
+        else:
+            # Long key ranges with few (query, head) rows: the keys are split over workgroups (statistics,
+            # then partial p . v with the row's statistics, then the in-order sum of the splits).
+            stats = self.allocate((tokens * kv_heads * splits * group * 2,), torch.float32)
+            partial = self.allocate((tokens * kv_heads * splits * group * dim,), torch.float32)
+            for phase in (1, 2):
+                k, split, _ = self._attention_kernel(out, q, k_past, k_new, v_past, v_new, mask, sinks, (stats, partial, splits))
+                k.line(f"const uint32_t begin = blockIdx.z * {SPLIT_KEYS}u;")
+                k.line(f"const uint32_t end = begin + {SPLIT_KEYS}u < {keys}u ? begin + {SPLIT_KEYS}u : {keys}u;")
+                k.line(f"chroma::attention_rows<{phase}, {dim}, {group}, 256, {str(bf16).lower()}>(begin, end, {float_literal(scale)}, "
+                       f"load_q, load_k, load_v, load_mask, load_sink, store, {split});")
+                self.launch(k, (tokens, kv_heads, splits), 256, inputs + [stats] + ([partial] if phase == 2 else []), kind=f"attention_split{phase}")
+            k, _, row = self._attention_kernel(out, q, k_past, k_new, v_past, v_new, mask, sinks, (stats, partial, splits), loaders=False)
+            table = k.slot(partial.name, torch.float32, extent=self.extents[partial.name])
+            k.line(f"chroma::attention_combine<{dim}, {group}>({table} + {row} * {group * dim}u, {splits}u, store);")
+            self.launch(k, (tokens, kv_heads, 1), 256, [partial], kind="attention_combine")
+        self.fused_attentions += 1
+        return out
+
+    def _attention_kernel(self, out, q, k_past, k_new, v_past, v_new, mask, sinks, split, loaders: bool = True) -> Tuple[Kernel, str, str]:
+        """A kernel over (query row, key/value head) with the attention loaders and the result store
+        declared as lambdas (operands read through generated code, so views and fused expressions are
+        evaluated in place); returns it with the C expression of its ``AttentionSplit`` and the C
+        expression of its first split row in the split scratch."""
+        tokens, kv_heads, group, dim = q.shape
+        past = k_past.shape[0] if k_past is not None else 0
+        keys = past + k_new.shape[0]
+        k = Kernel(1)
+        t = Aff.of(k.atom("blockIdx.x", tokens - 1, prefix="t"))
+        h = Aff.of(k.atom("blockIdx.y", kv_heads - 1, prefix="h"))
+        slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        scores_shape = (kv_heads, group, tokens, keys)
+
+        def loader(name: str, params: Sequence[Tuple[str, int]], body: Callable[[List[Aff]], Optional[tuple]], split=None) -> None:
+            signature = ", ".join(f"uint32_t {p}" for p, _ in params)
+            with k.block(f"auto {name} = [&]({signature}) -> float {{", "};"):
+                coords = [Aff.of(Atom(p, hi)) for p, hi in params]
+                if split is None:
+                    k.line(f"return {k.emit(body(coords))};")
+                    return
+                bound, first, second = split
+                with k.block(f"if ({params[0][0]} < {bound}u) {{"):
+                    k.line(f"return {k.emit(first(coords))};")
+                k.line(f"return {k.emit(second(coords))};")
+
+        def key_source(past_value: Optional[Value], new_value: Value, name: str) -> None:
+            if past_value is None:
+                loader(name, [("j", keys - 1), ("d", dim - 1)], lambda c: self.read(k, new_value, [c[0], h, c[1]]))
+                return
+            params = [("j", keys - 1), ("d", dim - 1)]
+
+            def first(c):
+                return self.read(k, past_value, [Aff.of(Atom("j", past - 1)), h, c[1]])
+
+            def second(c):
+                shifted = k.derived(c[0], f"({{}}) - {past}u", keys - past - 1)
+                return self.read(k, new_value, [shifted, h, c[1]])
+
+            loader(name, params, None, split=(past, first, second))
+
+        if loaders:
+            loader("load_q", [("g", group - 1), ("d", dim - 1)], lambda c: self.read(k, q, [t, h, c[0], c[1]]))
+            key_source(k_past, k_new, "load_k")
+            key_source(v_past, v_new, "load_v")
+            loader("load_mask", [("j", keys - 1), ("g", group - 1)], lambda c: self.broadcast_read(k, mask, [h, c[1], t, c[0]], scores_shape))
+            loader("load_sink", [("g", group - 1)], lambda c: self.broadcast_read(k, sinks, [h, c[0], t, ZERO], scores_shape[:3] + (1,)))
+        with k.block("auto store = [&](uint32_t g, uint32_t d, float value) {", "};"):
+            g_atom, d_atom = Aff.of(Atom("g", group - 1)), Aff.of(Atom("d", dim - 1))
+            node = self._lane_values(k, ["value"])
+            k.store(slot, out.dtype, Kernel.flatten([t, h, g_atom, d_atom], out.shape), node)
+        if split is None:
+            return k, "", ""
+        stats, partial, splits = split
+        row = f"(size_t({t.code()}) * {kv_heads}u + {h.code()}) * {splits}u"
+        stats_slot = k.slot(stats.name, torch.float32, writable=True, extent=self.extents[stats.name]) if loaders else None
+        partial_slot = k.slot(partial.name, torch.float32, writable=True, extent=self.extents[partial.name]) if loaders else None
+        descriptor = (f"chroma::AttentionSplit{{{stats_slot} + {row} * {group * 2}u, {partial_slot} + {row} * {group * dim}u, "
+                      f"{splits}u, blockIdx.z}}") if loaders else ""
+        return k, descriptor, row
+
+    @staticmethod
+    def _in_place(value: Value) -> Tuple[Optional[Value], Tuple[int, ...]]:
+        """(the stored value or strided view to read in place, or None when ``value`` is an expression that
+        must be stored first; its element strides)."""
+        if value.stored:
+            return value, tuple(value.view.strides)
+        if value.view is not None and value.view.base is not None:
+            return Value(value.name, value.shape, value.dtype, value.deps, stored=True, view=value.view), tuple(value.view.strides)
+        return None, contiguous_strides(value.shape)
+
+    def _operand(self, value: Value, shape: Sequence[int]) -> Tuple[Value, List[int], int]:
+        """(stored value, element strides broadcast to ``shape``, element offset): views are read in place,
+        expressions are stored once."""
+        stored, strides = self._in_place(value)
+        if stored is None:
+            stored = self.store(value)
+        pad = len(shape) - len(value.shape)
+        broadcast = [0] * pad + [0 if size == 1 else stride for size, stride in zip(value.shape, strides)]
+        return stored, broadcast, stored.view.offset if stored.view.base is not None else 0
+
+    def _matrix_attention(self, out, q, k_past, k_new, v_past, v_new, mask, sinks, scale) -> bool:
+        """The long-prefill attention on the matrix cores (``attention_mfma_bf16``); False (nothing
+        emitted) when an operand's layout does not allow 16-byte rows."""
+        tokens, kv_heads, group, dim = q.shape
+        past = k_past.shape[0] if k_past is not None else 0
+        keys = past + k_new.shape[0]
+        scores_shape = (kv_heads, group, tokens, keys)
+        operands = {"q": (q, q.shape), "k_new": (k_new, k_new.shape), "v_new": (v_new, v_new.shape), "mask": (mask, scores_shape),
+                    "sinks": (sinks, scores_shape[:3] + (1,))}
+        if k_past is not None:
+            operands["k_past"], operands["v_past"] = (k_past, k_past.shape), (v_past, v_past.shape)
+        # Check every layout before anything is stored: rows of q, K and V contiguous along the head
+        # dimension with 16-byte aligned starts, unit key stride in the mask, one sink per head.
+        for name, (value, shape) in operands.items():
+            stored, strides = self._in_place(value)
+            pad = len(shape) - len(value.shape)
+            strides = [0] * pad + [0 if size == 1 else stride for size, stride in zip(value.shape, strides)]
+            offset = stored.view.offset if stored is not None and stored.view.base is not None else 0
+            if name in ("q", "k_new", "v_new", "k_past", "v_past") and (strides[-1] != 1 or any(x % 8 for x in strides[:-1]) or offset % 8):
+                return False
+            if (name == "mask" and strides[3] != 1) or (name == "sinks" and strides[2] != 0):
+                return False
+        plan = {name: self._operand(value, shape) for name, (value, shape) in operands.items()}
+        plan.setdefault("k_past", None)
+        plan.setdefault("v_past", None)
+        q_strides, mask_strides, sink_strides = plan["q"][1], plan["mask"][1], plan["sinks"][1]
+        k = Kernel(1)
+        slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+
+        def pointer(name: str) -> str:
+            entry = plan[name]
+            if entry is None:
+                entry = plan[name.replace("past", "new")]
+            value, _, offset = entry
+            root = value.root
+            base = k.slot(root.name, root.dtype, extent=self.extents[root.name])
+            return f"{base} + {offset}u" if offset else base
+
+        kp = plan["k_past"][1] if plan["k_past"] is not None else plan["k_new"][1]
+        vp = plan["v_past"][1] if plan["v_past"] is not None else plan["v_new"][1]
+        kn, vn = plan["k_new"][1], plan["v_new"][1]
+        k.line("chroma::AttentionOperands a;")
+        k.line(f"a.q = {pointer('q')}; a.qt = {q_strides[0]}u; a.qh = {q_strides[1]}u; a.qg = {q_strides[2]}u;")
+        k.line(f"a.k_past = {pointer('k_past')}; a.k_new = {pointer('k_new')}; a.v_past = {pointer('v_past')}; a.v_new = {pointer('v_new')};")
+        k.line(f"a.kpj = {kp[0]}u; a.kph = {kp[1]}u; a.knj = {kn[0]}u; a.knh = {kn[1]}u;")
+        k.line(f"a.vpj = {vp[0]}u; a.vph = {vp[1]}u; a.vnj = {vn[0]}u; a.vnh = {vn[1]}u;")
+        k.line(f"a.mask = {pointer('mask')}; a.mt = {mask_strides[2]}u; a.mh = {mask_strides[0]}u; a.mg = {mask_strides[1]}u;")
+        k.line(f"a.sinks = {pointer('sinks')}; a.sh = {sink_strides[0]}u; a.sg = {sink_strides[1]}u;")
+        k.line(f"a.out = {slot}; a.tokens = {tokens}u; a.past = {past}u; a.keys = {keys}u; a.kv_heads = {kv_heads}u; a.group = {group}u;")
+        k.line(f"a.scale = {float_literal(scale)};")
+        k.line(f"chroma::attention_mfma_bf16<{dim}>(a);")
+        operands = [entry[0] for entry in plan.values() if entry is not None]
+        self.launch(k, (-(-tokens // 64), kv_heads * group, 1), 256, operands, kind="attention_mfma")
+        self.fused_attentions += 1
+        self.mfma_matmuls += 1
+        return True
+
     # ================================================================================= einsum
     def einsum(self, meta, eqn: str, values: Sequence[Value]) -> Value:
         labels, output, sizes, reduction = contraction(eqn, values)
@@ -1138,6 +1322,7 @@ class HIPCodegen(Codegen):
             tiled_matmuls=self.tiled_matmuls,
             skinny_matmuls=self.skinny_matmuls,
             mfma_matmuls=self.mfma_matmuls,
+            fused_attentions=self.fused_attentions,
             unique_kernels=len(self.kernel_sources),
             launches=len(self.launches),
         )

@@ -70,6 +70,8 @@ class Compiler:
     @classmethod
     def from_export(cls, program: Union[ExportedProgram, str, "os.PathLike[str]"], codegen: Codegen) -> "Compiler":
         compiler = cls(prepare(program), codegen)
+        for rewrite in codegen.graph_passes:
+            rewrite(compiler.program)
         placeholders = [node for node in compiler.program.graph.nodes if node.op == "placeholder"]
         for node, spec in zip(placeholders, compiler.program.graph_signature.input_specs):
             if spec.kind.name == "USER_INPUT":

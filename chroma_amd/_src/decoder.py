@@ -44,12 +44,15 @@ class CacheState:
 
 @contextlib.contextmanager
 def _interrupts_deferred() -> Iterator[None]:
-    """Hold SIGINT until the block ends (main thread only; other threads never receive it)."""
-    if threading.current_thread() is not threading.main_thread():
+    """Hold SIGINT until the block ends. Only the main thread receives it, and only a handler installed
+    from Python can be put back afterwards; otherwise (a profiler's or embedder's native handler) the
+    block runs as it is."""
+    previous = signal.getsignal(signal.SIGINT)
+    if threading.current_thread() is not threading.main_thread() or previous is None:
         yield
         return
     pending: List[int] = []
-    previous = signal.signal(signal.SIGINT, lambda number, frame: pending.append(number))
+    signal.signal(signal.SIGINT, lambda number, frame: pending.append(number))
     try:
         yield
     finally:

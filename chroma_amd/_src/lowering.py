@@ -107,6 +107,22 @@ def _rmsnorm(x: torch.Tensor, weight: torch.Tensor, epsilon: float) -> torch.Ten
     return x * torch.rsqrt(x.square().mean(-1, keepdim=True) + epsilon) * weight
 
 
+def _attention(q, k_past, k_new, v_past, v_new, mask, sinks, scale: float) -> torch.Tensor:
+    """Graph target that ``fuse_attention`` substitutes for grouped-query attention with sinks: the same
+    operations in the same order as the chain it replaces (reference chroma/models/gpt_oss.py sdpa and
+    cached.py:38-48), so folding or tracing it gives the chain's result. q [T, KV, G, D]; keys and
+    values [S, KV, D], each given whole (past None) or as past and new rows; mask broadcasts to
+    [KV, G, T, S]; sinks [KV, G, T, 1]."""
+    k = k_new if k_past is None else torch.cat((k_past, k_new))
+    v = v_new if v_past is None else torch.cat((v_past, v_new))
+    group = q.shape[2]
+    k = k[:, :, None, :].expand(-1, -1, group, -1)
+    v = v[:, :, None, :].expand(-1, -1, group, -1)
+    scores = torch.einsum("qhmd,khmd->hmqk", q, k) * scale + mask
+    weights = torch.cat((scores, sinks), dim=-1).softmax(-1)[..., :-1]
+    return torch.einsum("hmqk,khmd->qhmd", weights, v)
+
+
 def _arg(args: Sequence[Any], kwargs: Dict[str, Any], index: int, name: str, default: Any = None) -> Any:
     return args[index] if len(args) > index else kwargs.get(name, default)
 
@@ -208,6 +224,8 @@ def lower(codegen, target: Any, meta: Any, args: Tuple[Any, ...], kwargs: Dict[s
         return args[0][args[1]]
     if target is _rmsnorm:
         return codegen.norm(meta, args[0], args[1], args[2])
+    if target is _attention:
+        return codegen.attention(meta, *args)
     name = str(target)
     family = OPERATIONS.get(name)
 

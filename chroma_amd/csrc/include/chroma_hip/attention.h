@@ -1,0 +1,438 @@
+// Fused grouped-query attention with sinks: the replacement for the reference workload's chain
+//
+//     s   = einsum("qhmd,khmd->hmqk", q, k) * scale + mask          (each step rounded to the storage type)
+//     p   = softmax(cat([s, sink], -1), -1)[..., :-1]                (float statistics, p rounded)
+//     out = einsum("hmqk,khmd->qhmd", p, v)                          (float accumulation, rounded once)
+//
+// (chroma/models/gpt_oss.py sdpa, chroma/models/cached.py:38-48, lowered by the reference into two
+// contractions, two elementwise steps, a concatenation and a softmax: gpu.py:275-298, :390-424) without
+// storing the [heads, queries, keys] scores. Every rounding point of the chain is kept: the scores, the
+// scaled scores and the masked scores are rounded to the storage type, the softmax statistics are float,
+// each probability is exp(x - max) / sum rounded to the storage type before it meets V, and the output
+// sum is float. Only the order of the float sums differs from the reference.
+#pragma once
+
+#include "device.h"
+#include "linear.h"
+
+namespace chroma {
+
+template <bool BF16> __device__ __forceinline__ float storage_round(float x) {
+    if constexpr (BF16) {
+        return round_bf16(x);
+    } else {
+        return x;
+    }
+}
+
+// Online (max, sum of exp) update with -inf handled like the reference's two-pass softmax: a row whose
+// values are all -inf keeps sum 0.
+__device__ __forceinline__ void softmax_stats_add(float& peak, float& total, float x) {
+    const float top = __builtin_fmaxf(peak, x);
+    total = top == -__builtin_inff() ? 0.0f : total * fast_exp(peak - top) + fast_exp(x - top);
+    peak = top;
+}
+
+// Merge the statistics (other_peak, other_total) of another set of values into (peak, total).
+__device__ __forceinline__ void softmax_stats_merge(float& peak, float& total, float other_peak, float other_total) {
+    const float top = __builtin_fmaxf(peak, other_peak);
+    total = top == -__builtin_inff() ? 0.0f
+                                     : (peak == -__builtin_inff() ? 0.0f : total * fast_exp(peak - top)) +
+                                           (other_peak == -__builtin_inff() ? 0.0f : other_total * fast_exp(other_peak - top));
+    peak = top;
+}
+
+// Scratch of the split-key form for one (query row, key/value head): per split the partial statistics
+// [G][2] (max, sum of exp) and the partial sums p . v [G][D].
+struct AttentionSplit {
+    float* stats;
+    float* partial;
+    uint32_t splits, split;
+};
+
+// One workgroup computes one query row t for all G query heads of one key/value head (the caller fixes t
+// and the head inside its loaders) over the keys [begin, end). Loaders: load_q(g, d), load_k(j, d),
+// load_v(j, d), load_mask(j, g), load_sink(g) return floats (storage values widened); store(g, d, value)
+// writes one rounded result.
+//
+// PHASE 0 (whole row): pass 1 computes thread-per-key scores and per-thread online statistics, reduced
+// over the workgroup with the sink logit folded in; pass 2, per chunk of THREADS keys, writes
+// thread-per-key probabilities to LDS, then threads arranged as KL key lanes x DG dimension groups (DS =
+// D / DG consecutive dimensions each) accumulate p * v, and the key lanes are summed at the end.
+// Long rows split their keys over workgroups: PHASE 1 writes each split's statistics (no sink), PHASE 2
+// combines every split's statistics and the sink into the row's, then writes the split's p . v sums;
+// ``attention_combine`` adds the splits in order. Every probability is the row's exp(x - max) / sum,
+// rounded, in all phases.
+template <int PHASE, int D, int G, int THREADS, bool BF16, class LoadQ, class LoadK, class LoadV, class LoadMask, class LoadSink, class Store>
+__device__ __forceinline__ void attention_rows(uint32_t begin, uint32_t end, float scale, LoadQ load_q, LoadK load_k, LoadV load_v,
+                                               LoadMask load_mask, LoadSink load_sink, Store store, AttentionSplit split) {
+    constexpr int WAVES = THREADS / kWave;
+    constexpr int DG = D >= 32 ? 8 : (D >= 8 ? D / 4 : 1);  // dimension groups
+    constexpr int DS = D / DG;                               // dimensions per thread
+    constexpr int KL = THREADS / DG < kWave ? THREADS / DG : kWave;  // key lanes of one group in a wave
+    constexpr int SLABS = THREADS / (DG * KL);               // groups of key lanes summed through LDS
+    static_assert(D % DG == 0 && THREADS % (DG * KL) == 0 && (KL & (KL - 1)) == 0, "attention_rows shape");
+    __shared__ float q_s[G][D];
+    __shared__ float p_s[G][THREADS];
+    __shared__ float wave_peak[WAVES][G], wave_total[WAVES][G];
+    __shared__ float peak_s[G], total_s[G];
+    __shared__ float slab_s[SLABS > 1 ? SLABS : 1][G][D];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid % kWave, wave = tid / kWave;
+    const float neg_inf = -__builtin_inff();
+    for (uint32_t i = tid; i < uint32_t(G * D); i += THREADS) {
+        q_s[i / D][i % D] = load_q(i / D, i % D);
+    }
+    __syncthreads();
+
+    // Masked score of key j for every head: s2[g].
+    auto scores = [&](uint32_t j, float (&s2)[G]) {
+        float kd[D];
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            kd[d] = load_k(j, d);
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float dot = 0.0f;
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                dot += q_s[g][d] * kd[d];
+            }
+            const float s = storage_round<BF16>(dot);
+            const float s1 = storage_round<BF16>(s * scale);
+            s2[g] = storage_round<BF16>(s1 + load_mask(j, g));
+        }
+    };
+
+    // ---- pass 1: statistics (phases 0 and 1)
+    if constexpr (PHASE != 2) {
+        float peak[G], total[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            peak[g] = neg_inf;
+            total[g] = 0.0f;
+        }
+        for (uint32_t j = begin + tid; j < end; j += THREADS) {
+            float s2[G];
+            scores(j, s2);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                softmax_stats_add(peak[g], total[g], s2[g]);
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float top = wave_max(peak[g]);
+            const float sum = wave_sum(peak[g] == neg_inf ? 0.0f : total[g] * fast_exp(peak[g] - top));
+            if (lane == 0) {
+                wave_peak[wave][g] = top;
+                wave_total[wave][g] = sum;
+            }
+        }
+        __syncthreads();
+        if (tid < uint32_t(G)) {
+            float top = neg_inf, sum = 0.0f;
+            for (int w = 0; w < WAVES; ++w) {
+                softmax_stats_merge(top, sum, wave_peak[w][tid], wave_total[w][tid]);
+            }
+            if constexpr (PHASE == 1) {
+                split.stats[(split.split * G + tid) * 2] = top;
+                split.stats[(split.split * G + tid) * 2 + 1] = sum;
+            } else {
+                softmax_stats_add(top, sum, load_sink(tid));
+                peak_s[tid] = top;
+                total_s[tid] = sum;
+            }
+        }
+        if constexpr (PHASE == 1) {
+            return;
+        }
+    } else {
+        if (tid < uint32_t(G)) {
+            float top = neg_inf, sum = 0.0f;
+            for (uint32_t w = 0; w < split.splits; ++w) {
+                softmax_stats_merge(top, sum, split.stats[(w * G + tid) * 2], split.stats[(w * G + tid) * 2 + 1]);
+            }
+            softmax_stats_add(top, sum, load_sink(tid));
+            peak_s[tid] = top;
+            total_s[tid] = sum;
+        }
+    }
+    __syncthreads();
+
+    // ---- pass 2: probabilities and p . v
+    const uint32_t kl = tid % KL, dg = (tid / KL) % DG, slab = tid / (KL * DG);
+    float acc[G][DS];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+        for (int e = 0; e < DS; ++e) {
+            acc[g][e] = 0.0f;
+        }
+    }
+    for (uint32_t base = begin; base < end; base += THREADS) {
+        const uint32_t j = base + tid;
+        if (j < end) {
+            float s2[G];
+            scores(j, s2);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                p_s[g][tid] = storage_round<BF16>(fast_exp(s2[g] - peak_s[g]) / total_s[g]);
+            }
+        }
+        __syncthreads();
+        const uint32_t count = end - base < uint32_t(THREADS) ? end - base : uint32_t(THREADS);
+        for (uint32_t i = slab * KL + kl; i < count; i += KL * SLABS) {
+            float vd[DS];
+#pragma unroll
+            for (int e = 0; e < DS; ++e) {
+                vd[e] = load_v(base + i, dg * DS + e);
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float p = p_s[g][i];
+#pragma unroll
+                for (int e = 0; e < DS; ++e) {
+                    acc[g][e] += p * vd[e];
+                }
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+        for (int e = 0; e < DS; ++e) {
+#pragma unroll
+            for (int offset = KL / 2; offset > 0; offset >>= 1) {
+                acc[g][e] += __shfl_xor(acc[g][e], offset, kWave);
+            }
+        }
+    }
+    // Results: phase 0 stores them, phase 2 writes the split's partial sums.
+    auto emit = [&](uint32_t g, uint32_t d, float value) {
+        if constexpr (PHASE == 2) {
+            split.partial[(size_t(split.split) * G + g) * D + d] = value;
+        } else {
+            store(g, d, value);
+        }
+    };
+    if constexpr (SLABS > 1) {
+        if (kl == 0) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+#pragma unroll
+                for (int e = 0; e < DS; ++e) {
+                    slab_s[slab][g][dg * DS + e] = acc[g][e];
+                }
+            }
+        }
+        __syncthreads();
+        for (uint32_t i = tid; i < uint32_t(G * D); i += THREADS) {
+            float sum = 0.0f;
+            for (int w = 0; w < SLABS; ++w) {
+                sum += slab_s[w][i / D][i % D];
+            }
+            emit(i / D, i % D, sum);
+        }
+    } else if (kl == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+#pragma unroll
+            for (int e = 0; e < DS; ++e) {
+                emit(g, dg * DS + e, acc[g][e]);
+            }
+        }
+    }
+}
+
+// The split-key result: out(g, d) = sum over splits, in split order, of the partial p . v sums.
+template <int D, int G, class Store>
+__device__ __forceinline__ void attention_combine(const float* partial, uint32_t splits, Store store) {
+    for (uint32_t i = threadIdx.x; i < uint32_t(G * D); i += blockDim.x) {
+        float sum = 0.0f;
+        for (uint32_t s = 0; s < splits; ++s) {
+            sum += partial[size_t(s) * G * D + i];
+        }
+        store(i / D, i % D, sum);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Matrix-core attention for long bfloat16 query blocks (the prefill of a cached export): the same
+// computation as ``attention_rows`` with the two contractions on v_mfma_f32_16x16x32_bf16.
+//
+// Workgroup: 4 waves = 64 queries of one head (grid.x: query blocks, grid.y: kv_head * group + g);
+// keys in blocks of 32, staged in LDS (K row-major, V transposed). Each wave computes
+// S^T[32 keys x 16 queries] = K . Q^T as two 16 x 16 tiles (lane l ends with keys 4(l/16)+r and
+// 16+4(l/16)+r of query l%16), so its own accumulators, rounded, become the B operand of
+// O^T[D x 16] = V^T . P^T once the 32 keys are ordered as slot 8a+b -> key (b < 4 ? 4a+b : 16+4a+b-4);
+// the A operand reads V^T in that order. Pass 1 accumulates (max, sum of exp) per query, pass 2
+// recomputes the scores and accumulates p . v. A key block whose mask is -inf for every query of the
+// workgroup is skipped in both passes: its probabilities are exactly 0, so skipping it changes no bit as
+// long as the skipped K/V rows are finite (a NaN there would have poisoned the reference's sum).
+//
+// Operands: q [T, KV, G, D] with strides (qt, qh, qg, 1); keys and values as rows [.., KV, D] with row
+// strides (past rows [0, past), new rows [past, keys)); mask[t, j] at mask + t*mt + kv*mh + g*mg + j;
+// sinks at sinks + kv*sh + g*sg; out [T, KV, G, D] contiguous. Row strides and bases keep 16-byte alignment.
+struct AttentionOperands {
+    const uint16_t* q;
+    uint32_t qt, qh, qg;
+    const uint16_t *k_past, *k_new, *v_past, *v_new;
+    uint32_t kpj, kph, knj, knh, vpj, vph, vnj, vnh;
+    const uint16_t* mask;
+    uint32_t mt, mh, mg;
+    const uint16_t* sinks;
+    uint32_t sh, sg;
+    uint16_t* out;
+    uint32_t tokens, past, keys, kv_heads, group;
+    float scale;
+};
+
+template <int D> __device__ __forceinline__ void attention_mfma_bf16(const AttentionOperands& a) {
+    static_assert(D % 32 == 0 && D <= 128, "head dimension");
+    constexpr int KB = 32, KPAD = D + 8, VPAD = KB + 8;
+    __shared__ __attribute__((aligned(16))) uint16_t k_s[KB * KPAD];
+    __shared__ __attribute__((aligned(16))) uint16_t v_s[D * VPAD];
+    const uint32_t tid = threadIdx.x, lane = tid % 64u, wave = tid / 64u, quad = lane / 16u, col = lane % 16u;
+    const uint32_t head = blockIdx.y, kv = head / a.group, g = head % a.group;
+    const uint32_t block_q0 = blockIdx.x * 64u;
+    const uint32_t query = block_q0 + wave * 16u + col;
+    const bool live = query < a.tokens;
+    const uint32_t qrow = live ? query : a.tokens - 1u;
+
+    bf16x8_t qf[D / 32];
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) {
+        qf[ks] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(a.q + size_t(qrow) * a.qt + kv * a.qh + g * a.qg + ks * 32u + quad * 8u));
+    }
+    const uint16_t* mask_row = a.mask + size_t(qrow) * a.mt + kv * a.mh + g * a.mg;
+    const float neg_inf = -__builtin_inff();
+
+    // The mask values of this lane's 8 scores in key block kb (-inf past the last key or query).
+    auto masks = [&](uint32_t kb, float (&m)[8]) -> bool {
+        bool any = false;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t j = kb * KB + (i < 4 ? quad * 4u + i : 16u + quad * 4u + (i - 4));
+            m[i] = (live && j < a.keys) ? bf16_to_f32(mask_row[j]) : neg_inf;
+            any |= m[i] != neg_inf;
+        }
+        return any;
+    };
+    auto stage = [&](uint32_t kb, bool values) {
+        for (uint32_t c = tid; c < uint32_t(KB * D / 8); c += 256u) {
+            const uint32_t r = c / (D / 8), dc = (c % (D / 8)) * 8u, j = kb * KB + r;
+            uint4 kv_k = uint4{0, 0, 0, 0}, kv_v = uint4{0, 0, 0, 0};
+            if (j < a.keys) {
+                const bool old = j < a.past;
+                const size_t kr = old ? size_t(j) * a.kpj + kv * a.kph : size_t(j - a.past) * a.knj + kv * a.knh;
+                kv_k = *reinterpret_cast<const uint4*>((old ? a.k_past : a.k_new) + kr + dc);
+                if (values) {
+                    const size_t vr = old ? size_t(j) * a.vpj + kv * a.vph : size_t(j - a.past) * a.vnj + kv * a.vnh;
+                    kv_v = *reinterpret_cast<const uint4*>((old ? a.v_past : a.v_new) + vr + dc);
+                }
+            }
+            *reinterpret_cast<uint4*>(&k_s[r * KPAD + dc]) = kv_k;
+            if (values) {
+                const uint16_t* e = reinterpret_cast<const uint16_t*>(&kv_v);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    v_s[(dc + i) * VPAD + r] = e[i];
+                }
+            }
+        }
+    };
+    // Masked scores s2 of this lane's 8 (key, query) pairs.
+    auto scores = [&](const float (&m)[8], float (&s2)[8]) {
+        f32x4_t acc[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) {
+                const bf16x8_t kf = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(&k_s[(t * 16u + col) * KPAD + ks * 32u + quad * 8u]));
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ks], acc[t], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float s = round_bf16(acc[i / 4][i % 4]);
+            const float s1 = round_bf16(s * a.scale);
+            s2[i] = round_bf16(s1 + m[i]);
+        }
+    };
+
+    const uint32_t blocks = (a.keys + KB - 1) / KB;
+    float peak = neg_inf, total = 0.0f;
+    for (uint32_t kb = 0; kb < blocks; ++kb) {
+        float m[8];
+        const bool any = masks(kb, m);
+        if (!__syncthreads_or(any)) {
+            continue;
+        }
+        stage(kb, false);
+        __syncthreads();
+        float s2[8];
+        scores(m, s2);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            softmax_stats_add(peak, total, s2[i]);
+        }
+    }
+    // Combine the four lane groups that share a query, then fold in the sink.
+#pragma unroll
+    for (int offset = 16; offset < 64; offset <<= 1) {
+        const float other_peak = __shfl_xor(peak, offset, kWave), other_total = __shfl_xor(total, offset, kWave);
+        const float top = __builtin_fmaxf(peak, other_peak);
+        total = top == neg_inf ? 0.0f
+                               : (peak == neg_inf ? 0.0f : total * fast_exp(peak - top)) +
+                                     (other_peak == neg_inf ? 0.0f : other_total * fast_exp(other_peak - top));
+        peak = top;
+    }
+    softmax_stats_add(peak, total, bf16_to_f32(a.sinks[kv * a.sh + g * a.sg]));
+    const float inverse = 1.0f / total;
+
+    f32x4_t o[D / 16];
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) {
+        o[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    for (uint32_t kb = 0; kb < blocks; ++kb) {
+        float m[8];
+        const bool any = masks(kb, m);
+        if (!__syncthreads_or(any)) {
+            continue;
+        }
+        stage(kb, true);
+        __syncthreads();
+        float s2[8];
+        scores(m, s2);
+        bf16x8_t pf;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            pf[i] = __builtin_bit_cast(__bf16, f32_to_bf16(fast_exp(s2[i] - peak) * inverse));
+        }
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt) {
+            const uint16_t* row = &v_s[(dt * 16u + col) * VPAD];
+            const uint2 lo = *reinterpret_cast<const uint2*>(row + quad * 4u);
+            const uint2 hi = *reinterpret_cast<const uint2*>(row + 16u + quad * 4u);
+            const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, uint4{lo.x, lo.y, hi.x, hi.y});
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[dt], 0, 0, 0);
+        }
+    }
+    if (live) {
+        uint16_t* dst = a.out + ((size_t(query) * a.kv_heads + kv) * a.group + g) * D;
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt) {
+            const uint32_t d = dt * 16u + quad * 4u;
+            const uint32_t w0 = uint32_t(f32_to_bf16(o[dt][0])) | (uint32_t(f32_to_bf16(o[dt][1])) << 16);
+            const uint32_t w1 = uint32_t(f32_to_bf16(o[dt][2])) | (uint32_t(f32_to_bf16(o[dt][3])) << 16);
+            *reinterpret_cast<uint2*>(dst + d) = uint2{w0, w1};
+        }
+    }
+}
+
+}  // namespace chroma

@@ -3,3 +3,4 @@
 
 #include "device.h"
 #include "linear.h"
+#include "attention.h"

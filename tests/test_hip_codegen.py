@@ -56,9 +56,11 @@ def test_dev_model_reuses_kernels_across_layers():
     stats = generated.stats
     assert stats["expert_contractions"] == 24
     assert stats["workspace_bytes"] < stats["unreused_workspace_bytes"]
-    # Small concatenations, clones of views and multi-consumer expressions fuse into their consumers:
-    # 14 launches per layer plus the final norm and unembedding (the reference's CUDA backend: 361).
-    assert stats["launches"] == stats["kernels"] == 12 * 14 + 3
+    # Small concatenations, clones of views and multi-consumer expressions fuse into their consumers and
+    # the attention chain is one launch: 12 launches per layer plus the final norm and unembedding (the
+    # reference's CUDA backend: 361).
+    assert stats["fused_attentions"] == 12
+    assert stats["launches"] == stats["kernels"] == 12 * 12 + 3
     assert stats["unique_kernels"] < stats["launches"] // 3
 
 

@@ -8,6 +8,7 @@ returns the given arrays, that a later call leaves earlier results untouched, an
 
 from __future__ import annotations
 
+import math
 import subprocess
 import sys
 from pathlib import Path
@@ -625,3 +626,67 @@ def test_gpt_oss_20b_slice_decoder(tmp_path):
             if top[0, 1] - top[0, 0] > 0.15:
                 assert got.argmax() == want.argmax()
         assert decoder.position == 44
+
+
+# ----------------------------------------------------------------------------------- fused attention
+def sink_attention(q, k, v, mask, sinks):
+    """The workload's attention chain with explicit operands (gpt_oss.py sdpa)."""
+    tokens, kv_heads, group, dim = q.shape
+    k = k[:, :, None, :].expand(-1, -1, group, -1)
+    v = v[:, :, None, :].expand(-1, -1, group, -1)
+    scores = torch.einsum("qhmd,khmd->hmqk", q, k) * (1 / math.sqrt(dim))
+    scores = scores + mask[None, None, :, :]
+    s = sinks.reshape(kv_heads, group, 1, 1).expand(-1, -1, tokens, -1)
+    weights = torch.softmax(torch.cat([scores, s], dim=-1), dim=-1)[..., :-1]
+    return torch.einsum("hmqk,khmd->qhmd", weights, v)
+
+
+class SinkAttention(torch.nn.Module):
+    """Past and new keys concatenated, as in the cached export."""
+
+    def forward(self, q, k_past, k_new, v_past, v_new, mask, sinks):
+        return sink_attention(q, torch.cat((k_past, k_new)), torch.cat((v_past, v_new)), mask, sinks)
+
+
+class FreshAttention(torch.nn.Module):
+    def forward(self, q, k, v, mask, sinks):
+        return sink_attention(q, k, v, mask, sinks)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize(
+    "tokens, past, kv_heads, group, dim",
+    [(1, 257, 1, 8, 16), (5, 3, 2, 4, 64), (3, 700, 2, 2, 4), (16, 0, 1, 1, 8), (100, 60, 2, 4, 64), (130, 0, 1, 2, 128),
+     (1, 4096, 8, 8, 64), (2, 1500, 1, 8, 16)],
+)
+def test_fused_attention_matches_oracle(tmp_path, dtype, tokens, past, kv_heads, group, dim):
+    """The fused attention against the oracle's unfused chain: causal and windowed masks, a query row whose
+    keys are all masked (only the sink remains), sinks of both signs; one launch per row, the matrix-core
+    kernel for long bfloat16 prefills, and keys split over workgroups (3 launches) for long caches."""
+    generator = torch.Generator().manual_seed(tokens * 31 + past)
+
+    def rand(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=generator) * scale).to(dtype)
+
+    keys = past + tokens
+    mask = torch.zeros(tokens, keys)
+    for t in range(tokens):
+        mask[t, past + t + 1 :] = -math.inf
+        mask[t, : max(0, past + t - 40)] = -math.inf
+    if tokens > 2:
+        mask[1, :] = -math.inf
+    inputs = (rand(tokens, kv_heads, group, dim), rand(past or 1, kv_heads, dim), rand(tokens, kv_heads, dim),
+              rand(past or 1, kv_heads, dim), rand(tokens, kv_heads, dim), mask.to(dtype), rand(kv_heads * group, scale=2.0))
+    if not past:  # no cached rows: a single key source
+        module, inputs = FreshAttention(), (inputs[0], inputs[2], inputs[4], inputs[5], inputs[6])
+    else:
+        module = SinkAttention()
+    exported = torch.export.export(module, inputs)
+    with chroma_amd.compile(exported, tmp_path / "hip") as model:
+        split = past + tokens > 1024 and tokens * kv_heads < 64
+        assert model.stats["fused_attentions"] == 1 and model.stats["launches"] <= (4 if split else 2)
+        # bfloat16 prefills of 64 or more queries take the matrix-core kernel
+        assert model.stats["mfma_matmuls"] == int(dtype == torch.bfloat16 and tokens >= 64)
+        got = model(*inputs)
+    want = compile_cpu(exported, tmp_path / "cpu")(*[numpy_of(v) for v in inputs])
+    compare(got, want)
