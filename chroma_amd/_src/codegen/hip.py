@@ -55,6 +55,8 @@ MATRIX_MIN_WORK = 1 << 18  # smaller batched products stay on the generic contra
 GROUPED_SLOTS = 64  # from this many (token, expert) slots on, expert products are grouped by expert
 MATRIX_ATTENTION_TOKENS = 64  # bfloat16 attention over at least this many queries runs on the matrix cores
 SPLIT_KEYS = 256  # keys per workgroup when an attention row's keys are split over workgroups
+STREAM_BLOCKS = 2048  # workgroups of a weight-streaming product (4-8 per compute unit keep HBM busy)
+STAGED_FLOATS = 8192  # X rows up to this many floats are widened into LDS once per workgroup
 
 UNARY_OPS = {
     "reciprocal": "reciprocal",
@@ -118,6 +120,7 @@ class HIPCodegen(Codegen):
         self.skinny_matmuls = 0
         self.mfma_matmuls = 0
         self.fused_attentions = 0
+        self.live_block_tables: Dict[tuple, Value] = {}
 
     # ===================================================================================== storage
     def extern(self, tensor: torch.Tensor, kind: str, offset: int) -> Value:
@@ -824,7 +827,44 @@ class HIPCodegen(Codegen):
         offset = value.view.offset
         return f"({slot} + {offset}u)" if offset else slot
 
+    @staticmethod
+    def _stream_plan(rows: int, inner: int, dtype: torch.dtype) -> Optional[Tuple[int, int]]:
+        """(lanes per row, rows per step) for ``stream_rows``: the widest power-of-two lane group that still
+        gives each lane 4 or more 16-byte chunks of a row (or a whole short row), and enough row steps
+        that about 32 chunks per lane are in flight; None when a row is not a whole number of chunks."""
+        per_chunk = 16 // ITEMSIZE[dtype]
+        if inner % per_chunk:
+            return None
+        chunks = inner // per_chunk
+        lanes = next((l for l in (64, 32, 16, 8, 4, 2) if chunks % l == 0 and chunks // l >= 4), 1)
+        per_lane = chunks // lanes
+        if per_lane > 64:
+            return None
+        steps = max(1, min(8, 32 // per_lane, max(1, 32 // rows)))
+        return lanes, steps
+
+    def _stream_blocks(self, columns: int, lanes: int, steps: int) -> int:
+        waves = -(-columns // (64 // lanes * steps))
+        return max(1, min(-(-waves // 4), STREAM_BLOCKS))
+
     def _skinny_linear(self, out, x, weight, bias, rows, columns, inner) -> None:
+        plan = self._stream_plan(rows, inner, out.dtype)
+        aligned = weight.view.offset % (16 // ITEMSIZE[weight.dtype]) == 0
+        # The streaming kernel widens X into LDS; larger X keeps the skinny kernel, which reads X in place.
+        if plan is not None and aligned and rows * inner <= STAGED_FLOATS:
+            lanes, steps = plan
+            k = Kernel(1)
+            args = [self._matrix_slot(k, x), self._matrix_slot(k, weight), self._matrix_slot(k, bias) if bias is not None else "nullptr"]
+            out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+            staged = True
+            prologue = [f"__shared__ float xs[{rows * inner}];"]
+            k.line(
+                f"chroma::stream_linear<{rows}, {inner}, {lanes}, {steps}, {str(staged).lower()}, {ctype_of(out.dtype)}>("
+                f"{args[0]}, {'xs' if staged else 'nullptr'}, {args[1]}, {args[2]}, {out_slot}, {columns}u);"
+            )
+            self.launch(k, self._stream_blocks(columns, lanes, steps), 256, [x, weight] + ([bias] if bias is not None else []),
+                        kind="linear_stream", prologue=prologue)
+            return
         lanes_per_row = 64
         while lanes_per_row > 1 and inner % (4 * lanes_per_row):
             lanes_per_row //= 2
@@ -1046,12 +1086,35 @@ class HIPCodegen(Codegen):
         k.line(f"a.sinks = {pointer('sinks')}; a.sh = {sink_strides[0]}u; a.sg = {sink_strides[1]}u;")
         k.line(f"a.out = {slot}; a.tokens = {tokens}u; a.past = {past}u; a.keys = {keys}u; a.kv_heads = {kv_heads}u; a.group = {group}u;")
         k.line(f"a.scale = {float_literal(scale)};")
+        live = self._live_blocks(plan["mask"], tokens, keys) if mask_strides[0] == mask_strides[1] == 0 else None
+        if live is not None:
+            k.line(f"a.live_blocks = reinterpret_cast<const uint8_t*>({k.slot(live.name, torch.int64, extent=self.extents[live.name])});")
+        else:
+            k.line("a.live_blocks = nullptr;")
         k.line(f"chroma::attention_mfma_bf16<{dim}>(a);")
-        operands = [entry[0] for entry in plan.values() if entry is not None]
+        operands = [entry[0] for entry in plan.values() if entry is not None] + ([live] if live is not None else [])
         self.launch(k, (-(-tokens // 64), kv_heads * group, 1), 256, operands, kind="attention_mfma")
         self.fused_attentions += 1
         self.mfma_matmuls += 1
         return True
+
+    def _live_blocks(self, mask_plan, tokens: int, keys: int) -> Value:
+        """Per (64-query, 32-key) block of a head-independent bfloat16 mask, whether any entry is not -inf:
+        computed once per mask and shared by every attention that reads it."""
+        value, strides, offset = mask_plan
+        key = (value.root.name, offset, strides[2], tokens, keys)
+        if key not in self.live_block_tables:
+            query_blocks, key_blocks = -(-tokens // 64), -(-keys // 32)
+            table = self.allocate((-(-query_blocks * key_blocks // 8),), torch.int64)
+            k = Kernel(1)
+            root = value.root
+            base = k.slot(root.name, root.dtype, extent=self.extents[root.name])
+            flags = k.slot(table.name, torch.int64, writable=True, extent=self.extents[table.name])
+            pointer = f"{base} + {offset}u" if offset else base
+            k.line(f"chroma::attention_live_blocks({pointer}, {strides[2]}u, {tokens}u, {keys}u, reinterpret_cast<uint8_t*>({flags}));")
+            self.launch(k, (query_blocks, key_blocks, 1), 256, [value], kind="attention_blocks")
+            self.live_block_tables[key] = table
+        return self.live_block_tables[key]
 
     # ================================================================================= einsum
     def einsum(self, meta, eqn: str, values: Sequence[Value]) -> Value:
@@ -1096,6 +1159,24 @@ class HIPCodegen(Codegen):
             self._grouped_experts(out, weight, indices, x, tokens, selected, experts, channels, inner, per_slot)
             self.expert_contractions += 1
             return out
+        per_expert = "true" if eqn == "beck,bek->bec" else "false"
+        plan = self._stream_plan(1, inner, out.dtype)
+        if plan is not None and weight.view.offset % (16 // ITEMSIZE[weight.dtype]) == 0 and inner <= STAGED_FLOATS:
+            lanes, steps = plan
+            k = Kernel(1)
+            w, idx, xs = self._matrix_slot(k, weight), self._matrix_slot(k, indices), self._matrix_slot(k, x)
+            out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+            k.uses_error = True
+            blocks_per_slot = max(1, min(-(-(-(-channels // (64 // lanes * steps))) // 4), STREAM_BLOCKS))
+            staged = True
+            k.line(
+                f"chroma::stream_expert_linear<{inner}, {lanes}, {steps}, {str(staged).lower()}, {ctype_of(out.dtype)}, {per_expert}>("
+                f"{w}, {idx}, {xs}, {'xs' if staged else 'nullptr'}, {out_slot}, {selected}u, {experts}u, {channels}u, {blocks_per_slot}u, error);"
+            )
+            self.launch(k, (blocks_per_slot, tokens * selected, 1), 256, [weight, indices, x], kind="expert_stream",
+                        prologue=[f"__shared__ float xs[{inner}];"] if staged else [])
+            self.expert_contractions += 1
+            return out
         lanes_per_row = 64
         while lanes_per_row > 1 and inner % (4 * lanes_per_row):
             lanes_per_row //= 2
@@ -1103,7 +1184,6 @@ class HIPCodegen(Codegen):
         w, idx, xs = self._matrix_slot(k, weight), self._matrix_slot(k, indices), self._matrix_slot(k, x)
         out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
         k.uses_error = True
-        per_expert = "true" if eqn == "beck,bek->bec" else "false"
         rows_per_wave = 64 // lanes_per_row
         blocks_per_slot = -(-(-(-channels // rows_per_wave)) // 4)
         k.line(

@@ -85,8 +85,10 @@ __device__ __forceinline__ void attention_rows(uint32_t begin, uint32_t end, flo
     }
     __syncthreads();
 
-    // Masked score of key j for every head: s2[g].
+    // Masked score of key j for every head: s2[g]. The empty asm keeps the compiler from hoisting the
+    // G x D query values out of the key loop into registers (they are LDS broadcasts, cheap to re-read).
     auto scores = [&](uint32_t j, float (&s2)[G]) {
+        __asm__ volatile("" ::: "memory");
         float kd[D];
 #pragma unroll
         for (int d = 0; d < D; ++d) {
@@ -288,7 +290,26 @@ struct AttentionOperands {
     uint16_t* out;
     uint32_t tokens, past, keys, kv_heads, group;
     float scale;
+    const uint8_t* live_blocks;  // [query blocks][key blocks]: 0 where the mask is -inf throughout (or nullptr)
 };
+
+// live_blocks[qb * key_blocks + kb] = whether any mask value of queries [64 qb, 64 qb + 64) and keys
+// [32 kb, 32 kb + 32) is not -inf, for a mask shared by every head (grid: query blocks x key blocks).
+__device__ __forceinline__ void attention_live_blocks(const uint16_t* __restrict__ mask, uint32_t mt, uint32_t tokens, uint32_t keys,
+                                                      uint8_t* __restrict__ live_blocks) {
+    const uint32_t qb = blockIdx.x, kb = blockIdx.y;
+    bool any = false;
+    for (uint32_t i = threadIdx.x; i < 64u * 32u; i += blockDim.x) {
+        const uint32_t t = qb * 64u + i / 32u, j = kb * 32u + i % 32u;
+        if (t < tokens && j < keys) {
+            any |= mask[size_t(t) * mt + j] != 0xff80u;
+        }
+    }
+    any = __syncthreads_or(any);
+    if (threadIdx.x == 0) {
+        live_blocks[qb * gridDim.y + kb] = any ? 1 : 0;
+    }
+}
 
 template <int D> __device__ __forceinline__ void attention_mfma_bf16(const AttentionOperands& a) {
     static_assert(D % 32 == 0 && D <= 128, "head dimension");
@@ -365,11 +386,23 @@ template <int D> __device__ __forceinline__ void attention_mfma_bf16(const Atten
     };
 
     const uint32_t blocks = (a.keys + KB - 1) / KB;
+    const uint8_t* live_row = a.live_blocks ? a.live_blocks + size_t(blockIdx.x) * blocks : nullptr;
+    // Whether key block kb has any unmasked score in this workgroup (a uniform answer for every thread).
+    auto active = [&](uint32_t kb, float (&m)[8]) -> bool {
+        if (live_row) {
+            if (!live_row[kb]) {
+                return false;
+            }
+            masks(kb, m);
+            __syncthreads();  // the previous block's LDS reads are done before the tile is restaged
+            return true;
+        }
+        return __syncthreads_or(masks(kb, m));
+    };
     float peak = neg_inf, total = 0.0f;
     for (uint32_t kb = 0; kb < blocks; ++kb) {
         float m[8];
-        const bool any = masks(kb, m);
-        if (!__syncthreads_or(any)) {
+        if (!active(kb, m)) {
             continue;
         }
         stage(kb, false);
@@ -401,8 +434,7 @@ template <int D> __device__ __forceinline__ void attention_mfma_bf16(const Atten
     }
     for (uint32_t kb = 0; kb < blocks; ++kb) {
         float m[8];
-        const bool any = masks(kb, m);
-        if (!__syncthreads_or(any)) {
+        if (!active(kb, m)) {
             continue;
         }
         stage(kb, true);

@@ -138,6 +138,142 @@ __device__ __forceinline__ void expert_linear(const T* __restrict__ w, const int
                            blocks_per_slot * waves_per_block);
 }
 
+// Streaming products for few rows of X: Y[m, n] = X[m, :] . W[n, :] (+ bias[n]) with every byte of W read
+// once through 16-byte non-temporal loads (the weight read is the whole cost of these products). LPR
+// lanes share one row of W, each holding PER_LANE 16-byte chunks; a wave covers 64 / LPR rows per step
+// and ROWS steps at once, and every chunk of those rows is requested before any arithmetic, so about
+// PER_LANE * ROWS * 1 KiB per wave is in flight. X is widened to float in LDS (``xs``, M * K floats) when
+// the caller provides it, else read through the cache. Partial sums meet through a butterfly over the
+// LPR lanes; the first lane of each row adds the bias and stores.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+template <class T> struct Chunk16;
+template <> struct Chunk16<float> {
+    static constexpr int N = 4;
+    static __device__ __forceinline__ u32x4_t load(const float* p) { return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p)); }
+    static __device__ __forceinline__ float get(const u32x4_t& c, int e) { return __uint_as_float(c[e]); }
+};
+template <> struct Chunk16<uint16_t> {
+    static constexpr int N = 8;
+    static __device__ __forceinline__ u32x4_t load(const uint16_t* p) { return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p)); }
+    static __device__ __forceinline__ float get(const u32x4_t& c, int e) {
+        return __uint_as_float((e & 1) ? (c[e / 2] & 0xffff0000u) : (c[e / 2] << 16));
+    }
+};
+
+template <int M, int K, class T>
+__device__ __forceinline__ void stage_rows(const T* __restrict__ x, float* xs) {
+    for (uint32_t i = threadIdx.x; i < uint32_t(M * K); i += blockDim.x) {
+        xs[i] = load1<T>(x + i);
+    }
+    __syncthreads();
+}
+
+template <int M, int K, int LPR, int ROWS, bool STAGED, class T>
+__device__ __forceinline__ void stream_rows(const T* __restrict__ x, const float* xs, const T* __restrict__ w, const T* __restrict__ bias,
+                                            T* __restrict__ out, uint32_t out_stride, uint32_t rows, uint32_t wave, uint32_t waves) {
+    using C = Chunk16<T>;
+    constexpr int CHUNKS = K / C::N;
+    constexpr int PER_LANE = CHUNKS / LPR;
+    constexpr int G = kWave / LPR;
+    static_assert(K % C::N == 0 && CHUNKS % LPR == 0, "rows must split into 16-byte chunks per lane");
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint32_t group = lane / LPR;
+    const uint32_t sub = lane % LPR;
+    auto xv = [&](int m, uint32_t k) -> float {
+        if constexpr (STAGED) {
+            return xs[m * K + k];
+        } else {
+            return load1<T>(x + size_t(m) * K + k);
+        }
+    };
+    for (uint32_t base = wave * G * ROWS; base < rows; base += waves * G * ROWS) {
+        // Keep X's values from being hoisted out of this loop: they would take K registers per lane
+        // (LDS or cache reads are cheap to repeat; registers are needed for the chunks in flight).
+        __asm__ volatile("" ::: "memory");
+        u32x4_t chunks[ROWS][PER_LANE];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+            const uint32_t row = base + r * G + group;
+            const uint32_t safe = row < rows ? row : rows - 1;
+#pragma unroll
+            for (int c = 0; c < PER_LANE; ++c) {
+                chunks[r][c] = C::load(w + size_t(safe) * K + (c * LPR + sub) * C::N);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+            float acc[M];
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                acc[m] = 0.0f;
+            }
+#pragma unroll
+            for (int c = 0; c < PER_LANE; ++c) {
+                const uint32_t k0 = (c * LPR + sub) * C::N;
+#pragma unroll
+                for (int e = 0; e < C::N; ++e) {
+                    const float wv = C::get(chunks[r][c], e);
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        acc[m] += wv * xv(m, k0 + e);
+                    }
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+#pragma unroll
+                for (int offset = LPR / 2; offset > 0; offset >>= 1) {
+                    acc[m] += __shfl_xor(acc[m], offset, kWave);
+                }
+            }
+            const uint32_t row = base + r * G + group;
+            if (sub == 0 && row < rows) {
+                const float b = bias ? load1<T>(bias + row) : 0.0f;
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    store1<T>(out + size_t(m) * out_stride + row, acc[m] + b);
+                }
+            }
+        }
+    }
+}
+
+// Y = X . W^T (+ bias) for M <= 16 rows of X through ``stream_rows``; with STAGED, ``xs`` is an LDS array of
+// M * K floats that X is widened into first.
+template <int M, int K, int LPR, int ROWS, bool STAGED, class T>
+__device__ __forceinline__ void stream_linear(const T* __restrict__ x, float* xs, const T* __restrict__ w, const T* __restrict__ bias,
+                                              T* __restrict__ out, uint32_t n) {
+    if constexpr (STAGED) {
+        stage_rows<M, K, T>(x, xs);
+    }
+    const uint32_t waves_per_block = blockDim.x / kWave;
+    const uint32_t wave = blockIdx.x * waves_per_block + threadIdx.x / kWave;
+    stream_rows<M, K, LPR, ROWS, STAGED, T>(x, xs, w, bias, out, n, n, wave, gridDim.x * waves_per_block);
+}
+
+// Selected-expert products through ``stream_rows``: out[slot, :] = W[expert(slot)] . x[token or slot]^T,
+// reading the chosen expert's [C, K] slab in place (the reference's expert_linear,
+// chroma/_src/codegen/cpu/kernels.h:76-99). Indices wrap when negative; an index outside
+// [-experts, experts) raises the error word and reads expert 0. grid.y enumerates the slots.
+template <int K, int LPR, int ROWS, bool STAGED, class T, bool PER_SLOT_INPUT>
+__device__ __forceinline__ void stream_expert_linear(const T* __restrict__ w, const int64_t* __restrict__ indices, const T* __restrict__ x,
+                                                     float* xs, T* __restrict__ out, uint32_t selected, uint32_t experts, uint32_t channels,
+                                                     uint32_t blocks_per_slot, unsigned int* error) {
+    const uint32_t slot = blockIdx.y;
+    const uint32_t token = slot / selected;
+    const uint64_t expert = checked_index(indices[slot], experts, true, error);
+    const T* slab = w + expert * uint64_t(channels) * K;
+    const T* row = x + uint64_t(PER_SLOT_INPUT ? slot : token) * K;
+    if constexpr (STAGED) {
+        stage_rows<1, K, T>(row, xs);
+    }
+    const uint32_t waves_per_block = blockDim.x / kWave;
+    const uint32_t wave = blockIdx.x * waves_per_block + threadIdx.x / kWave;
+    stream_rows<1, K, LPR, ROWS, STAGED, T>(row, xs, slab, nullptr, out + uint64_t(slot) * channels, channels, channels, wave,
+                                            blocks_per_slot * waves_per_block);
+}
+
 // General product for larger M: 64 x 64 output tiles, K staged through LDS 16 at a time, each of the
 // 256 threads accumulating a 4 x 4 block in registers.
 template <class T>

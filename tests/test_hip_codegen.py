@@ -66,11 +66,13 @@ def test_dev_model_reuses_kernels_across_layers():
 
 def test_linear_kernel_selection():
     module = torch.nn.Linear(16, 7).eval()
-    for blas, rows, kind in ((True, 3, "linear_skinny"), (True, 40, "linear_mfma"), (False, 3, "linear_scalar")):
+    for blas, rows, kind in ((True, 3, "linear_stream"), (True, 40, "linear_mfma"), (False, 3, "linear_scalar")):
         generated = lower(module, torch.ones(rows, 16), blas=blas)
         assert kind in generated.files["model.hip"], kind
         assert generated.stats["workspace_bytes"] == 0  # the result is written straight into the output
     assert "linear_tiled" in lower(torch.nn.Linear(17, 7).eval(), torch.ones(40, 17)).files["model.hip"]
+    # rows that are not a whole number of 16-byte chunks keep the 4-element skinny kernel
+    assert "linear_skinny" in lower(torch.nn.Linear(12, 7).bfloat16().eval(), torch.ones(3, 12, dtype=torch.bfloat16)).files["model.hip"]
     assert "mfma_linear<uint16_t>" in lower(torch.nn.Linear(64, 7).bfloat16().eval(), torch.ones(40, 64, dtype=torch.bfloat16)).files["model.hip"]
     # bfloat16 keeps float accumulation in both paths
     generated = lower(torch.nn.Linear(17, 7).bfloat16().eval(), torch.ones(3, 5, 17, dtype=torch.bfloat16))

@@ -134,6 +134,26 @@ def test_linear_kernels(tmp_path, blas):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows, inner, columns", [(1, 2880, 5003), (8, 128, 3001), (2, 4096, 200), (4, 16, 64), (8, 1024, 77)])
+def test_weight_streaming_linear(tmp_path, dtype, rows, inner, columns):
+    """Few-row products on the 16-byte weight-streaming kernel (X staged in LDS or read through the cache,
+    ragged last row groups, bias) against the oracle."""
+    generator = torch.Generator().manual_seed(rows * 7 + inner)
+    layer = torch.nn.Linear(inner, columns).eval()
+    with torch.no_grad():
+        layer.weight.copy_(torch.randn(columns, inner, generator=generator) * 0.05)
+        layer.bias.copy_(torch.randn(columns, generator=generator))
+    layer = layer.to(dtype)
+    x = torch.randn(rows, inner, generator=generator).to(dtype)
+    exported = torch.export.export(layer, (x,))
+    with chroma_amd.compile(exported, tmp_path / "hip") as model:
+        assert "linear_stream" in (tmp_path / "hip" / "model.hip").read_text()
+        got = model(x)
+    want = compile_cpu(exported, tmp_path / "cpu")(numpy_of(x))
+    assert_close(got, want, **tolerance(want))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("rows, inner, columns", [(300, 200, 384), (129, 64, 130), (17, 2888, 96)])
 def test_matrix_core_linear(tmp_path, dtype, rows, inner, columns):
     """MFMA products with partial 128 x 128 tiles and a partial last K step, against the oracle."""
