@@ -57,6 +57,7 @@ MATRIX_ATTENTION_TOKENS = 64  # bfloat16 attention over at least this many queri
 SPLIT_KEYS = 256  # keys per workgroup when an attention row's keys are split over workgroups
 STREAM_BLOCKS = 2048  # workgroups of a weight-streaming product (4-8 per compute unit keep HBM busy)
 STAGED_FLOATS = 8192  # X rows up to this many floats are widened into LDS once per workgroup
+STAGED_ROWS = 4096  # new key/value rows of an attention up to this many floats are evaluated into LDS once
 
 UNARY_OPS = {
     "reciprocal": "reciprocal",
@@ -441,22 +442,25 @@ class HIPCodegen(Codegen):
         return out
 
     def _concat_expression(self, meta, values: Sequence[Value], dim: int) -> Value:
-        """Concatenation folded into its consumer: a select over the parts along ``dim``. Every part is
-        evaluated, each at its coordinate clamped into range, so unselected reads stay in bounds."""
+        """Concatenation folded into its consumer: a case split over the parts along ``dim`` (only the
+        selected part is evaluated when the position along ``dim`` is the same for every lane of a thread;
+        otherwise every part is evaluated and selected). Coordinates are clamped into each part's range,
+        so no read leaves its buffer either way."""
         starts = [0]
         for value in values:
             starts.append(starts[-1] + value.shape[dim])
 
         def closure(k: Kernel, coords: List[Aff]) -> tuple:
             along = coords[dim]
-            node = None
-            for i in reversed(range(len(values))):
+            parts, tests = [], []
+            for i in range(len(values)):
                 start, size = starts[i], values[i].shape[dim]
                 local = list(coords)
                 local[dim] = k.derived(along, f"({{0}}) < {start}u ? 0u : (({{0}}) - {start}u < {size}u ? ({{0}}) - {start}u : {size - 1}u)", size - 1)
-                part = self.read(k, values[i], local)
-                node = part if node is None else ("sel", ("cmp", "<", along, ZERO, starts[i + 1]), part, node)
-            return node
+                parts.append(self.read(k, values[i], local))
+                if i < len(values) - 1:
+                    tests.append(("cmp", "<", along, ZERO, starts[i + 1]))
+            return ("cases", tuple(tests), tuple(parts))
 
         return self.expr(meta, closure, list(values))
 
@@ -981,14 +985,37 @@ class HIPCodegen(Codegen):
                     k.line(f"return {k.emit(first(coords))};")
                 k.line(f"return {k.emit(second(coords))};")
 
+        fresh = keys - past
+        staged = loaders and fresh * dim <= STAGED_ROWS
+
         def key_source(past_value: Optional[Value], new_value: Value, name: str) -> None:
-            if past_value is None:
-                loader(name, [("j", keys - 1), ("d", dim - 1)], lambda c: self.read(k, new_value, [c[0], h, c[1]]))
-                return
             params = [("j", keys - 1), ("d", dim - 1)]
+            if staged:
+                # The new rows (often a fused expression such as the rotary embedding) are evaluated once,
+                # cooperatively, into LDS; the key loops then read plain LDS values.
+                k.line(f"__shared__ float {name}_new[{fresh * dim}];")
+                with k.block(f"for (uint32_t i = threadIdx.x; i < {fresh * dim}u; i += blockDim.x) {{"):
+                    i = Aff.of(Atom("i", fresh * dim - 1))
+                    row, column = k.div(i, dim), k.mod(i, dim)
+                    k.line(f"{name}_new[i] = {k.emit(self.read(k, new_value, [row, h, column]))};")
+
+            if past_value is None:
+                if staged:
+                    with k.block(f"auto {name} = [&](uint32_t j, uint32_t d) -> float {{", "};"):
+                        k.line(f"return {name}_new[j * {dim}u + d];")
+                    return
+                loader(name, params, lambda c: self.read(k, new_value, [c[0], h, c[1]]))
+                return
 
             def first(c):
                 return self.read(k, past_value, [Aff.of(Atom("j", past - 1)), h, c[1]])
+
+            if staged:
+                with k.block(f"auto {name} = [&](uint32_t j, uint32_t d) -> float {{", "};"):
+                    with k.block(f"if (j < {past}u) {{"):
+                        k.line(f"return {k.emit(first([Aff.of(Atom('j', keys - 1)), Aff.of(Atom('d', dim - 1))]))};")
+                    k.line(f"return {name}_new[(j - {past}u) * {dim}u + d];")
+                return
 
             def second(c):
                 shifted = k.derived(c[0], f"({{}}) - {past}u", keys - past - 1)

@@ -128,7 +128,7 @@ def is_int(dtype: torch.dtype) -> bool:
 
 # Expression nodes are tuples (hash-consed through the kernel's memo):
 #   ("ld", slot, dtype, aff)   ("f", value)   ("i", value)   ("un", op, x)   ("bin", op, x, y)
-#   ("rnd", x)   ("sel", cond, x, y)   ("cmp", op, aff_a, aff_b, constant)
+#   ("rnd", x)   ("sel", cond, x, y)   ("cmp", op, aff_a, aff_b, constant)   ("cases", tests, parts)
 Node = tuple
 
 UNARY_CODE = {
@@ -355,6 +355,8 @@ class Kernel:
             return True
         if tag == "sel":
             return Kernel.node_is_int(node[2])
+        if tag == "cases":
+            return Kernel.node_is_int(node[2][0])
         return False
 
     def _vector_aligned(self, aff: Aff, vector: Atom) -> bool:
@@ -376,6 +378,8 @@ class Kernel:
             result = self._emit_load(node)
         elif tag == "cmp":
             result = self._emit_compare(node)
+        elif tag == "cases":
+            result = self._emit_cases(node)
         else:
             operands = [self.emit(part) for part in node[2:]] if tag in ("un", "bin") else [self.emit(part) for part in node[1:]]
             varying = any(isinstance(o, list) for o in operands)
@@ -400,6 +404,37 @@ class Kernel:
             result = names if varying else names[0]
         self.nodes[node] = result
         return result
+
+    def _emit_cases(self, node: Node) -> Union[str, List[str]]:
+        """("cases", tests, parts): parts[i] for the first true tests[i] (the last part otherwise). With
+        uniform tests only the selected part is evaluated (one branch each); tests that vary across lanes
+        fall back to selects over every part."""
+        _, tests, parts = node
+        if any(test[2].varying or test[3].varying for test in tests):
+            chained = parts[-1]
+            for test, part in zip(reversed(tests), reversed(parts[:-1])):
+                chained = ("sel", test, part, chained)
+            return self.emit(chained)
+        ctype = "int64_t" if self.node_is_int(parts[0]) else "float"
+        base = self.fresh("c")
+        # One result per lane (parts may vary across lanes even when the tests do not).
+        names = [base] if self.lanes == 1 else [f"{base}_{lane}" for lane in range(self.lanes)]
+        self.line(f"{ctype} {', '.join(names)};")
+        conditions = [self.emit(test) for test in tests]
+        for i, part in enumerate(parts):
+            if i < len(tests):
+                self.line(("if (" if i == 0 else "} else if (") + f"{conditions[i]}) {{")
+            else:
+                self.line("} else {" if tests else "{")
+            saved = (dict(self.atoms), dict(self.nodes), dict(self.values))
+            self.indent += 1
+            value = self.emit(part)
+            for lane, name in enumerate(names):
+                self.line(f"{name} = {value[lane] if isinstance(value, list) else value};")
+            self.indent -= 1
+            self.atoms, self.nodes, self.values = saved
+        self.line("}")
+        return names if self.lanes > 1 else base
 
     def _emit_compare(self, node: Node) -> Union[str, List[str]]:
         _, op, left, right, constant = node
