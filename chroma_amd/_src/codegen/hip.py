@@ -49,7 +49,8 @@ ROW_RESIDENT = 32
 STREAMING_STORES = True
 STREAMING_BYTES = 64 << 20  # smaller operands and results may stay in L2 / the last-level cache
 FUSED_CONCAT_ELEMENTS = 1 << 16  # smaller concatenations are fused into their consumers
-DEFERRED_ELEMENTS = 1 << 16  # smaller expressions the front end asks to store stay fused instead
+DEFERRED_ELEMENTS = 1 << 16  # smaller expressions the front end asks to store stay fused instead...
+DEFERRED_SOURCES = 4  # ...when they read at most this many buffers (a residual stream is stored every few adds)
 REUSED_EVALUATIONS = 1 << 18  # a contraction operand is stored when (elements x reuse) reaches this
 MATRIX_MIN_WORK = 1 << 18  # smaller batched products stay on the generic contraction kernel
 GROUPED_SLOTS = 64  # from this many (token, expert) slots on, expert products are grouped by expert
@@ -58,6 +59,8 @@ SPLIT_KEYS = 256  # keys per workgroup when an attention row's keys are split ov
 STREAM_BLOCKS = 2048  # workgroups of a weight-streaming product (4-8 per compute unit keep HBM busy)
 STAGED_FLOATS = 8192  # X rows up to this many floats are widened into LDS once per workgroup
 STAGED_ROWS = 4096  # new key/value rows of an attention up to this many floats are evaluated into LDS once
+FOLDED_NORM_ROWS = 16  # RMSNorms over at most this many rows are folded into the kernels that stage them
+FOLDED_STAGING_BLOCKS = 32  # staging kernels with more workgroups read a stored copy of an expression operand
 
 UNARY_OPS = {
     "reciprocal": "reciprocal",
@@ -122,6 +125,12 @@ class HIPCodegen(Codegen):
         self.mfma_matmuls = 0
         self.fused_attentions = 0
         self.live_block_tables: Dict[tuple, Value] = {}
+        self.pending_norms: Dict[str, tuple] = {}  # deferred RMSNorm value -> (meta, x, weight, epsilon)
+        self.pending_of: Dict[str, frozenset] = {}  # value -> deferred norms its expression reads
+        self.retractable: Dict[str, tuple] = {}  # small linear output -> (launch index, x, weight, bias)
+        self.router_weights: Dict[str, Value] = {}  # top-k values -> their softmax, written by the router
+        self.folded_norms = 0
+        self.fused_routers = 0
 
     # ===================================================================================== storage
     def extern(self, tensor: torch.Tensor, kind: str, offset: int) -> Value:
@@ -152,6 +161,9 @@ class HIPCodegen(Codegen):
         name = f"e{next(self.counter)}"
         self.closures[name] = closure
         self.sources[name] = frozenset().union(*(self.sources[v.name] for v in inputs)) if inputs else frozenset()
+        pending = frozenset().union(*(self.pending_of.get(v.name, frozenset()) for v in inputs)) if inputs else frozenset()
+        if pending:
+            self.pending_of[name] = pending
         value = self.expression_value(name, meta, inputs)
         if value.depth >= MAX_DEPTH or len(self.sources[name]) >= MAX_SOURCES:
             return self.store(value)
@@ -189,15 +201,19 @@ class HIPCodegen(Codegen):
 
         * a strided view of a stored buffer already has storage and is returned as one (consumers read it
           through its strides; matrix kernels ask for ``contiguous`` instead);
-        * an expression of at most ``DEFERRED_ELEMENTS`` elements stays fused into each consumer, where it
-          costs a few instructions instead of a launch (consumers evaluate shared subexpressions once);
+        * an expression of at most ``DEFERRED_ELEMENTS`` elements reading at most ``DEFERRED_SOURCES``
+          buffers stays fused into each consumer, where it costs a few instructions instead of a launch
+          (consumers evaluate shared subexpressions once); longer chains, such as a residual stream over
+          many layers, are stored so that no consumer re-evaluates the whole chain;
         * anything larger is written to the arena once.
         """
         if value.stored:
             return value
         if value.view is not None and value.view.base is not None:
             return Value(value.name, value.shape, value.dtype, value.deps, stored=True, view=value.view)
-        if math.prod(value.shape) <= DEFERRED_ELEMENTS:
+        if value.name in self.pending_norms:
+            return value  # consumers that stage their rows fold it; any other reader stores it
+        if math.prod(value.shape) <= DEFERRED_ELEMENTS and len(self.sources[value.name]) <= DEFERRED_SOURCES:
             return value
         return self.store(value)
 
@@ -205,6 +221,8 @@ class HIPCodegen(Codegen):
         """Write ``value`` to a fresh arena allocation (once; later requests reuse it)."""
         if value.stored:
             return value
+        if value.name in self.pending_norms:
+            return self._force_norm(value.name)
         if value.name not in self.materialized:
             out = self.allocate(value.shape, value.dtype)
             self.map_kernel(out, value)
@@ -352,6 +370,8 @@ class HIPCodegen(Codegen):
         for buffer in k.slots:
             allocation = self.allocations.get(buffer)
             if allocation is not None:
+                # live at every launch that touches it (a fused launch may take the index of an earlier one)
+                allocation.start = min(allocation.start, self.kernels)
                 allocation.end = max(allocation.end, self.kernels)
         self.record_usage(inputs)
         self.launches.append(Launch(name, grid3, block, bindings, shared))
@@ -480,6 +500,9 @@ class HIPCodegen(Codegen):
         return [*outer_coords, along, *inner_coords]
 
     def softmax(self, meta, x: Value, dim: int) -> Value:
+        routed = self.router_weights.get(x.name)
+        if routed is not None and dim == len(x.shape) - 1 and routed.dtype == meta.dtype:
+            return routed
         out = self.allocate(tuple(meta.shape), meta.dtype)
         shape = tuple(x.shape)
         width, inner, outer = self._row_layout(shape, dim)
@@ -636,6 +659,108 @@ class HIPCodegen(Codegen):
 
     # -------------------------------------------------------------------------------- RMSNorm
     def norm(self, meta, x: Value, weight: Value, epsilon: float) -> Value:
+        """RMSNorm. A norm over at most ``FOLDED_NORM_ROWS`` rows is deferred: kernels that stage their
+        operand rows in LDS (weight-streaming linears, selected experts, the router) compute the row
+        scales in their prologue and apply ``x * scale * w`` while staging, so the normalised rows are
+        never written; the first other reader stores it with the norm kernel below."""
+        shape = _shape(x.shape)
+        if math.prod(shape) // shape[-1] <= FOLDED_NORM_ROWS and self.blas:
+            name = f"r{next(self.counter)}"
+            value = Value(name, tuple(meta.shape), meta.dtype, x.deps | weight.deps, depth=1)
+            self.pending_norms[name] = (meta, x, weight, epsilon)
+            self.sources[name] = self.sources[x.name] | self.sources[weight.name]
+            self.pending_of[name] = frozenset({name})
+            self.closures[name] = lambda k, coords, name=name: self._norm_node(k, name, coords)
+            return value
+        return self._norm_kernel(meta, x, weight, epsilon)
+
+    def _force_norm(self, name: str) -> Value:
+        if name not in self.materialized:
+            self.materialized[name] = self._norm_kernel(*self.pending_norms[name])
+        return self.materialized[name]
+
+    def _norm_node(self, k: Kernel, name: str, coords: Sequence[Aff]) -> tuple:
+        """The deferred norm at ``coords``: from its stored copy if one exists, from the row scales a
+        staging prologue declared in ``k``, or else by storing it now."""
+        if name in self.materialized:
+            return self.read(k, self.materialized[name], coords)
+        scales = getattr(k, "norm_scales", {}).get(name)
+        if scales is None:
+            return self.read(k, self._force_norm(name), coords)
+        meta, x, weight, _ = self.pending_norms[name]
+        shape = _shape(x.shape)
+        row = Kernel.flatten(list(coords[:-1]), shape[:-1]) if len(shape) > 1 else ZERO
+        key = ("norm_scale", name, row)
+        if key not in k.nodes:
+            scale = k.fresh("s")
+            k.line(f"const float {scale} = {scales}[{row.code()}];")
+            k.nodes[key] = scale
+        scale_node = ("raw", (k.nodes[key],))
+        k.nodes[scale_node] = k.nodes[key]
+        return ("bin", "mul", ("bin", "mul", self.read(k, x, coords), scale_node), self.read(k, weight, [coords[-1]]))
+
+    def _stageable(self, x: Value, blocks: int) -> Value:
+        """The operand a staging kernel of ``blocks`` workgroups should read: every workgroup evaluates
+        the staged rows itself, so an expression (or a deferred norm) is stored once first when many
+        workgroups would repeat it."""
+        if blocks <= FOLDED_STAGING_BLOCKS or x.stored or (x.view is not None and x.view.base is not None):
+            return x
+        return self.store(x)
+
+    def _stage(self, k: Kernel, x: Value, rows: int, inner: int, coords_of: Callable[[Aff], List[Aff]], threads: int, array: str = "xs") -> None:
+        """Emit the prologue that fills ``__shared__ float array[rows * inner]`` with ``x`` row by row:
+        element (r, c) is ``x`` at ``coords_of(r) + [c]``, evaluated through generated code (so views and
+        fused expressions are read in place). Deferred norms that ``x`` depends on get their row scales
+        computed first. Ends with a workgroup barrier."""
+        waves = threads // 64
+        k.norm_scales = {}
+        for name in sorted(self.pending_of.get(x.name, frozenset())):
+            if name in self.materialized:
+                continue
+            _, source, _, epsilon = self.pending_norms[name]
+            shape = _shape(source.shape)
+            norm_rows, columns = math.prod(shape) // shape[-1], shape[-1]
+            scales = k.fresh("ns")
+            k.line(f"__shared__ float {scales}[{norm_rows}];")
+            # All rows at once: ``lanes`` consecutive threads (a power of two, at most a wave) sum the
+            # squares of one row and meet through a butterfly.
+            span = 1 << (norm_rows - 1).bit_length()
+            lanes = max(1, threads // span)
+            with k.block("{"):
+                k.line(f"const uint32_t nr = threadIdx.x / {lanes}u, nl = threadIdx.x % {lanes}u;")
+                k.line("float squares = 0.0f;")
+                with k.block(f"if (nr < {norm_rows}u) {{"):
+                    r_atom = Aff.of(Atom("nr", norm_rows - 1))
+                    row_coords = k.unflatten(r_atom, shape[:-1]) if len(shape) > 1 else []
+                    k.line("#pragma unroll 4")
+                    with k.block(f"for (uint32_t c = nl; c < {columns}u; c += {lanes}u) {{"):
+                        value = k.emit(self.read(k, source, [*row_coords, Aff.of(Atom("c", columns - 1))]))
+                        k.line(f"squares += {value} * {value};")
+                k.line(f"for (uint32_t o = {min(lanes, 64) // 2}u; o > 0u; o >>= 1) squares += __shfl_xor(squares, int(o), 64);")
+                formula = f"1.0f / sqrtf(total / {float_literal(columns)} + {float_literal(epsilon)})"
+                if lanes <= 64:
+                    k.line(f"if (nl == 0u && nr < {norm_rows}u) {{ const float total = squares; {scales}[nr] = {formula}; }}")
+                else:
+                    # a row spans several waves: their sums meet in LDS
+                    per_row = lanes // 64
+                    k.line(f"__shared__ float {scales}_waves[{threads // 64}];")
+                    k.line(f"if (threadIdx.x % 64u == 0u) {scales}_waves[threadIdx.x / 64u] = squares;")
+                    k.line("__syncthreads();")
+                    k.line(f"if (nl == 0u && nr < {norm_rows}u) {{ float total = 0.0f; "
+                           f"for (uint32_t w = 0; w < {per_row}u; ++w) total += {scales}_waves[nr * {per_row}u + w]; {scales}[nr] = {formula}; }}")
+            k.norm_scales[name] = scales
+        if k.norm_scales:
+            k.line("__syncthreads();")
+        k.line(f"__shared__ float {array}[{rows * inner}];")
+        k.line("#pragma unroll 4")
+        with k.block(f"for (uint32_t i = threadIdx.x; i < {rows * inner}u; i += {threads}u) {{"):
+            i = Aff.of(Atom("i", rows * inner - 1))
+            row, column = k.div(i, inner), k.mod(i, inner)
+            k.line(f"{array}[i] = {k.emit(self.read(k, x, [*coords_of(row), column]))};")
+        k.line("__syncthreads();")
+        k.norm_scales = {}
+
+    def _norm_kernel(self, meta, x: Value, weight: Value, epsilon: float) -> Value:
         out = self.allocate(tuple(meta.shape), meta.dtype)
         shape = _shape(x.shape)
         columns = shape[-1]
@@ -753,6 +878,8 @@ class HIPCodegen(Codegen):
     def topk(self, meta, x: Value, dim: int, largest: bool, sort: bool):
         values = self.allocate(tuple(meta[0].shape), meta[0].dtype)
         indices = self.allocate(tuple(meta[1].shape), meta[1].dtype)
+        if self._router(meta, x, dim, largest, sort, values, indices):
+            return values, indices
         shape = tuple(x.shape)
         width, inner, outer = self._row_layout(shape, dim)
         count = meta[0].shape[dim]
@@ -799,17 +926,69 @@ class HIPCodegen(Codegen):
         self.launch(k, -(-rows // groups), 64 * groups, [x], kind="topk")
         return values, indices
 
+    def _router(self, meta, x: Value, dim: int, largest: bool, sort: bool, values: Value, indices: Value) -> bool:
+        """Top-k of a few-row linear's output that was the last launch (a mixture-of-experts router): the
+        linear launch is replaced by one kernel per row that recomputes its logits (writing them, so any
+        other reader of the linear still finds them), selects the top k and also writes the softmax of
+        the selected values, which ``softmax`` then returns without a launch."""
+        entry = self.retractable.get(x.name)
+        if entry is None or entry[0] != len(self.launches) - 1 or not sort or dim != len(x.shape) - 1:
+            return False
+        _, source, weight, bias, rows, columns, inner = entry
+        count = values.shape[dim]
+        if x.dtype not in (torch.float32, torch.bfloat16) or math.prod(values.shape) != rows * count:
+            return False
+        popped = self.launches.pop()
+        self.kernels -= 1
+        if all(launch.kernel != popped.kernel for launch in self.launches):
+            text = next(src for src, name in self.kernel_names.items() if name == popped.kernel)
+            del self.kernel_names[text]
+            self.kernel_sources = [text for text in self.kernel_sources if f" {popped.kernel}(" not in text]
+        weights = self.allocate(tuple(values.shape), values.dtype)
+        k = Kernel(1)
+        row = Aff.of(k.atom("blockIdx.x", rows - 1, prefix="r"))
+        lead = tuple(source.shape[:-1])
+        self._stage(k, source, 1, inner, lambda _r: k.unflatten(row, lead) if lead else [], 256)
+        ctype = ctype_of(x.dtype)
+        w_arg = self._matrix_slot(k, weight)
+        b_arg = self._matrix_slot(k, bias) if bias is not None else "nullptr"
+        logits = k.slot(x.name, x.dtype, writable=True, extent=self.extents[x.name])
+        value_slot = k.slot(values.name, values.dtype, writable=True, extent=self.extents[values.name])
+        index_slot = k.slot(indices.name, indices.dtype, writable=True, extent=self.extents[indices.name])
+        weight_slot = k.slot(weights.name, weights.dtype, writable=True, extent=self.extents[weights.name])
+        r = row.code()
+        per_chunk = 16 // ITEMSIZE[x.dtype]
+        chunks = inner // per_chunk if inner % per_chunk == 0 else 0
+        lanes = next((l for l in (64, 32, 16, 8, 4, 2) if chunks and chunks % l == 0 and chunks // l >= 4), 1 if chunks else 0)
+        k.line(
+            f"chroma::router_row<{columns}, {inner}, {lanes}, {str(bool(largest)).lower()}, {ctype}>(xs, {w_arg}, {b_arg}, {logits} + {r} * {columns}u, "
+            f"{value_slot} + {r} * {count}u, {index_slot} + {r} * {count}u, {weight_slot} + {r} * {count}u, {count}u);"
+        )
+        self.launch(k, rows, 256, [source, weight] + ([bias] if bias is not None else []), kind="router")
+        self.router_weights[values.name] = weights
+        self.fused_routers += 1
+        return True
+
     # =================================================================================== linear
     def linear(self, meta, x: Value, weight: Value, bias: Optional[Value]) -> Value:
         rows, columns, inner = math.prod(x.shape[:-1]), weight.shape[0], weight.shape[1]
         if max(rows, columns, inner) > 2**31 - 1:
             raise ValueError("Matrix dimensions exceed the integer range of the matrix kernels")
-        x, weight = self.contiguous(x), self.contiguous(weight)
+        weight = self.contiguous(weight)
         bias = self.contiguous(bias) if bias is not None else None
         out = self.allocate(tuple(meta.shape), meta.dtype)
         dtypes = {x.dtype, weight.dtype, meta.dtype} | ({bias.dtype} if bias is not None else set())
         if len(dtypes) != 1:
             raise NotImplementedError(f"mixed-dtype linear {dtypes}")
+        plan = self._stream_plan(rows, inner, meta.dtype)
+        if (self.blas and rows <= 16 and plan is not None and rows * inner <= STAGED_FLOATS
+                and weight.view.offset % (16 // ITEMSIZE[weight.dtype]) == 0):
+            self._stream_linear(out, x, weight, bias, rows, columns, inner, plan)
+            self.skinny_matmuls += 1
+            if columns <= 64:
+                self.retractable[out.name] = (len(self.launches) - 1, x, weight, bias, rows, columns, inner)
+            return out
+        x = self.contiguous(x)
         inputs = [x, weight] + ([bias] if bias is not None else [])
         if self.blas and rows <= 16 and inner % 4 == 0:
             self._skinny_linear(out, x, weight, bias, rows, columns, inner)
@@ -851,24 +1030,25 @@ class HIPCodegen(Codegen):
         waves = -(-columns // (64 // lanes * steps))
         return max(1, min(-(-waves // 4), STREAM_BLOCKS))
 
+    def _stream_linear(self, out, x, weight, bias, rows, columns, inner, plan) -> None:
+        """A few-row linear on the weight-streaming kernel; X (any view or fused expression, including a
+        deferred norm) is evaluated into LDS by the generated prologue."""
+        lanes, steps = plan
+        blocks = self._stream_blocks(columns, lanes, steps)
+        x = self._stageable(x, blocks)
+        k = Kernel(1)
+        w_arg = self._matrix_slot(k, weight)
+        b_arg = self._matrix_slot(k, bias) if bias is not None else "nullptr"
+        out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        lead = tuple(x.shape[:-1])
+        self._stage(k, x, rows, inner, lambda row: k.unflatten(row, lead) if lead else [], 256)
+        k.line(
+            f"chroma::stream_linear<{rows}, {inner}, {lanes}, {steps}, true, {ctype_of(out.dtype)}>("
+            f"nullptr, xs, {w_arg}, {b_arg}, {out_slot}, {columns}u);"
+        )
+        self.launch(k, blocks, 256, [x, weight] + ([bias] if bias is not None else []), kind="linear_stream")
+
     def _skinny_linear(self, out, x, weight, bias, rows, columns, inner) -> None:
-        plan = self._stream_plan(rows, inner, out.dtype)
-        aligned = weight.view.offset % (16 // ITEMSIZE[weight.dtype]) == 0
-        # The streaming kernel widens X into LDS; larger X keeps the skinny kernel, which reads X in place.
-        if plan is not None and aligned and rows * inner <= STAGED_FLOATS:
-            lanes, steps = plan
-            k = Kernel(1)
-            args = [self._matrix_slot(k, x), self._matrix_slot(k, weight), self._matrix_slot(k, bias) if bias is not None else "nullptr"]
-            out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
-            staged = True
-            prologue = [f"__shared__ float xs[{rows * inner}];"]
-            k.line(
-                f"chroma::stream_linear<{rows}, {inner}, {lanes}, {steps}, {str(staged).lower()}, {ctype_of(out.dtype)}>("
-                f"{args[0]}, {'xs' if staged else 'nullptr'}, {args[1]}, {args[2]}, {out_slot}, {columns}u);"
-            )
-            self.launch(k, self._stream_blocks(columns, lanes, steps), 256, [x, weight] + ([bias] if bias is not None else []),
-                        kind="linear_stream", prologue=prologue)
-            return
         lanes_per_row = 64
         while lanes_per_row > 1 and inner % (4 * lanes_per_row):
             lanes_per_row //= 2
@@ -1174,7 +1354,7 @@ class HIPCodegen(Codegen):
         weight, indices = source
         if weight.dtype != meta.dtype or weight.shape[-1] % 4:
             return None
-        weight, indices, x = self.contiguous(weight), self.contiguous(indices), self.contiguous(values[1])
+        weight, indices, x = self.contiguous(weight), self.contiguous(indices), values[1]
         if x.dtype != meta.dtype:
             return None
         out = self.allocate(tuple(meta.shape), meta.dtype)
@@ -1182,26 +1362,36 @@ class HIPCodegen(Codegen):
         inner = weight.shape[-1]
         experts = weight.shape[0]
         per_slot = eqn == "beck,bek->bec"
-        if tokens * selected >= GROUPED_SLOTS and inner % (8 if meta.dtype == torch.bfloat16 else 4) == 0 and experts <= 4096:
-            self._grouped_experts(out, weight, indices, x, tokens, selected, experts, channels, inner, per_slot)
-            self.expert_contractions += 1
-            return out
-        per_expert = "true" if eqn == "beck,bek->bec" else "false"
+        per_expert = "true" if per_slot else "false"
         plan = self._stream_plan(1, inner, out.dtype)
-        if plan is not None and weight.view.offset % (16 // ITEMSIZE[weight.dtype]) == 0 and inner <= STAGED_FLOATS:
+        if (tokens * selected < GROUPED_SLOTS and plan is not None and inner <= STAGED_FLOATS
+                and weight.view.offset % (16 // ITEMSIZE[weight.dtype]) == 0):
+            # One slot per workgroup row of the grid: the slot's input row (per token or per slot; any
+            # view or fused expression, e.g. the gated activation of the first expert product) is
+            # evaluated into LDS, then the selected expert's slab is streamed.
             lanes, steps = plan
+            blocks_per_slot = max(1, min(-(-(-(-channels // (64 // lanes * steps))) // 4), STREAM_BLOCKS))
+            x = self._stageable(x, blocks_per_slot * tokens * selected)
             k = Kernel(1)
-            w, idx, xs = self._matrix_slot(k, weight), self._matrix_slot(k, indices), self._matrix_slot(k, x)
+            w, idx = self._matrix_slot(k, weight), self._matrix_slot(k, indices)
             out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
             k.uses_error = True
-            blocks_per_slot = max(1, min(-(-(-(-channels // (64 // lanes * steps))) // 4), STREAM_BLOCKS))
-            staged = True
+            slot = Aff.of(k.atom("blockIdx.y", tokens * selected - 1, prefix="s"))
+            if per_slot:
+                coords_of = lambda _row: [k.div(slot, selected), k.mod(slot, selected)]
+            else:
+                coords_of = lambda _row: [k.div(slot, selected)]
+            self._stage(k, x, 1, inner, coords_of, 256)
             k.line(
-                f"chroma::stream_expert_linear<{inner}, {lanes}, {steps}, {str(staged).lower()}, {ctype_of(out.dtype)}, {per_expert}>("
-                f"{w}, {idx}, {xs}, {'xs' if staged else 'nullptr'}, {out_slot}, {selected}u, {experts}u, {channels}u, {blocks_per_slot}u, error);"
+                f"chroma::stream_expert_linear<{inner}, {lanes}, {steps}, true, {ctype_of(out.dtype)}, {per_expert}>("
+                f"{w}, {idx}, nullptr, xs, {out_slot}, {selected}u, {experts}u, {channels}u, {blocks_per_slot}u, error);"
             )
-            self.launch(k, (blocks_per_slot, tokens * selected, 1), 256, [weight, indices, x], kind="expert_stream",
-                        prologue=[f"__shared__ float xs[{inner}];"] if staged else [])
+            self.launch(k, (blocks_per_slot, tokens * selected, 1), 256, [weight, indices, x], kind="expert_stream")
+            self.expert_contractions += 1
+            return out
+        x = self.contiguous(x)
+        if tokens * selected >= GROUPED_SLOTS and inner % (8 if meta.dtype == torch.bfloat16 else 4) == 0 and experts <= 4096:
+            self._grouped_experts(out, weight, indices, x, tokens, selected, experts, channels, inner, per_slot)
             self.expert_contractions += 1
             return out
         lanes_per_row = 64
@@ -1430,6 +1620,7 @@ class HIPCodegen(Codegen):
             skinny_matmuls=self.skinny_matmuls,
             mfma_matmuls=self.mfma_matmuls,
             fused_attentions=self.fused_attentions,
+            fused_routers=self.fused_routers,
             unique_kernels=len(self.kernel_sources),
             launches=len(self.launches),
         )

@@ -161,14 +161,6 @@ template <> struct Chunk16<uint16_t> {
     }
 };
 
-template <int M, int K, class T>
-__device__ __forceinline__ void stage_rows(const T* __restrict__ x, float* xs) {
-    for (uint32_t i = threadIdx.x; i < uint32_t(M * K); i += blockDim.x) {
-        xs[i] = load1<T>(x + i);
-    }
-    __syncthreads();
-}
-
 template <int M, int K, int LPR, int ROWS, bool STAGED, class T>
 __device__ __forceinline__ void stream_rows(const T* __restrict__ x, const float* xs, const T* __restrict__ w, const T* __restrict__ bias,
                                             T* __restrict__ out, uint32_t out_stride, uint32_t rows, uint32_t wave, uint32_t waves) {
@@ -240,13 +232,11 @@ __device__ __forceinline__ void stream_rows(const T* __restrict__ x, const float
 }
 
 // Y = X . W^T (+ bias) for M <= 16 rows of X through ``stream_rows``; with STAGED, ``xs`` is an LDS array of
-// M * K floats that X is widened into first.
+// M * K floats that already holds X (the caller's generated code widens X, or evaluates the fused
+// expression X stands for, into it and synchronizes).
 template <int M, int K, int LPR, int ROWS, bool STAGED, class T>
-__device__ __forceinline__ void stream_linear(const T* __restrict__ x, float* xs, const T* __restrict__ w, const T* __restrict__ bias,
+__device__ __forceinline__ void stream_linear(const T* __restrict__ x, const float* xs, const T* __restrict__ w, const T* __restrict__ bias,
                                               T* __restrict__ out, uint32_t n) {
-    if constexpr (STAGED) {
-        stage_rows<M, K, T>(x, xs);
-    }
     const uint32_t waves_per_block = blockDim.x / kWave;
     const uint32_t wave = blockIdx.x * waves_per_block + threadIdx.x / kWave;
     stream_rows<M, K, LPR, ROWS, STAGED, T>(x, xs, w, bias, out, n, n, wave, gridDim.x * waves_per_block);
@@ -256,22 +246,117 @@ __device__ __forceinline__ void stream_linear(const T* __restrict__ x, float* xs
 // reading the chosen expert's [C, K] slab in place (the reference's expert_linear,
 // chroma/_src/codegen/cpu/kernels.h:76-99). Indices wrap when negative; an index outside
 // [-experts, experts) raises the error word and reads expert 0. grid.y enumerates the slots.
+// With STAGED, ``xs`` already holds this slot's input row (K floats, written by the caller).
 template <int K, int LPR, int ROWS, bool STAGED, class T, bool PER_SLOT_INPUT>
 __device__ __forceinline__ void stream_expert_linear(const T* __restrict__ w, const int64_t* __restrict__ indices, const T* __restrict__ x,
-                                                     float* xs, T* __restrict__ out, uint32_t selected, uint32_t experts, uint32_t channels,
+                                                     const float* xs, T* __restrict__ out, uint32_t selected, uint32_t experts, uint32_t channels,
                                                      uint32_t blocks_per_slot, unsigned int* error) {
     const uint32_t slot = blockIdx.y;
     const uint32_t token = slot / selected;
     const uint64_t expert = checked_index(indices[slot], experts, true, error);
     const T* slab = w + expert * uint64_t(channels) * K;
-    const T* row = x + uint64_t(PER_SLOT_INPUT ? slot : token) * K;
-    if constexpr (STAGED) {
-        stage_rows<1, K, T>(row, xs);
-    }
+    const T* row = STAGED ? x : x + uint64_t(PER_SLOT_INPUT ? slot : token) * K;
     const uint32_t waves_per_block = blockDim.x / kWave;
     const uint32_t wave = blockIdx.x * waves_per_block + threadIdx.x / kWave;
     stream_rows<1, K, LPR, ROWS, STAGED, T>(row, xs, slab, nullptr, out + uint64_t(slot) * channels, channels, channels, wave,
                                             blocks_per_slot * waves_per_block);
+}
+
+// Mixture-of-experts router for one token row per workgroup: logits[e] = x . W[e] (+ bias[e])
+// for E <= 64 experts, rounded to the storage type and written out; then the reference's top-k (k
+// rounds of a wave argmax over keys that rank NaN highest and break ties toward the lower index, sorted,
+// chroma/_src/codegen/gpu.py:300-337) writes values and int64 indices; then the softmax of the k chosen
+// values (float max, exp, sum, division; rounded) is written too. ``xs`` holds the row (K floats).
+//
+// The logits are LPR-lane dot products over 16-byte chunks of W (all of a step's chunks requested before
+// any arithmetic), 64 / LPR experts per step; LPR == 0 means rows that are not whole chunks (a scalar
+// wave-wide loop instead).
+template <int E, int K, int LPR, bool LARGEST, class T>
+__device__ __forceinline__ void router_row(const float* xs, const T* __restrict__ w, const T* __restrict__ bias, T* __restrict__ logits,
+                                           T* __restrict__ values, int64_t* __restrict__ indices, T* __restrict__ weights, uint32_t k) {
+    static_assert(E <= kWave, "one expert per lane");
+    __shared__ float logit_s[E];
+    const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
+    if constexpr (LPR > 0) {
+        using C = Chunk16<T>;
+        constexpr int PER_LANE = K / C::N / LPR;
+        constexpr int G = kWave / LPR;
+        const uint32_t group = lane / LPR, sub = lane % LPR;
+        for (uint32_t e0 = wave * G; e0 < uint32_t(E); e0 += waves * G) {
+            const uint32_t e = e0 + group;
+            const uint32_t safe = e < uint32_t(E) ? e : uint32_t(E) - 1u;
+            u32x4_t chunks[PER_LANE];
+#pragma unroll
+            for (int c = 0; c < PER_LANE; ++c) {
+                chunks[c] = C::load(w + size_t(safe) * K + (c * LPR + sub) * C::N);
+            }
+            float partial = 0.0f;
+#pragma unroll
+            for (int c = 0; c < PER_LANE; ++c) {
+#pragma unroll
+                for (int i = 0; i < C::N; ++i) {
+                    partial += C::get(chunks[c], i) * xs[(c * LPR + sub) * C::N + i];
+                }
+            }
+#pragma unroll
+            for (int offset = LPR / 2; offset > 0; offset >>= 1) {
+                partial += __shfl_xor(partial, offset, kWave);
+            }
+            if (sub == 0 && e < uint32_t(E)) {
+                logit_s[e] = partial;
+            }
+        }
+    } else {
+        for (uint32_t e = wave; e < uint32_t(E); e += waves) {
+            float partial = 0.0f;
+            for (uint32_t i = lane; i < uint32_t(K); i += kWave) {
+                partial += xs[i] * load1<T>(w + size_t(e) * K + i);
+            }
+            partial = wave_sum(partial);
+            if (lane == 0) {
+                logit_s[e] = partial;
+            }
+        }
+    }
+    __syncthreads();
+    if (wave != 0) {
+        return;  // the first wave selects; no barrier follows
+    }
+    const float mine = lane < uint32_t(E) ? logit_s[lane] : 0.0f;
+    float logit = 0.0f;
+    uint64_t key = 0;
+    if (lane < uint32_t(E)) {
+        const float b = bias ? load1<T>(bias + lane) : 0.0f;
+        store1<T>(logits + lane, mine + b);
+        logit = load1<T>(logits + lane);  // the rounded logit, as stored
+        key = topk_key(logit, lane, LARGEST);
+    }
+    float chosen[E];
+    for (uint32_t s = 0; s < k; ++s) {
+        const uint64_t top = wave_max_u64(key);
+        const uint32_t winner = 0xffffffffu - uint32_t(top);
+        chosen[s] = __shfl(logit, int(winner), kWave);
+        if (lane == winner) {
+            key = 0;
+        }
+        if (lane == 0) {
+            store1<T>(values + s, chosen[s]);
+            indices[s] = int64_t(winner);
+        }
+    }
+    if (lane == 0) {
+        float peak = -__builtin_inff();
+        for (uint32_t s = 0; s < k; ++s) {
+            peak = __builtin_fmaxf(peak, chosen[s]);
+        }
+        float total = 0.0f;
+        for (uint32_t s = 0; s < k; ++s) {
+            total += fast_exp(chosen[s] - peak);
+        }
+        for (uint32_t s = 0; s < k; ++s) {
+            store1<T>(weights + s, fast_exp(chosen[s] - peak) / total);
+        }
+    }
 }
 
 // General product for larger M: 64 x 64 output tiles, K staged through LDS 16 at a time, each of the
