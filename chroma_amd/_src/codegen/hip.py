@@ -56,6 +56,7 @@ MATRIX_MIN_WORK = 1 << 18  # smaller batched products stay on the generic contra
 GROUPED_SLOTS = 64  # from this many (token, expert) slots on, expert products are grouped by expert
 MATRIX_ATTENTION_TOKENS = 64  # bfloat16 attention over at least this many queries runs on the matrix cores
 SPLIT_KEYS = 256  # keys per workgroup when an attention row's keys are split over workgroups
+WAVE_ATTENTION_KEYS = 1024  # up to this many keys, attention runs one wave per query head
 STREAM_BLOCKS = 2048  # workgroups of a weight-streaming product (4-8 per compute unit keep HBM busy)
 STAGED_FLOATS = 8192  # X rows up to this many floats are widened into LDS once per workgroup
 STAGED_ROWS = 4096  # new key/value rows of an attention up to this many floats are evaluated into LDS once
@@ -1115,7 +1116,13 @@ class HIPCodegen(Codegen):
                 return out
         splits = -(-keys // SPLIT_KEYS) if keys > 4 * SPLIT_KEYS and tokens * kv_heads < 64 else 1
         inputs = [v for v in (q, k_past, k_new, v_past, v_new, mask, sinks) if v is not None]
-        if splits == 1:
+        if splits == 1 and keys <= WAVE_ATTENTION_KEYS and dim <= 64 and group <= 16:
+            # Short key ranges: one wave per query head, wave-level reductions only.
+            k, _, _ = self._attention_kernel(out, q, k_past, k_new, v_past, v_new, mask, sinks, None)
+            k.line(f"chroma::attention_waves<{dim}, {group}, {str(bf16).lower()}>({keys}u, {float_literal(scale)}, "
+                   "load_q, load_k, load_v, load_mask, load_sink, store);")
+            self.launch(k, (tokens, kv_heads, 1), 64 * group, inputs, kind="attention")
+        elif splits == 1:
             k, split, _ = self._attention_kernel(out, q, k_past, k_new, v_past, v_new, mask, sinks, None)
             k.line(f"chroma::attention_rows<0, {dim}, {group}, 256, {str(bf16).lower()}>(0u, {keys}u, {float_literal(scale)}, "
                    "load_q, load_k, load_v, load_mask, load_sink, store, chroma::AttentionSplit{nullptr, nullptr, 1u, 0u});")

@@ -249,6 +249,70 @@ __device__ __forceinline__ void attention_rows(uint32_t begin, uint32_t end, flo
     }
 }
 
+// One query row and one key/value head per workgroup with one wave per query head (blockDim.x = 64 G):
+// for short key ranges the wave's lanes split the keys and every reduction is a wave butterfly, so the
+// workgroup synchronizes only once, after the query rows are staged. Same numerics as attention_rows.
+template <int D, int G, bool BF16, class LoadQ, class LoadK, class LoadV, class LoadMask, class LoadSink, class Store>
+__device__ __forceinline__ void attention_waves(uint32_t keys, float scale, LoadQ load_q, LoadK load_k, LoadV load_v, LoadMask load_mask,
+                                                LoadSink load_sink, Store store) {
+    __shared__ float q_s[G][D];
+    const uint32_t tid = threadIdx.x, lane = tid % kWave, g = tid / kWave;
+    const float neg_inf = -__builtin_inff();
+    for (uint32_t i = tid; i < uint32_t(G * D); i += blockDim.x) {
+        q_s[i / D][i % D] = load_q(i / D, i % D);
+    }
+    __syncthreads();
+    float q[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        q[d] = q_s[g][d];
+    }
+    auto score = [&](uint32_t j) -> float {
+        float dot = 0.0f;
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            dot += q[d] * load_k(j, d);
+        }
+        const float s = storage_round<BF16>(dot);
+        const float s1 = storage_round<BF16>(s * scale);
+        return storage_round<BF16>(s1 + load_mask(j, g));
+    };
+    float peak = neg_inf, total = 0.0f;
+    for (uint32_t j = lane; j < keys; j += kWave) {
+        softmax_stats_add(peak, total, score(j));
+    }
+#pragma unroll
+    for (int offset = 1; offset < kWave; offset <<= 1) {
+        softmax_stats_merge(peak, total, __shfl_xor(peak, offset, kWave), __shfl_xor(total, offset, kWave));
+    }
+    softmax_stats_add(peak, total, load_sink(g));
+    float acc[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        acc[d] = 0.0f;
+    }
+    for (uint32_t j = lane; j < keys; j += kWave) {
+        const float p = storage_round<BF16>(fast_exp(score(j) - peak) / total);
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            acc[d] += p * load_v(j, d);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+#pragma unroll
+        for (int offset = 1; offset < kWave; offset <<= 1) {
+            acc[d] += __shfl_xor(acc[d], offset, kWave);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        if (lane == uint32_t(d) % kWave) {
+            store(g, d, acc[d]);
+        }
+    }
+}
+
 // The split-key result: out(g, d) = sum over splits, in split order, of the partial p . v sums.
 template <int D, int G, class Store>
 __device__ __forceinline__ void attention_combine(const float* partial, uint32_t splits, Store store) {
