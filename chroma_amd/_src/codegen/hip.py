@@ -21,7 +21,7 @@ from __future__ import annotations
 import hashlib
 import math
 from dataclasses import dataclass, field
-from typing import Callable, Dict, Iterator, List, Optional, Sequence, Tuple, Union
+from typing import Callable, Dict, Iterator, List, Optional, Sequence, Set, Tuple, Union
 
 import torch
 
@@ -41,6 +41,10 @@ MAX_GRID = 16384
 # Elementwise (map and concatenation) kernels launch one thread per vector up to this many workgroups,
 # so no thread walks a grid-stride loop and every load of the launch can be in flight at once.
 MAP_GRID = 1 << 20
+# Elementwise results of at most this many vectors with an outermost extent up to this many launch one
+# workgroup row per outermost index.
+SPLIT_MAP_VECTORS = 4096
+SPLIT_MAP_ROWS = 1024
 # Row kernels: threads per row for rows of at least 2048 elements (smaller rows use one wave), the most
 # elements a thread keeps in registers for a single-pass row, and whether results that nothing in the
 # same kernel reads again are written with non-temporal (streaming) stores.
@@ -52,6 +56,8 @@ FUSED_CONCAT_ELEMENTS = 1 << 16  # smaller concatenations are fused into their c
 DEFERRED_ELEMENTS = 1 << 16  # smaller expressions the front end asks to store stay fused instead...
 DEFERRED_SOURCES = 4  # ...when they read at most this many buffers (a residual stream is stored every few adds)
 REUSED_EVALUATIONS = 1 << 18  # a contraction operand is stored when (elements x reuse) reaches this
+SMALL_REDUCTION = 8  # contractions summing at most this many products are fused expressions...
+SMALL_OPERAND_COST = 8  # ...over operands that cost at most this much per element (others are stored)
 MATRIX_MIN_WORK = 1 << 18  # smaller batched products stay on the generic contraction kernel
 GROUPED_SLOTS = 64  # from this many (token, expert) slots on, expert products are grouped by expert
 MATRIX_ATTENTION_TOKENS = 64  # bfloat16 attention over at least this many queries runs on the matrix cores
@@ -110,6 +116,7 @@ class HIPCodegen(Codegen):
         super().__init__()
         self.blas = blas
         self.closures: Dict[str, Closure] = {}
+        self.costs: Dict[str, int] = {}
         self.sources: Dict[str, frozenset] = {}
         self.bindings: Dict[str, Binding] = {}
         self.dtypes: Dict[str, torch.dtype] = {}
@@ -125,11 +132,19 @@ class HIPCodegen(Codegen):
         self.skinny_matmuls = 0
         self.mfma_matmuls = 0
         self.fused_attentions = 0
+        self.small_contractions = 0
         self.live_block_tables: Dict[tuple, Value] = {}
         self.pending_norms: Dict[str, tuple] = {}  # deferred RMSNorm value -> (meta, x, weight, epsilon)
         self.pending_of: Dict[str, frozenset] = {}  # value -> deferred norms its expression reads
         self.retractable: Dict[str, tuple] = {}  # small linear output -> (launch index, x, weight, bias)
         self.router_weights: Dict[str, Value] = {}  # top-k values -> their softmax, written by the router
+        # Write-through stores: a small expression the front end asks to store gets its arena buffer at
+        # once, but the buffer is written by the first kernel that reads it. A staging kernel computes the
+        # expression itself and also stores it; any other reader has a copy kernel launched before it.
+        self.store_expressions: Dict[str, Value] = {}  # arena buffer -> the expression it holds
+        self.pending_stores: Set[str] = set()  # buffers not written yet
+        self.resolved_by_launch: Dict[int, List[str]] = {}  # launch index -> buffers that launch writes
+        self.write_through_stores = 0
         self.folded_norms = 0
         self.fused_routers = 0
 
@@ -158,9 +173,11 @@ class HIPCodegen(Codegen):
         return Value(name, shape, meta.dtype, root.deps, stored=True, view=View(root, contiguous_strides(shape), offset))
 
     # ================================================================================= expressions
-    def expr(self, meta: torch.Tensor, closure: Closure, inputs: Sequence[Value]) -> Value:
+    def expr(self, meta: torch.Tensor, closure: Closure, inputs: Sequence[Value], cost: Optional[int] = None) -> Value:
         name = f"e{next(self.counter)}"
         self.closures[name] = closure
+        # rough count of the loads and operations one element costs (stored inputs count one load)
+        self.costs[name] = cost if cost is not None else 1 + sum(self.cost(v) for v in inputs)
         self.sources[name] = frozenset().union(*(self.sources[v.name] for v in inputs)) if inputs else frozenset()
         pending = frozenset().union(*(self.pending_of.get(v.name, frozenset()) for v in inputs)) if inputs else frozenset()
         if pending:
@@ -170,14 +187,25 @@ class HIPCodegen(Codegen):
             return self.store(value)
         return value
 
+    def cost(self, value: Value) -> int:
+        return 1 if value.stored else self.costs.get(value.name, 1)
+
     def read(self, k: Kernel, value: Value, coords: Sequence[Aff]) -> tuple:
         """The node for ``value`` at ``coords`` (one affine coordinate per dimension)."""
+        staged = k.staged_values.get(value.name)
+        if staged is not None:
+            return ("lds", staged, Kernel.flatten(coords, _shape(value.shape)) if value.shape else ZERO)
         if value.stored:
             root, view = value.root, value.view
             address = Aff((), view.offset)
             for coord, stride, size in zip(coords, view.strides, value.shape):
                 if size != 1 and stride:
                     address = address + coord.scale(stride)
+            expression = k.unstored.get(root.name)
+            if expression is not None:
+                if value.name == root.name:
+                    return self.read(k, expression, coords)
+                return self.read(k, expression, k.unflatten(address, expression.shape))
             return ("ld", k.slot(root.name, root.dtype, extent=self.extents[root.name]), value.dtype, address)
         key = (value.name, tuple(coords))
         node = k.values.get(key)
@@ -187,7 +215,7 @@ class HIPCodegen(Codegen):
         return node
 
     def read_flat(self, k: Kernel, value: Value, flat: Aff) -> tuple:
-        if value.stored and value.view.base is None:
+        if value.stored and value.view.base is None and value.name not in k.unstored:
             return ("ld", k.slot(value.name, value.dtype, extent=self.extents[value.name]), value.dtype, flat)
         return self.read(k, value, k.unflatten(flat, value.shape))
 
@@ -216,7 +244,19 @@ class HIPCodegen(Codegen):
             return value  # consumers that stage their rows fold it; any other reader stores it
         if math.prod(value.shape) <= DEFERRED_ELEMENTS and len(self.sources[value.name]) <= DEFERRED_SOURCES:
             return value
+        if self.blas and value.name in self.closures and value.name not in self.materialized and math.prod(value.shape) <= STAGED_FLOATS:
+            out = self.allocate(value.shape, value.dtype)
+            self.materialized[value.name] = out
+            self.store_expressions[out.name] = value
+            self.pending_stores.add(out.name)
+            return out
         return self.store(value)
+
+    def _flush_store(self, buffer: str) -> None:
+        """Write a pending write-through buffer with a copy kernel (launched before its reader)."""
+        self.pending_stores.discard(buffer)
+        value = self.store_expressions[buffer]
+        self.map_kernel(self.materialized[value.name], value)
 
     def store(self, value: Value) -> Value:
         """Write ``value`` to a fresh arena allocation (once; later requests reuse it)."""
@@ -358,6 +398,9 @@ class HIPCodegen(Codegen):
 
         Kernels are named ``chroma_<kind>_<hash of their source>`` so profiles stay readable and
         stable across programs."""
+        for buffer in list(k.slots):
+            if buffer in self.pending_stores and buffer not in k.unstored:
+                self._flush_store(buffer)
         source = k.render("KERNEL_NAME", block, prologue)
         name = self.kernel_names.get(source)
         if name is None:
@@ -376,6 +419,8 @@ class HIPCodegen(Codegen):
                 allocation.end = max(allocation.end, self.kernels)
         self.record_usage(inputs)
         self.launches.append(Launch(name, grid3, block, bindings, shared))
+        if k.resolved_stores:
+            self.resolved_by_launch[len(self.launches) - 1] = list(k.resolved_stores)
         self.kernels += 1
 
     def map_kernel(self, out: Value, value: Value, target: Optional[str] = None) -> None:
@@ -388,22 +433,32 @@ class HIPCodegen(Codegen):
         k.streaming_loads = STREAMING_BYTES if k.streaming else 0
         slot = k.slot(target or out.name, value.dtype, writable=True, extent=self.extents[target or out.name])
         vectors = count // lanes
+        vshape = shape[:-1] + (shape[-1] // lanes,)
+        # A small result gets one workgroup per outermost index: that index is then uniform, so a
+        # concatenation along it (stacked per-layer results) evaluates one part per workgroup instead of
+        # every part in one wave.
+        split = len(shape) > 1 and 1 < shape[0] <= SPLIT_MAP_ROWS and vectors <= SPLIT_MAP_VECTORS
+        if split:
+            outer = Aff.of(k.atom("blockIdx.y", shape[0] - 1))
+            vshape = vshape[1:]
+            vectors //= shape[0]
         wide = vectors > 2**31 - 1
         itype = "uint64_t" if wide else "uint32_t"
         loop = f"for ({itype} v = {itype}(blockIdx.x) * {MAP_THREADS}u + threadIdx.x; v < {vectors}u; v += {itype}(gridDim.x) * {MAP_THREADS}u) {{"
         with k.block(loop):
             v = Atom("v", vectors - 1)
-            vshape = shape[:-1] + (shape[-1] // lanes,)
-            coords = k.unflatten(Aff.of(v), vshape)
+            coords = ([outer] if split else []) + k.unflatten(Aff.of(v), vshape)
             if lanes > 1:
                 coords[-1] = Aff.of(k.vector_atom(f"({coords[-1].code()}) * {lanes}u", shape[-1] - 1))
             node = self.read(k, value, coords if value.shape else coords[:0])
             k.store(slot, value.dtype, Kernel.flatten(coords, shape), node)
         grid = max(1, min(-(-vectors // MAP_THREADS), MAP_GRID))
-        self.launch(k, grid, MAP_THREADS, [value], kind="map")
+        self.launch(k, (grid, shape[0], 1) if split else grid, MAP_THREADS, [value], kind="map")
 
     # ==================================================================================== outputs
     def output(self, index: int, value: Value) -> None:
+        if value.stored and value.root.name in self.pending_stores:
+            self._flush_store(value.root.name)
         if self.promote_output(index, value):
             return
         name = f"output{index}"
@@ -714,6 +769,48 @@ class HIPCodegen(Codegen):
         fused expressions are read in place). Deferred norms that ``x`` depends on get their row scales
         computed first. Ends with a workgroup barrier."""
         waves = threads // 64
+        resolved = []
+        for buffer in sorted((self.sources[x.name] & self.pending_stores) - set(k.slots)):
+            # ``x`` reads a write-through buffer nothing has written yet: this kernel evaluates its
+            # expression wherever it would load it, and the first workgroup also stores it. (A buffer
+            # the kernel already reads through a pointer is left to the copy kernel instead.)
+            k.unstored[buffer] = self.store_expressions[buffer]
+            k.resolved_stores.append(buffer)
+            self.pending_stores.discard(buffer)
+            resolved.append(buffer)
+            self.write_through_stores += 1
+        # A deferred norm over a computed operand (an expression, or a buffer computed in place) reads
+        # it twice (squares, then scaling): the operand's rows are evaluated once into LDS instead.
+        staged_sources = False
+        for name in sorted(self.pending_of.get(x.name, frozenset())):
+            if name in self.materialized:
+                continue
+            source = self.pending_norms[name][1]
+            computed = not source.stored or source.root.name in k.unstored
+            count = math.prod(_shape(source.shape))
+            if not computed or source.name in k.staged_values or count > STAGED_FLOATS:
+                continue
+            rows_array = k.fresh("hs")
+            k.line(f"__shared__ float {rows_array}[{count}];")
+            k.line("#pragma unroll 4")
+            with k.block(f"for (uint32_t i = threadIdx.x; i < {count}u; i += {threads}u) {{"):
+                i = Aff.of(Atom("i", count - 1))
+                k.line(f"{rows_array}[i] = {k.emit(self.read(k, source, k.unflatten(i, _shape(source.shape)) if source.shape else []))};")
+            k.staged_values[source.name] = rows_array
+            staged_sources = True
+        if staged_sources:
+            k.line("__syncthreads();")
+        for buffer in resolved:
+            expression = k.unstored[buffer]
+            shape = _shape(expression.shape)
+            count = math.prod(shape)
+            slot = k.slot(buffer, expression.dtype, writable=True, extent=self.extents[buffer])
+            with k.block("if (blockIdx.x == 0u && blockIdx.y == 0u && blockIdx.z == 0u) {"):
+                with k.block(f"for (uint32_t i = threadIdx.x; i < {count}u; i += {threads}u) {{"):
+                    i = Aff.of(Atom("i", count - 1))
+                    target = next((v for v in (buffer, expression.name) if v in k.staged_values), None)
+                    node = ("lds", k.staged_values[target], i) if target else self.read(k, expression, k.unflatten(i, shape) if expression.shape else [])
+                    k.store(slot, expression.dtype, i, node)
         k.norm_scales = {}
         for name in sorted(self.pending_of.get(x.name, frozenset())):
             if name in self.materialized:
@@ -941,6 +1038,8 @@ class HIPCodegen(Codegen):
             return False
         popped = self.launches.pop()
         self.kernels -= 1
+        for buffer in self.resolved_by_launch.pop(len(self.launches), []):
+            self.pending_stores.add(buffer)  # the replacement kernel stages the same operand and writes it
         if all(launch.kernel != popped.kernel for launch in self.launches):
             text = next(src for src, name in self.kernel_names.items() if name == popped.kernel)
             del self.kernel_names[text]
@@ -949,21 +1048,26 @@ class HIPCodegen(Codegen):
         k = Kernel(1)
         row = Aff.of(k.atom("blockIdx.x", rows - 1, prefix="r"))
         lead = tuple(source.shape[:-1])
-        self._stage(k, source, 1, inner, lambda _r: k.unflatten(row, lead) if lead else [], 256)
         ctype = ctype_of(x.dtype)
         w_arg = self._matrix_slot(k, weight)
+        per_chunk = 16 // ITEMSIZE[x.dtype]
+        chunks = inner // per_chunk if inner % per_chunk == 0 else 0
+        lanes = next((l for l in (64, 32, 16, 8, 4, 2) if chunks and chunks % l == 0 and chunks // l >= 4), 1 if chunks else 0)
+        if lanes:
+            # the gate weights are requested before the prologue that stages the row
+            k.line(f"chroma::StreamStep<{inner}, {lanes}, 1, {ctype}> prefetched;")
+            k.line(f"chroma::router_fetch<{columns}>(prefetched, {w_arg});")
+        self._stage(k, source, 1, inner, lambda _r: k.unflatten(row, lead) if lead else [], 256)
         b_arg = self._matrix_slot(k, bias) if bias is not None else "nullptr"
         logits = k.slot(x.name, x.dtype, writable=True, extent=self.extents[x.name])
         value_slot = k.slot(values.name, values.dtype, writable=True, extent=self.extents[values.name])
         index_slot = k.slot(indices.name, indices.dtype, writable=True, extent=self.extents[indices.name])
         weight_slot = k.slot(weights.name, weights.dtype, writable=True, extent=self.extents[weights.name])
         r = row.code()
-        per_chunk = 16 // ITEMSIZE[x.dtype]
-        chunks = inner // per_chunk if inner % per_chunk == 0 else 0
-        lanes = next((l for l in (64, 32, 16, 8, 4, 2) if chunks and chunks % l == 0 and chunks // l >= 4), 1 if chunks else 0)
         k.line(
             f"chroma::router_row<{columns}, {inner}, {lanes}, {str(bool(largest)).lower()}, {ctype}>(xs, {w_arg}, {b_arg}, {logits} + {r} * {columns}u, "
-            f"{value_slot} + {r} * {count}u, {index_slot} + {r} * {count}u, {weight_slot} + {r} * {count}u, {count}u);"
+            f"{value_slot} + {r} * {count}u, {index_slot} + {r} * {count}u, {weight_slot} + {r} * {count}u, {count}u"
+            + (", prefetched);" if lanes else ");")
         )
         self.launch(k, rows, 256, [source, weight] + ([bias] if bias is not None else []), kind="router")
         self.router_weights[values.name] = weights
@@ -1007,6 +1111,8 @@ class HIPCodegen(Codegen):
     def _matrix_slot(self, k: Kernel, value: Value) -> str:
         """A pointer to a stored, row-major value (an alias is rebased onto its root at its offset)."""
         root = value.root
+        if root.name in k.unstored:
+            raise AssertionError(f"{root.name} is computed in place by this kernel and has no stored copy to point at")
         slot = k.slot(root.name, root.dtype)
         offset = value.view.offset
         return f"({slot} + {offset}u)" if offset else slot
@@ -1042,10 +1148,13 @@ class HIPCodegen(Codegen):
         b_arg = self._matrix_slot(k, bias) if bias is not None else "nullptr"
         out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
         lead = tuple(x.shape[:-1])
+        # The first step of W is requested before the prologue, so the weight read overlaps it.
+        k.line(f"chroma::StreamStep<{inner}, {lanes}, {steps}, {ctype_of(out.dtype)}> prefetched;")
+        k.line(f"chroma::stream_linear_fetch(prefetched, {w_arg}, {columns}u);")
         self._stage(k, x, rows, inner, lambda row: k.unflatten(row, lead) if lead else [], 256)
         k.line(
             f"chroma::stream_linear<{rows}, {inner}, {lanes}, {steps}, true, {ctype_of(out.dtype)}>("
-            f"nullptr, xs, {w_arg}, {b_arg}, {out_slot}, {columns}u);"
+            f"nullptr, xs, {w_arg}, {b_arg}, {out_slot}, {columns}u, prefetched);"
         )
         self.launch(k, blocks, 256, [x, weight] + ([bias] if bias is not None else []), kind="linear_stream")
 
@@ -1337,6 +1446,14 @@ class HIPCodegen(Codegen):
         expert = self._expert_einsum(meta, eqn, labels, sizes, values)
         if expert is not None:
             return expert
+        width = math.prod(sizes[letter] for letter in reduction)
+        small = len(values) == 2 and meta.dtype in (torch.float32, torch.bfloat16) and width <= SMALL_REDUCTION
+        if small:
+            # Each output reads ``width`` elements of each operand: an operand whose evaluation costs
+            # more than a few loads and operations (such as another small contraction) is stored
+            # first, so that chains of small contractions never multiply their re-evaluations.
+            operands = [v if width == 1 or self.cost(v) <= SMALL_OPERAND_COST else self.store(v) for v in values]
+            return self._small_contraction(meta, labels, output, sizes, reduction, operands)
         matrix = self._matrix_einsum(meta, labels, output, sizes, reduction, values)
         if matrix is not None:
             return matrix
@@ -1348,6 +1465,39 @@ class HIPCodegen(Codegen):
                 value = self.store(value)
             prepared.append(value)
         return self._loop_einsum(meta, labels, output, sizes, reduction, prepared)
+
+    def _small_contraction(self, meta, labels, output, sizes, reduction, values) -> Value:
+        """A contraction over at most ``SMALL_REDUCTION`` summed positions (an outer product such as
+        position x inverse frequency, or the weighted sum of the selected experts' outputs) as an
+        elementwise expression that fuses into its consumers instead of a launch of its own. Each output
+        is ``((0 + a0*b0) + a1*b1) + ...`` in the accumulating loop's order (summed labels in sorted order,
+        row-major) and rounded once, so it equals the loop kernel's result bit for bit (a negative-zero
+        product still comes out as +0)."""
+        bf16 = meta.dtype == torch.bfloat16
+        reduce_shape = [sizes[letter] for letter in reduction]
+        steps = []
+        for r in range(math.prod(reduce_shape)):
+            digits = []
+            for size in reversed(reduce_shape):
+                digits.append(r % size)
+                r //= size
+            steps.append(dict(zip(reduction, [Aff((), d) for d in reversed(digits)])))
+
+        def closure(k: Kernel, coords: List[Aff]) -> tuple:
+            node = ("f", 0.0)
+            for step in steps:
+                by_label = dict(zip(output, coords))
+                by_label.update(step)
+                factors = [
+                    self.read(k, value, [ZERO if size == 1 else by_label[letter] for letter, size in zip(label, value.shape)])
+                    for label, value in zip(labels, values)
+                ]
+                node = ("bin", "add", node, ("bin", "mul", factors[0], factors[1]))
+            return ("rnd", node) if bf16 else node
+
+        self.small_contractions += 1
+        cost = len(steps) * (2 + sum(self.cost(v) for v in values))
+        return self.expr(meta, closure, list(values), cost=cost)
 
     def _expert_einsum(self, meta, eqn, labels, sizes, values) -> Optional[Value]:
         if not self.blas or eqn not in ("beck,bk->bec", "beck,bek->bec"):
@@ -1388,10 +1538,12 @@ class HIPCodegen(Codegen):
                 coords_of = lambda _row: [k.div(slot, selected), k.mod(slot, selected)]
             else:
                 coords_of = lambda _row: [k.div(slot, selected)]
+            k.line(f"chroma::StreamStep<{inner}, {lanes}, {steps}, {ctype_of(out.dtype)}> prefetched;")
+            k.line(f"chroma::stream_expert_fetch(prefetched, {w}, {idx}, {experts}u, {channels}u, error);")
             self._stage(k, x, 1, inner, coords_of, 256)
             k.line(
                 f"chroma::stream_expert_linear<{inner}, {lanes}, {steps}, true, {ctype_of(out.dtype)}, {per_expert}>("
-                f"{w}, {idx}, nullptr, xs, {out_slot}, {selected}u, {experts}u, {channels}u, {blocks_per_slot}u, error);"
+                f"{w}, {idx}, nullptr, xs, {out_slot}, {selected}u, {experts}u, {channels}u, {blocks_per_slot}u, error, prefetched);"
             )
             self.launch(k, (blocks_per_slot, tokens * selected, 1), 256, [weight, indices, x], kind="expert_stream")
             self.expert_contractions += 1
@@ -1628,6 +1780,8 @@ class HIPCodegen(Codegen):
             mfma_matmuls=self.mfma_matmuls,
             fused_attentions=self.fused_attentions,
             fused_routers=self.fused_routers,
+            small_contractions=self.small_contractions,
+            write_through_stores=self.write_through_stores,
             unique_kernels=len(self.kernel_sources),
             launches=len(self.launches),
         )

@@ -192,6 +192,13 @@ class Kernel:
         self.load_replay: Optional[Iterator[str]] = None
         self.load_index = "c"
         self.shared: List[str] = []
+        # Arena buffers this kernel computes from their expressions instead of loading (buffer -> Value),
+        # and the subset whose stores this kernel performs.
+        self.unstored: Dict[str, object] = {}
+        self.resolved_stores: List[str] = []
+        # Values whose elements this kernel has evaluated into a __shared__ float array (value -> array),
+        # in row-major order; reads of them become LDS reads ("lds" nodes).
+        self.staged_values: Dict[str, str] = {}
 
     # -- parameters ------------------------------------------------------------------------------
     def slot(self, buffer: str, dtype: torch.dtype, writable: bool = False, extent: Optional[int] = None) -> str:
@@ -376,6 +383,16 @@ class Kernel:
             result = f"int64_t({int(node[1])}ll)"
         elif tag == "ld":
             result = self._emit_load(node)
+        elif tag == "lds":
+            _, array, aff = node
+            if aff.varying:
+                result = []
+                for lane in range(self.lanes):
+                    result.append(self.fresh("s"))
+                    self.line(f"const float {result[-1]} = {array}[{aff.code(lane)}];")
+            else:
+                result = self.fresh("s")
+                self.line(f"const float {result} = {array}[{aff.code()}];")
         elif tag == "cmp":
             result = self._emit_compare(node)
         elif tag == "cases":
@@ -449,6 +466,9 @@ class Kernel:
     def _emit_load(self, node: Node) -> Union[str, List[str]]:
         _, slot, dtype, aff = node
         self.check_bounds(slot, aff)
+        if any(buffer in self.slots and self.slots[buffer][0] == slot for buffer in self.unstored):
+            # the first workgroup is writing this buffer during the kernel: a load would race with it
+            raise AssertionError(f"generated load from {slot}, which this kernel computes in place")
         vector = next((a for a, _ in aff.terms if a.vector), None)
         wide = aff.hi() > U32_LIMIT
 

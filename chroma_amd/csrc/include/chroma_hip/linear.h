@@ -3,6 +3,8 @@
 // float32 or bfloat16 storage, float32 accumulation, bias added to the finished sum.
 #pragma once
 
+#include <type_traits>
+
 #include "device.h"
 
 namespace chroma {
@@ -161,14 +163,40 @@ template <> struct Chunk16<uint16_t> {
     }
 };
 
-template <int M, int K, int LPR, int ROWS, bool STAGED, class T>
+// One step of ``stream_rows`` for one lane: its 16-byte chunks of ROWS rows of W, all requested before
+// any arithmetic. A kernel may request its first step before its prologue (see ``stream_linear_fetch``),
+// so the weight read overlaps the evaluation of X into LDS.
+template <int K, int LPR, int ROWS, class T>
+struct StreamStep {
+    static constexpr int N = Chunk16<T>::N;
+    static constexpr int PER_LANE = K / N / LPR;
+    static constexpr int G = kWave / LPR;
+    static_assert(K % N == 0 && (K / N) % LPR == 0, "rows must split into 16-byte chunks per lane");
+    u32x4_t chunks[ROWS][PER_LANE];
+
+    __device__ __forceinline__ void fetch(const T* __restrict__ w, uint32_t base, uint32_t rows) {
+        const uint32_t lane = threadIdx.x % kWave;
+        const uint32_t group = lane / LPR, sub = lane % LPR;
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+            const uint32_t row = base + r * G + group;
+            const uint32_t safe = row < rows ? row : rows - 1;
+#pragma unroll
+            for (int c = 0; c < PER_LANE; ++c) {
+                chunks[r][c] = Chunk16<T>::load(w + size_t(safe) * K + (c * LPR + sub) * N);
+            }
+        }
+    }
+};
+
+template <int M, int K, int LPR, int ROWS, bool STAGED, bool PREFETCHED, class T>
 __device__ __forceinline__ void stream_rows(const T* __restrict__ x, const float* xs, const T* __restrict__ w, const T* __restrict__ bias,
-                                            T* __restrict__ out, uint32_t out_stride, uint32_t rows, uint32_t wave, uint32_t waves) {
+                                            T* __restrict__ out, uint32_t out_stride, uint32_t rows, uint32_t wave, uint32_t waves,
+                                            StreamStep<K, LPR, ROWS, T>* first) {
     using C = Chunk16<T>;
-    constexpr int CHUNKS = K / C::N;
-    constexpr int PER_LANE = CHUNKS / LPR;
-    constexpr int G = kWave / LPR;
-    static_assert(K % C::N == 0 && CHUNKS % LPR == 0, "rows must split into 16-byte chunks per lane");
+    using Step = StreamStep<K, LPR, ROWS, T>;
+    constexpr int PER_LANE = Step::PER_LANE;
+    constexpr int G = Step::G;
     const uint32_t lane = threadIdx.x % kWave;
     const uint32_t group = lane / LPR;
     const uint32_t sub = lane % LPR;
@@ -179,20 +207,19 @@ __device__ __forceinline__ void stream_rows(const T* __restrict__ x, const float
             return load1<T>(x + size_t(m) * K + k);
         }
     };
-    for (uint32_t base = wave * G * ROWS; base < rows; base += waves * G * ROWS) {
+    uint32_t base = wave * G * ROWS;
+    if (base >= rows) {
+        return;
+    }
+    Step local;
+    Step& step = PREFETCHED ? *first : local;  // the prefetched step is used (and refilled) in place
+    if constexpr (!PREFETCHED) {
+        step.fetch(w, base, rows);
+    }
+    for (;;) {
         // Keep X's values from being hoisted out of this loop: they would take K registers per lane
         // (LDS or cache reads are cheap to repeat; registers are needed for the chunks in flight).
         __asm__ volatile("" ::: "memory");
-        u32x4_t chunks[ROWS][PER_LANE];
-#pragma unroll
-        for (int r = 0; r < ROWS; ++r) {
-            const uint32_t row = base + r * G + group;
-            const uint32_t safe = row < rows ? row : rows - 1;
-#pragma unroll
-            for (int c = 0; c < PER_LANE; ++c) {
-                chunks[r][c] = C::load(w + size_t(safe) * K + (c * LPR + sub) * C::N);
-            }
-        }
 #pragma unroll
         for (int r = 0; r < ROWS; ++r) {
             float acc[M];
@@ -205,7 +232,7 @@ __device__ __forceinline__ void stream_rows(const T* __restrict__ x, const float
                 const uint32_t k0 = (c * LPR + sub) * C::N;
 #pragma unroll
                 for (int e = 0; e < C::N; ++e) {
-                    const float wv = C::get(chunks[r][c], e);
+                    const float wv = C::get(step.chunks[r][c], e);
 #pragma unroll
                     for (int m = 0; m < M; ++m) {
                         acc[m] += wv * xv(m, k0 + e);
@@ -228,29 +255,66 @@ __device__ __forceinline__ void stream_rows(const T* __restrict__ x, const float
                 }
             }
         }
+        base += waves * G * ROWS;
+        if (base >= rows) {
+            break;
+        }
+        step.fetch(w, base, rows);
     }
 }
 
 // Y = X . W^T (+ bias) for M <= 16 rows of X through ``stream_rows``; with STAGED, ``xs`` is an LDS array of
 // M * K floats that already holds X (the caller's generated code widens X, or evaluates the fused
-// expression X stands for, into it and synchronizes).
+// expression X stands for, into it and synchronizes). With ``first``, this wave's first step was
+// requested by ``stream_linear_fetch`` before the prologue.
+template <int K, int LPR, int ROWS, class T>
+__device__ __forceinline__ void stream_linear_fetch(StreamStep<K, LPR, ROWS, T>& first, const T* __restrict__ w, uint32_t n) {
+    const uint32_t wave = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+    const uint32_t base = wave * StreamStep<K, LPR, ROWS, T>::G * ROWS;
+    if (base < n) {
+        first.fetch(w, base, n);
+    }
+}
+
 template <int M, int K, int LPR, int ROWS, bool STAGED, class T>
 __device__ __forceinline__ void stream_linear(const T* __restrict__ x, const float* xs, const T* __restrict__ w, const T* __restrict__ bias,
                                               T* __restrict__ out, uint32_t n) {
     const uint32_t waves_per_block = blockDim.x / kWave;
     const uint32_t wave = blockIdx.x * waves_per_block + threadIdx.x / kWave;
-    stream_rows<M, K, LPR, ROWS, STAGED, T>(x, xs, w, bias, out, n, n, wave, gridDim.x * waves_per_block);
+    stream_rows<M, K, LPR, ROWS, STAGED, false, T>(x, xs, w, bias, out, n, n, wave, gridDim.x * waves_per_block, nullptr);
+}
+
+// (The prefetched step is passed by reference and never compared with null: a private-memory address
+// in a comparison keeps the step out of registers.)
+template <int M, int K, int LPR, int ROWS, bool STAGED, class T>
+__device__ __forceinline__ void stream_linear(const T* __restrict__ x, const float* xs, const T* __restrict__ w, const T* __restrict__ bias,
+                                              T* __restrict__ out, uint32_t n, StreamStep<K, LPR, ROWS, T>& first) {
+    const uint32_t waves_per_block = blockDim.x / kWave;
+    const uint32_t wave = blockIdx.x * waves_per_block + threadIdx.x / kWave;
+    stream_rows<M, K, LPR, ROWS, STAGED, true, T>(x, xs, w, bias, out, n, n, wave, gridDim.x * waves_per_block, &first);
 }
 
 // Selected-expert products through ``stream_rows``: out[slot, :] = W[expert(slot)] . x[token or slot]^T,
 // reading the chosen expert's [C, K] slab in place (the reference's expert_linear,
 // chroma/_src/codegen/cpu/kernels.h:76-99). Indices wrap when negative; an index outside
 // [-experts, experts) raises the error word and reads expert 0. grid.y enumerates the slots.
-// With STAGED, ``xs`` already holds this slot's input row (K floats, written by the caller).
-template <int K, int LPR, int ROWS, bool STAGED, class T, bool PER_SLOT_INPUT>
-__device__ __forceinline__ void stream_expert_linear(const T* __restrict__ w, const int64_t* __restrict__ indices, const T* __restrict__ x,
-                                                     const float* xs, T* __restrict__ out, uint32_t selected, uint32_t experts, uint32_t channels,
-                                                     uint32_t blocks_per_slot, unsigned int* error) {
+// With STAGED, ``xs`` already holds this slot's input row (K floats, written by the caller); with
+// ``first``, this wave's first step of the slab was requested by ``stream_expert_fetch``.
+template <int K, int LPR, int ROWS, class T>
+__device__ __forceinline__ void stream_expert_fetch(StreamStep<K, LPR, ROWS, T>& first, const T* __restrict__ w, const int64_t* __restrict__ indices,
+                                                    uint32_t experts, uint32_t channels, unsigned int* error) {
+    const uint64_t expert = checked_index(indices[blockIdx.y], experts, true, error);
+    const uint32_t wave = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+    const uint32_t base = wave * StreamStep<K, LPR, ROWS, T>::G * ROWS;
+    if (base < channels) {
+        first.fetch(w + expert * uint64_t(channels) * K, base, channels);
+    }
+}
+
+template <int K, int LPR, int ROWS, bool STAGED, class T, bool PER_SLOT_INPUT, bool PREFETCHED = false>
+__device__ __forceinline__ void stream_expert_rows(const T* __restrict__ w, const int64_t* __restrict__ indices, const T* __restrict__ x,
+                                                   const float* xs, T* __restrict__ out, uint32_t selected, uint32_t experts, uint32_t channels,
+                                                   uint32_t blocks_per_slot, unsigned int* error, StreamStep<K, LPR, ROWS, T>* first) {
     const uint32_t slot = blockIdx.y;
     const uint32_t token = slot / selected;
     const uint64_t expert = checked_index(indices[slot], experts, true, error);
@@ -258,8 +322,24 @@ __device__ __forceinline__ void stream_expert_linear(const T* __restrict__ w, co
     const T* row = STAGED ? x : x + uint64_t(PER_SLOT_INPUT ? slot : token) * K;
     const uint32_t waves_per_block = blockDim.x / kWave;
     const uint32_t wave = blockIdx.x * waves_per_block + threadIdx.x / kWave;
-    stream_rows<1, K, LPR, ROWS, STAGED, T>(row, xs, slab, nullptr, out + uint64_t(slot) * channels, channels, channels, wave,
-                                            blocks_per_slot * waves_per_block);
+    stream_rows<1, K, LPR, ROWS, STAGED, PREFETCHED, T>(row, xs, slab, nullptr, out + uint64_t(slot) * channels, channels, channels, wave,
+                                                        blocks_per_slot * waves_per_block, first);
+}
+
+template <int K, int LPR, int ROWS, bool STAGED, class T, bool PER_SLOT_INPUT>
+__device__ __forceinline__ void stream_expert_linear(const T* __restrict__ w, const int64_t* __restrict__ indices, const T* __restrict__ x,
+                                                     const float* xs, T* __restrict__ out, uint32_t selected, uint32_t experts, uint32_t channels,
+                                                     uint32_t blocks_per_slot, unsigned int* error) {
+    stream_expert_rows<K, LPR, ROWS, STAGED, T, PER_SLOT_INPUT, false>(w, indices, x, xs, out, selected, experts, channels, blocks_per_slot, error,
+                                                                       nullptr);
+}
+
+template <int K, int LPR, int ROWS, bool STAGED, class T, bool PER_SLOT_INPUT>
+__device__ __forceinline__ void stream_expert_linear(const T* __restrict__ w, const int64_t* __restrict__ indices, const T* __restrict__ x,
+                                                     const float* xs, T* __restrict__ out, uint32_t selected, uint32_t experts, uint32_t channels,
+                                                     uint32_t blocks_per_slot, unsigned int* error, StreamStep<K, LPR, ROWS, T>& first) {
+    stream_expert_rows<K, LPR, ROWS, STAGED, T, PER_SLOT_INPUT, true>(w, indices, x, xs, out, selected, experts, channels, blocks_per_slot, error,
+                                                                      &first);
 }
 
 // Mixture-of-experts router for one token row per workgroup: logits[e] = x . W[e] (+ bias[e])
@@ -271,39 +351,62 @@ __device__ __forceinline__ void stream_expert_linear(const T* __restrict__ w, co
 // The logits are LPR-lane dot products over 16-byte chunks of W (all of a step's chunks requested before
 // any arithmetic), 64 / LPR experts per step; LPR == 0 means rows that are not whole chunks (a scalar
 // wave-wide loop instead).
-template <int E, int K, int LPR, bool LARGEST, class T>
-__device__ __forceinline__ void router_row(const float* xs, const T* __restrict__ w, const T* __restrict__ bias, T* __restrict__ logits,
-                                           T* __restrict__ values, int64_t* __restrict__ indices, T* __restrict__ weights, uint32_t k) {
+template <int E, int K, int LPR, class T>
+__device__ __forceinline__ void router_fetch(StreamStep<K, LPR, 1, T>& first, const T* __restrict__ w) {
+    const uint32_t e0 = threadIdx.x / kWave * StreamStep<K, LPR, 1, T>::G;
+    if (e0 < uint32_t(E)) {
+        first.fetch(w, e0, E);
+    }
+}
+
+// With PREFETCHED (LPR > 0 only), this wave's first step of W was requested into ``first`` by
+// ``router_fetch`` before the prologue that stages the row; the step is then used and refilled in place.
+template <int E, int K, int LPR, bool LARGEST, class T, bool PREFETCHED = false>
+__device__ __forceinline__ void router_rows(const float* xs, const T* __restrict__ w, const T* __restrict__ bias, T* __restrict__ logits,
+                                            T* __restrict__ values, int64_t* __restrict__ indices, T* __restrict__ weights, uint32_t k,
+                                            StreamStep<K, (LPR > 0 ? LPR : 1), 1, T>* first) {
     static_assert(E <= kWave, "one expert per lane");
     __shared__ float logit_s[E];
     const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
     if constexpr (LPR > 0) {
         using C = Chunk16<T>;
-        constexpr int PER_LANE = K / C::N / LPR;
-        constexpr int G = kWave / LPR;
+        using Step = StreamStep<K, LPR, 1, T>;
+        constexpr int PER_LANE = Step::PER_LANE;
+        constexpr int G = Step::G;
         const uint32_t group = lane / LPR, sub = lane % LPR;
-        for (uint32_t e0 = wave * G; e0 < uint32_t(E); e0 += waves * G) {
-            const uint32_t e = e0 + group;
-            const uint32_t safe = e < uint32_t(E) ? e : uint32_t(E) - 1u;
-            u32x4_t chunks[PER_LANE];
-#pragma unroll
-            for (int c = 0; c < PER_LANE; ++c) {
-                chunks[c] = C::load(w + size_t(safe) * K + (c * LPR + sub) * C::N);
+        uint32_t e0 = wave * G;
+        if (e0 < uint32_t(E)) {
+            Step local;
+            Step& step = PREFETCHED ? *first : local;
+            if constexpr (!PREFETCHED) {
+                step.fetch(w, e0, E);
             }
-            float partial = 0.0f;
+            for (;;) {
+                const uint32_t e = e0 + group;
+                float partial = 0.0f;
 #pragma unroll
-            for (int c = 0; c < PER_LANE; ++c) {
+                for (int c = 0; c < PER_LANE; ++c) {
+                    if (c % 8 == 0) {
+                        // read X from LDS a few chunks at a time (all of it at once would not fit in registers)
+                        __asm__ volatile("" ::: "memory");
+                    }
 #pragma unroll
-                for (int i = 0; i < C::N; ++i) {
-                    partial += C::get(chunks[c], i) * xs[(c * LPR + sub) * C::N + i];
+                    for (int i = 0; i < C::N; ++i) {
+                        partial += C::get(step.chunks[0][c], i) * xs[(c * LPR + sub) * C::N + i];
+                    }
                 }
-            }
 #pragma unroll
-            for (int offset = LPR / 2; offset > 0; offset >>= 1) {
-                partial += __shfl_xor(partial, offset, kWave);
-            }
-            if (sub == 0 && e < uint32_t(E)) {
-                logit_s[e] = partial;
+                for (int offset = LPR / 2; offset > 0; offset >>= 1) {
+                    partial += __shfl_xor(partial, offset, kWave);
+                }
+                if (sub == 0 && e < uint32_t(E)) {
+                    logit_s[e] = partial;
+                }
+                e0 += waves * G;
+                if (e0 >= uint32_t(E)) {
+                    break;
+                }
+                step.fetch(w, e0, E);
             }
         }
     } else {
@@ -357,6 +460,19 @@ __device__ __forceinline__ void router_row(const float* xs, const T* __restrict_
             store1<T>(weights + s, fast_exp(chosen[s] - peak) / total);
         }
     }
+}
+
+template <int E, int K, int LPR, bool LARGEST, class T>
+__device__ __forceinline__ void router_row(const float* xs, const T* __restrict__ w, const T* __restrict__ bias, T* __restrict__ logits,
+                                           T* __restrict__ values, int64_t* __restrict__ indices, T* __restrict__ weights, uint32_t k) {
+    router_rows<E, K, LPR, LARGEST, T, false>(xs, w, bias, logits, values, indices, weights, k, nullptr);
+}
+
+template <int E, int K, int LPR, bool LARGEST, class T>
+__device__ __forceinline__ void router_row(const float* xs, const T* __restrict__ w, const T* __restrict__ bias, T* __restrict__ logits,
+                                           T* __restrict__ values, int64_t* __restrict__ indices, T* __restrict__ weights, uint32_t k,
+                                           StreamStep<K, LPR, 1, T>& first) {
+    router_rows<E, K, LPR, LARGEST, T, true>(xs, w, bias, logits, values, indices, weights, k, &first);
 }
 
 // General product for larger M: 64 x 64 output tiles, K staged through LDS 16 at a time, each of the
