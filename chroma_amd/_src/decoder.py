@@ -29,6 +29,7 @@ from typing import Any, Iterator, List, Optional, Sequence, Tuple
 
 import numpy as np
 
+from chroma_amd._src import host
 from chroma_amd._src.dtypes import numpy_dtype
 from chroma_amd._src.program import Program
 
@@ -104,9 +105,12 @@ class Decoder:
         self._on_device = all(isinstance(model, Program) for model in self._models) and prefill.device == decode.device
         # Per program: the seven input arrays (the caches are bound at commit time, or stay on the
         # device) and the host arrays for the new K/V rows (device mode leaves those on the device).
+        # (With hip programs the host arrays are page-locked, so their copies go straight over the link.)
+        empty = host.empty if self._on_device else np.empty
+        self._empty_array = empty
         self._buffers: List[Tuple[List[Optional[np.ndarray]], List[Optional[np.ndarray]]]] = [
             (
-                [None if i in (2, 3) else np.empty(spec["shape"], dtype=numpy_dtype(spec["dtype"])) for i, spec in enumerate(model.inputs)],
+                [None if i in (2, 3) else empty(spec["shape"], numpy_dtype(spec["dtype"])) for i, spec in enumerate(model.inputs)],
                 [None if self._on_device else np.empty(spec["shape"], dtype=numpy_dtype(spec["dtype"])) for spec in model.outputs[1:]],
             )
             for model in self._models
@@ -208,7 +212,7 @@ class Decoder:
                 for mask, window in ((full_mask, self.context), (window_mask, self._window)):
                     _fill_mask(mask, causal & (key_times[None, :] > times[:, None] - window))
                 logit_index[0] = count - 1
-                logits = np.empty((1, self.vocab_size), dtype=self._logit_dtype)
+                logits = self._empty_array((1, self.vocab_size), self._logit_dtype)
                 rows = times[:count] % self.context
                 slots = state.slots.copy()
                 slots[rows] = times[:count]

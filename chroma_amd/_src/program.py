@@ -20,7 +20,7 @@ from typing import Any, List, Optional, Sequence, Tuple, Union
 
 import numpy as np
 
-from chroma_amd._src import native
+from chroma_amd._src import host, native
 from chroma_amd._src.dtypes import BFLOAT16, numpy_dtype
 from chroma_amd._src.spec import MANIFEST_VERSION, signature
 
@@ -188,7 +188,8 @@ class Program:
     def __call__(self, *inputs: Any, out: Union[Array, Sequence[Array], None] = None):
         arrays = [self._array(value) for value in inputs]
         if out is None:
-            results = [np.empty(spec["shape"], dtype=numpy_dtype(spec["dtype"])) for spec in self._outputs]
+            # page-locked, so the device writes them straight over the link
+            results = [host.empty(spec["shape"], numpy_dtype(spec["dtype"])) for spec in self._outputs]
         else:
             results = [out] if isinstance(out, np.ndarray) else list(out)
         with self._lock:

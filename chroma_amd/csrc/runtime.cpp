@@ -12,8 +12,10 @@
 #include <cstdlib>
 #include <cstring>
 #include <fstream>
+#include <algorithm>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <sstream>
 #include <stdexcept>
 #include <string>
@@ -58,6 +60,27 @@ struct Region {
     size_t offset = 0;
     size_t bytes = 0;
 };
+
+// Host transfers. Copies of at most kDirectBytes, and copies to or from pinned blocks handed out by
+// chroma_hip_host_alloc, are queued on the stream as they are. Larger copies of pageable memory move
+// through two pinned staging slots of kStagingSlot bytes: the CPU copy into or out of one slot overlaps
+// the DMA of the other (HIP's own pageable path reaches about a third of the link's pinned rate).
+constexpr size_t kDirectBytes = size_t(256) << 10;
+constexpr size_t kStagingSlot = size_t(2) << 20;
+
+std::mutex pinned_mutex;
+std::map<uintptr_t, size_t> pinned_blocks;  // start -> bytes of each block from chroma_hip_host_alloc
+
+bool is_pinned(const void* pointer, size_t bytes) {
+    std::lock_guard<std::mutex> lock(pinned_mutex);
+    const uintptr_t start = reinterpret_cast<uintptr_t>(pointer);
+    auto block = pinned_blocks.upper_bound(start);
+    if (block == pinned_blocks.begin()) {
+        return false;
+    }
+    --block;
+    return start >= block->first && start + bytes <= block->first + block->second;
+}
 
 struct Launch {
     std::string kernel;
@@ -196,6 +219,14 @@ public:
         if (error_host_) {
             hipHostFree(error_host_);
         }
+        for (int slot = 0; slot < 2; ++slot) {
+            if (staging_[slot]) {
+                hipHostFree(staging_[slot]);
+            }
+            if (staged_[slot]) {
+                hipEventDestroy(staged_[slot]);
+            }
+        }
         if (start_) {
             hipEventDestroy(start_);
         }
@@ -240,20 +271,18 @@ public:
         DeviceGuard guard(device_);
         for (size_t i = 0; i < plan_.inputs.size(); ++i) {
             if (plan_.inputs[i].bytes && inputs[i]) {
-                check(hipMemcpyAsync(static_cast<char*>(base_) + plan_.inputs[i].offset, inputs[i], plan_.inputs[i].bytes,
-                                     hipMemcpyHostToDevice, stream_),
-                      "Upload input");
+                to_device(static_cast<char*>(base_) + plan_.inputs[i].offset, inputs[i], plan_.inputs[i].bytes);
             }
         }
     }
 
+    // Pageable destinations hold their data when this returns; pinned and small ones once the stream
+    // has drained (finish_download).
     void download(void* const* outputs) {
         DeviceGuard guard(device_);
         for (size_t i = 0; i < plan_.outputs.size(); ++i) {
             if (plan_.outputs[i].bytes && outputs[i]) {
-                check(hipMemcpyAsync(outputs[i], static_cast<char*>(base_) + plan_.outputs[i].offset, plan_.outputs[i].bytes,
-                                     hipMemcpyDeviceToHost, stream_),
-                      "Download output");
+                to_host(outputs[i], static_cast<char*>(base_) + plan_.outputs[i].offset, plan_.outputs[i].bytes);
             }
         }
     }
@@ -304,6 +333,62 @@ public:
     }
 
 private:
+    void ensure_staging() {
+        for (int slot = 0; slot < 2; ++slot) {
+            if (!staged_[slot]) {
+                check(hipEventCreateWithFlags(&staged_[slot], hipEventDisableTiming), "hipEventCreateWithFlags");
+            }
+            if (!staging_[slot]) {
+                check(hipHostMalloc(&staging_[slot], kStagingSlot, hipHostMallocDefault), "hipHostMalloc staging");
+            }
+        }
+    }
+
+    void to_device(void* device, const void* host, size_t bytes) {
+        if (bytes <= kDirectBytes || is_pinned(host, bytes)) {
+            check(hipMemcpyAsync(device, host, bytes, hipMemcpyHostToDevice, stream_), "Upload input");
+            return;
+        }
+        ensure_staging();
+        for (size_t at = 0, chunk = 0; at < bytes; at += kStagingSlot, ++chunk) {
+            const int slot = int(chunk % 2);
+            const size_t n = std::min(kStagingSlot, bytes - at);
+            check(hipEventSynchronize(staged_[slot]), "Upload input");  // the slot's last DMA has finished
+            std::memcpy(staging_[slot], static_cast<const char*>(host) + at, n);
+            check(hipMemcpyAsync(static_cast<char*>(device) + at, staging_[slot], n, hipMemcpyHostToDevice, stream_), "Upload input");
+            check(hipEventRecord(staged_[slot], stream_), "Upload input");
+        }
+    }
+
+    void to_host(void* host, const void* device, size_t bytes) {
+        if (bytes <= kDirectBytes || is_pinned(host, bytes)) {
+            check(hipMemcpyAsync(host, device, bytes, hipMemcpyDeviceToHost, stream_), "Download output");
+            return;
+        }
+        ensure_staging();
+        const size_t chunks = (bytes + kStagingSlot - 1) / kStagingSlot;
+        auto drain = [&](size_t chunk) {
+            const int slot = int(chunk % 2);
+            const size_t at = chunk * kStagingSlot;
+            check(hipEventSynchronize(staged_[slot]), "Download output");
+            std::memcpy(static_cast<char*>(host) + at, staging_[slot], std::min(kStagingSlot, bytes - at));
+        };
+        for (size_t chunk = 0; chunk < chunks; ++chunk) {
+            const int slot = int(chunk % 2);
+            if (chunk >= 2) {
+                drain(chunk - 2);  // frees the slot while the DMA of chunk - 1 runs
+            }
+            const size_t at = chunk * kStagingSlot;
+            check(hipMemcpyAsync(staging_[slot], static_cast<const char*>(device) + at, std::min(kStagingSlot, bytes - at),
+                                 hipMemcpyDeviceToHost, stream_),
+                  "Download output");
+            check(hipEventRecord(staged_[slot], stream_), "Download output");
+        }
+        for (size_t chunk = chunks >= 2 ? chunks - 2 : 0; chunk < chunks; ++chunk) {
+            drain(chunk);
+        }
+    }
+
     void raise_index_error() {
         if (*error_host_) {
             *error_host_ = 0;
@@ -385,6 +470,8 @@ private:
     bool use_graph_ = false;
     hipGraph_t graph_ = nullptr;
     hipGraphExec_t graph_exec_ = nullptr;
+    void* staging_[2] = {nullptr, nullptr};  // pinned slots for pageable host transfers (allocated on first use)
+    hipEvent_t staged_[2] = {nullptr, nullptr};
 };
 
 int fail(int status, const char* message, char* error, size_t size) {
@@ -467,6 +554,26 @@ __attribute__((visibility("default"))) void* chroma_hip_input_pointer(void* hand
 
 __attribute__((visibility("default"))) void* chroma_hip_output_pointer(void* handle, int index) {
     return index < 0 ? nullptr : program(handle)->output_pointer(size_t(index));
+}
+
+__attribute__((visibility("default"))) int chroma_hip_host_alloc(size_t bytes, void** pointer, char* error, size_t error_size) {
+    return guarded(error, error_size, [&] {
+        *pointer = nullptr;
+        check(hipHostMalloc(pointer, bytes ? bytes : 1, hipHostMallocDefault), "hipHostMalloc");
+        std::lock_guard<std::mutex> lock(pinned_mutex);
+        pinned_blocks[reinterpret_cast<uintptr_t>(*pointer)] = bytes;
+    });
+}
+
+__attribute__((visibility("default"))) void chroma_hip_host_free(void* pointer) {
+    if (!pointer) {
+        return;
+    }
+    {
+        std::lock_guard<std::mutex> lock(pinned_mutex);
+        pinned_blocks.erase(reinterpret_cast<uintptr_t>(pointer));
+    }
+    hipHostFree(pointer);
 }
 
 __attribute__((visibility("default"))) int chroma_hip_copy_2d(void* handle, void* dst, size_t dst_pitch, const void* src, size_t src_pitch,

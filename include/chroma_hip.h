@@ -81,6 +81,14 @@ void* chroma_hip_output_pointer(void* handle, int index);
 int chroma_hip_copy_2d(void* handle, void* dst, size_t dst_pitch, const void* src, size_t src_pitch, size_t width, size_t height,
                        char* error, size_t error_size);
 
+/* Page-locked host memory for arrays that programs read and write: copies to and from it go straight to
+ * the DMA engines, while other host arrays above 256 KiB move through two pinned staging slots of the
+ * program. ``chroma_hip_host_free`` takes only pointers from ``chroma_hip_host_alloc``. No counterpart
+ * in the reference (its runtime copies pageable arrays, cuda/runtime.h:147-173); ``Program`` returns
+ * fresh outputs in such memory. */
+int chroma_hip_host_alloc(size_t bytes, void** pointer, char* error, size_t error_size);
+void chroma_hip_host_free(void* pointer);
+
 #ifdef __cplusplus
 }
 #endif

@@ -74,6 +74,33 @@ def uniform(seed, *shape):
     return torch.rand(*shape, generator=generator) * 8 - 4
 
 
+# ------------------------------------------------------------------------------------ host transfers
+@pytest.mark.parametrize("count", [1000, 65_536, 4 * 65_537, 3_000_001])
+def test_host_transfers_pinned_and_pageable(tmp_path, count):
+    """Results come back exactly through every host path: fresh outputs in page-locked blocks, pageable
+    ``out=`` arrays through the runtime's staging slots (up to several 2 MiB chunks with a ragged last
+    one), and pageable or page-locked inputs; a pooled block is reused once its array is gone."""
+    from chroma_amd._src import host
+
+    x = torch.arange(count, dtype=torch.float32) * 0.25 - 7
+    want = x.numpy() * np.float32(3) + np.float32(1)
+    with chroma_amd.compile(torch.export.export(Function(lambda v: v * 3 + 1), (x,)), tmp_path / "hip") as model:
+        fresh = model(x.numpy())
+        np.testing.assert_array_equal(fresh, want)
+        pageable = np.empty_like(want)
+        assert model(x.numpy(), out=pageable) is pageable
+        np.testing.assert_array_equal(pageable, want)
+        pinned = host.empty(x.shape, np.float32)
+        pinned[:] = x.numpy()
+        np.testing.assert_array_equal(model(pinned), want)
+        np.testing.assert_array_equal(model(pinned, out=pageable), want)
+        held = host.pooled_bytes()
+        for _ in range(3):
+            np.testing.assert_array_equal(model(x.numpy()), want)
+        assert host.pooled_bytes() == held
+        np.testing.assert_array_equal(fresh, want)  # earlier results are never reused while referenced
+
+
 # ----------------------------------------------------------------------------------- C2 bandwidth graph
 @pytest.mark.parametrize("shape", [(64, 8192), (33, 1000), (5, 40000), (7, 64), (3, 63), (4, 2050)])
 def test_bandwidth_graph_matches_oracle(tmp_path, shape):
