@@ -62,12 +62,14 @@ MATRIX_MIN_WORK = 1 << 18  # smaller batched products stay on the generic contra
 GROUPED_SLOTS = 64  # from this many (token, expert) slots on, expert products are grouped by expert
 MATRIX_ATTENTION_TOKENS = 64  # bfloat16 attention over at least this many queries runs on the matrix cores
 SPLIT_KEYS = 256  # keys per workgroup when an attention row's keys are split over workgroups
+DECODE_SPLIT_KEYS = 128  # the same for stored key/value rows read with 16-byte loads (decode steps)
 WAVE_ATTENTION_KEYS = 1024  # up to this many keys, attention runs one wave per query head
 STREAM_BLOCKS = 2048  # workgroups of a weight-streaming product (4-8 per compute unit keep HBM busy)
+SPREAD_BYTES = 8 << 20  # weight-streaming products up to this size take one row step per wave
 STAGED_FLOATS = 8192  # X rows up to this many floats are widened into LDS once per workgroup
 STAGED_ROWS = 4096  # new key/value rows of an attention up to this many floats are evaluated into LDS once
 FOLDED_NORM_ROWS = 16  # RMSNorms over at most this many rows are folded into the kernels that stage them
-FOLDED_STAGING_BLOCKS = 32  # staging kernels with more workgroups read a stored copy of an expression operand
+FOLDED_STAGING_BLOCKS = 1024  # staging kernels with more workgroups read a stored copy of an expression operand
 
 UNARY_OPS = {
     "reciprocal": "reciprocal",
@@ -1085,7 +1087,7 @@ class HIPCodegen(Codegen):
         dtypes = {x.dtype, weight.dtype, meta.dtype} | ({bias.dtype} if bias is not None else set())
         if len(dtypes) != 1:
             raise NotImplementedError(f"mixed-dtype linear {dtypes}")
-        plan = self._stream_plan(rows, inner, meta.dtype)
+        plan = self._stream_plan(rows, inner, meta.dtype, columns * inner * ITEMSIZE[meta.dtype])
         if (self.blas and rows <= 16 and plan is not None and rows * inner <= STAGED_FLOATS
                 and weight.view.offset % (16 // ITEMSIZE[weight.dtype]) == 0):
             self._stream_linear(out, x, weight, bias, rows, columns, inner, plan)
@@ -1118,10 +1120,13 @@ class HIPCodegen(Codegen):
         return f"({slot} + {offset}u)" if offset else slot
 
     @staticmethod
-    def _stream_plan(rows: int, inner: int, dtype: torch.dtype) -> Optional[Tuple[int, int]]:
+    def _stream_plan(rows: int, inner: int, dtype: torch.dtype, weight_bytes: int) -> Optional[Tuple[int, int]]:
         """(lanes per row, rows per step) for ``stream_rows``: the widest power-of-two lane group that still
         gives each lane 4 or more 16-byte chunks of a row (or a whole short row), and enough row steps
-        that about 32 chunks per lane are in flight; None when a row is not a whole number of chunks."""
+        that about 32 chunks per lane are in flight; None when a row is not a whole number of chunks.
+        Products streaming at most ``SPREAD_BYTES`` of weights take one row step per wave instead: a
+        workgroup's stream is bounded by its compute unit's outstanding requests, so small matrices go
+        fastest spread over as many compute units as they have rows for."""
         per_chunk = 16 // ITEMSIZE[dtype]
         if inner % per_chunk:
             return None
@@ -1130,7 +1135,7 @@ class HIPCodegen(Codegen):
         per_lane = chunks // lanes
         if per_lane > 64:
             return None
-        steps = max(1, min(8, 32 // per_lane, max(1, 32 // rows)))
+        steps = 1 if weight_bytes <= SPREAD_BYTES else max(1, min(8, 32 // per_lane, max(1, 32 // rows)))
         return lanes, steps
 
     def _stream_blocks(self, columns: int, lanes: int, steps: int) -> int:
@@ -1223,8 +1228,13 @@ class HIPCodegen(Codegen):
         if self.blas and bf16 and dim % 32 == 0 and dim <= 128 and tokens >= MATRIX_ATTENTION_TOKENS:
             if self._matrix_attention(out, q, k_past, k_new, v_past, v_new, mask, sinks, scale):
                 return out
-        splits = -(-keys // SPLIT_KEYS) if keys > 4 * SPLIT_KEYS and tokens * kv_heads < 64 else 1
         inputs = [v for v in (q, k_past, k_new, v_past, v_new, mask, sinks) if v is not None]
+        rows = self._decode_rows(k_past, v_past, keys - past, dim)
+        if rows is not None and keys > 4 * DECODE_SPLIT_KEYS and tokens * kv_heads < 64:
+            self._decode_attention(out, q, k_past, k_new, v_past, v_new, mask, sinks, scale, rows, inputs)
+            self.fused_attentions += 1
+            return out
+        splits = -(-keys // SPLIT_KEYS) if keys > 4 * SPLIT_KEYS and tokens * kv_heads < 64 else 1
         if splits == 1 and keys <= WAVE_ATTENTION_KEYS and dim <= 64 and group <= 16:
             # Short key ranges: one wave per query head, wave-level reductions only.
             k, _, _ = self._attention_kernel(out, q, k_past, k_new, v_past, v_new, mask, sinks, None)
@@ -1255,17 +1265,82 @@ class HIPCodegen(Codegen):
         self.fused_attentions += 1
         return out
 
-    def _attention_kernel(self, out, q, k_past, k_new, v_past, v_new, mask, sinks, split, loaders: bool = True) -> Tuple[Kernel, str, str]:
+    def _decode_rows(self, k_past: Optional[Value], v_past: Optional[Value], fresh: int, dim: int) -> Optional[dict]:
+        """The in-place layout of the stored key/value rows for ``attention_decode``: {"k"/"v": (stored
+        value, element strides, element offset)} when both are stored (or strided views) with contiguous
+        head dimensions, 16-byte aligned rows and whole 16-byte chunks per lane group, and the new rows fit
+        the LDS staging; else None."""
+        if k_past is None or v_past is None or k_past.dtype != v_past.dtype or fresh * dim > STAGED_ROWS:
+            return None
+        per_chunk = 16 // ITEMSIZE[k_past.dtype]
+        lanes = dim // per_chunk
+        if dim % per_chunk or lanes > 64 or lanes & (lanes - 1):
+            return None
+        layout = {}
+        for name, value in (("k", k_past), ("v", v_past)):
+            stored, strides = self._in_place(value)
+            if stored is None:
+                return None
+            strides = [0 if size == 1 else stride for size, stride in zip(value.shape, strides)]
+            offset = stored.view.offset if stored.view.base is not None else 0
+            if strides[2] not in (0, 1) or value.shape[2] != dim or any(x % per_chunk for x in (*strides[:2], offset)):
+                return None
+            layout[name] = (stored, strides, offset)
+        return layout
+
+    def _decode_attention(self, out, q, k_past, k_new, v_past, v_new, mask, sinks, scale, rows: dict, inputs: List[Value]) -> None:
+        """Long key ranges for a few query rows (decode steps) with ``attention_decode``: the keys are split
+        over workgroups of ``DECODE_SPLIT_KEYS``; phase 1 writes the masked scores and each split's
+        statistics, phase 2 the split's partial p . v sums, and the combine kernel adds the splits in order."""
+        tokens, kv_heads, group, dim = q.shape
+        past = k_past.shape[0]
+        keys = past + k_new.shape[0]
+        bf16 = out.dtype == torch.bfloat16
+        splits = -(-keys // DECODE_SPLIT_KEYS)
+        stats = self.allocate((tokens * kv_heads * splits * group * 2,), torch.float32)
+        partial = self.allocate((tokens * kv_heads * splits * group * dim,), torch.float32)
+        scores = self.allocate((tokens * kv_heads * keys * group,), torch.float32)
+        ctype = ctype_of(k_past.dtype)
+        prelude = [f"const uint32_t begin = blockIdx.z * {DECODE_SPLIT_KEYS}u;",
+                   f"const uint32_t end = begin + {DECODE_SPLIT_KEYS}u < {keys}u ? begin + {DECODE_SPLIT_KEYS}u : {keys}u;"]
+        for phase in (1, 2):
+            # phase 1 reads keys, phase 2 values; only the split that holds the new rows stages them
+            needed = "k" if phase == 1 else "v"
+            k, split, _ = self._attention_kernel(out, q, k_past, k_new, v_past, v_new, mask, sinks, (stats, partial, splits),
+                                                 prelude=prelude, fresh=((f"load_{needed}",), f"end > {past}u"))
+            scores_slot = k.slot(scores.name, torch.float32, writable=True, extent=self.extents[scores.name])
+            sources = []
+            for name in ("k", "v"):
+                stored, strides, offset = rows[name]
+                root = stored.root
+                base = k.slot(root.name, root.dtype, extent=self.extents[root.name])
+                staged_rows = f"load_{name}_new" if name == needed else "nullptr"
+                sources.append(f"chroma::KeyRows<{ctype}>{{{base} + {offset}u + blockIdx.y * {strides[1]}u, {strides[0]}u, {past}u, {staged_rows}}}")
+            k.line(f"chroma::attention_decode<{phase}, {dim}, {group}, {str(bf16).lower()}, {ctype}>(begin, end, {keys}u, {float_literal(scale)}, "
+                   f"load_q, {sources[0]}, {sources[1]}, load_mask, load_sink, {split}, "
+                   f"{scores_slot} + (size_t(blockIdx.x) * {kv_heads}u + blockIdx.y) * {keys * group}u);")
+            self.launch(k, (tokens, kv_heads, splits), 256, inputs + [stats, scores] + ([partial] if phase == 2 else []), kind=f"attention_decode{phase}")
+        k, _, row = self._attention_kernel(out, q, k_past, k_new, v_past, v_new, mask, sinks, (stats, partial, splits), loaders=False)
+        table = k.slot(partial.name, torch.float32, extent=self.extents[partial.name])
+        k.line(f"chroma::attention_combine<{dim}, {group}>({table} + {row} * {group * dim}u, {splits}u, store);")
+        self.launch(k, (tokens, kv_heads, 1), 256, [partial], kind="attention_combine")
+
+    def _attention_kernel(self, out, q, k_past, k_new, v_past, v_new, mask, sinks, split, loaders: bool = True,
+                          prelude: Sequence[str] = (), fresh: Optional[Tuple[Tuple[str, ...], str]] = None) -> Tuple[Kernel, str, str]:
         """A kernel over (query row, key/value head) with the attention loaders and the result store
         declared as lambdas (operands read through generated code, so views and fused expressions are
         evaluated in place); returns it with the C expression of its ``AttentionSplit`` and the C
-        expression of its first split row in the split scratch."""
+        expression of its first split row in the split scratch. ``prelude`` lines open the kernel;
+        ``fresh`` = (key sources, C condition) stages only those sources' new rows, and only in workgroups
+        where the condition holds (no ``load_k``/``load_v`` lambdas are declared then)."""
         tokens, kv_heads, group, dim = q.shape
         past = k_past.shape[0] if k_past is not None else 0
         keys = past + k_new.shape[0]
         k = Kernel(1)
         t = Aff.of(k.atom("blockIdx.x", tokens - 1, prefix="t"))
         h = Aff.of(k.atom("blockIdx.y", kv_heads - 1, prefix="h"))
+        for line in prelude:
+            k.line(line)
         slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
         scores_shape = (kv_heads, group, tokens, keys)
 
@@ -1281,19 +1356,26 @@ class HIPCodegen(Codegen):
                     k.line(f"return {k.emit(first(coords))};")
                 k.line(f"return {k.emit(second(coords))};")
 
+        fresh_only = fresh
         fresh = keys - past
         staged = loaders and fresh * dim <= STAGED_ROWS
+        assert fresh_only is None or staged, "selective staging needs the new rows in LDS"
 
         def key_source(past_value: Optional[Value], new_value: Value, name: str) -> None:
             params = [("j", keys - 1), ("d", dim - 1)]
+            if fresh_only is not None and name not in fresh_only[0]:
+                return
             if staged:
                 # The new rows (often a fused expression such as the rotary embedding) are evaluated once,
                 # cooperatively, into LDS; the key loops then read plain LDS values.
                 k.line(f"__shared__ float {name}_new[{fresh * dim}];")
-                with k.block(f"for (uint32_t i = threadIdx.x; i < {fresh * dim}u; i += blockDim.x) {{"):
-                    i = Aff.of(Atom("i", fresh * dim - 1))
-                    row, column = k.div(i, dim), k.mod(i, dim)
-                    k.line(f"{name}_new[i] = {k.emit(self.read(k, new_value, [row, h, column]))};")
+                with k.block(f"if ({fresh_only[1]}) {{" if fresh_only is not None else "{"):
+                    with k.block(f"for (uint32_t i = threadIdx.x; i < {fresh * dim}u; i += blockDim.x) {{"):
+                        i = Aff.of(Atom("i", fresh * dim - 1))
+                        row, column = k.div(i, dim), k.mod(i, dim)
+                        k.line(f"{name}_new[i] = {k.emit(self.read(k, new_value, [row, h, column]))};")
+                if fresh_only is not None:
+                    return
 
             if past_value is None:
                 if staged:
@@ -1520,7 +1602,7 @@ class HIPCodegen(Codegen):
         experts = weight.shape[0]
         per_slot = eqn == "beck,bek->bec"
         per_expert = "true" if per_slot else "false"
-        plan = self._stream_plan(1, inner, out.dtype)
+        plan = self._stream_plan(1, inner, out.dtype, tokens * selected * channels * inner * ITEMSIZE[out.dtype])
         if (tokens * selected < GROUPED_SLOTS and plan is not None and inner <= STAGED_FLOATS
                 and weight.view.offset % (16 // ITEMSIZE[weight.dtype]) == 0):
             # One slot per workgroup row of the grid: the slot's input row (per token or per slot; any

@@ -145,6 +145,7 @@ class Decoder:
         args[2] = args[3] = None
         if owner != which:
             target, source = self._models[which].native, self._models[owner].native
+            source.synchronize()  # its queued commits have landed
             size = int(np.prod(self._shape)) * self._cache_dtype.itemsize
             for index in (2, 3):
                 target.copy_2d(target.input_pointer(index), size, source.input_pointer(index), size, size, 1)
@@ -156,11 +157,13 @@ class Decoder:
         row, layers = self._row_bytes, self._shape[0]
         first = start % self.context
         head = min(count, self.context - first)
+        # Queued on the program's stream: its next run (or a synchronize before another program copies
+        # the cache) comes after them.
         for output, cache in ((1, 2), (2, 3)):
             src, dst = program.output_pointer(output), program.input_pointer(cache)
-            program.copy_2d(dst + first * row, self.context * row, src, steps * row, head * row, layers)
+            program.copy_2d(dst + first * row, self.context * row, src, steps * row, head * row, layers, queued=True)
             if count > head:
-                program.copy_2d(dst, self.context * row, src + head * row, steps * row, (count - head) * row, layers)
+                program.copy_2d(dst, self.context * row, src + head * row, steps * row, (count - head) * row, layers, queued=True)
 
     @property
     def position(self) -> int:

@@ -85,6 +85,8 @@ def library() -> ctypes.CDLL:
             getattr(lib, name).argtypes = [c.c_void_p, c.c_int]
             getattr(lib, name).restype = c.c_void_p
         lib.chroma_hip_copy_2d.argtypes = [c.c_void_p, c.c_void_p, c.c_size_t, c.c_void_p, c.c_size_t, c.c_size_t, c.c_size_t, c.c_char_p, c.c_size_t]
+        lib.chroma_hip_copy_2d_queued.argtypes = lib.chroma_hip_copy_2d.argtypes
+        lib.chroma_hip_synchronize.argtypes = [c.c_void_p, c.c_char_p, c.c_size_t]
         lib.chroma_hip_host_alloc.argtypes = [c.c_size_t, c.POINTER(c.c_void_p), c.c_char_p, c.c_size_t]
         lib.chroma_hip_host_free.argtypes = [c.c_void_p]
         lib.chroma_hip_host_free.restype = None
@@ -107,6 +109,8 @@ EXPORTED = (
     "chroma_hip_input_pointer",
     "chroma_hip_output_pointer",
     "chroma_hip_copy_2d",
+    "chroma_hip_copy_2d_queued",
+    "chroma_hip_synchronize",
     "chroma_hip_host_alloc",
     "chroma_hip_host_free",
 )

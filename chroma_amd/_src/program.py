@@ -59,26 +59,30 @@ class NativeModel:
         if len(inputs) != len(self._inputs) or len(outputs) != len(self._outputs):
             raise ValueError("wrong number of arrays")
         regions: List[Tuple[int, int]] = []
+        pointers: List[Optional[int]] = []
         for value, spec in zip(inputs, self._inputs):
             if value is None and resident:
+                pointers.append(None)
                 continue
             array = _checked(value, spec, False)
-            regions.append((array.ctypes.data, array.ctypes.data + array.nbytes))
+            begin = array.ctypes.data
+            pointers.append(begin)
+            regions.append((begin, begin + array.nbytes))
         for value, spec in zip(outputs, self._outputs):
             if value is None and resident:
+                pointers.append(None)
                 continue
             array = _checked(value, spec, True)
-            begin, end = array.ctypes.data, array.ctypes.data + array.nbytes
+            begin = array.ctypes.data
+            end = begin + array.nbytes
             if any(begin < last and first < end for first, last in regions):
                 raise ValueError("output overlap")
             regions.append((begin, end))
+            pointers.append(begin)
         error = ctypes.create_string_buffer(1024)
+        count = len(inputs)
         status = self._lib.chroma_hip_run(
-            self._handle,
-            native.pointer_array(None if a is None else a.ctypes.data for a in inputs),
-            native.pointer_array(None if a is None else a.ctypes.data for a in outputs),
-            error,
-            len(error),
+            self._handle, native.pointer_array(pointers[:count]), native.pointer_array(pointers[count:]), error, len(error)
         )
         native.check(status, error)
 
@@ -88,10 +92,17 @@ class NativeModel:
     def output_pointer(self, index: int) -> int:
         return int(self._lib.chroma_hip_output_pointer(self._handle, index) or 0)
 
-    def copy_2d(self, dst: int, dst_pitch: int, src: int, src_pitch: int, width: int, height: int) -> None:
-        """Device-to-device copy of ``height`` rows of ``width`` bytes on this program's stream."""
-        error = ctypes.create_string_buffer(1024)
-        native.check(self._lib.chroma_hip_copy_2d(self._handle, dst, dst_pitch, src, src_pitch, width, height, error, len(error)), error)
+    def copy_2d(self, dst: int, dst_pitch: int, src: int, src_pitch: int, width: int, height: int, *, queued: bool = False) -> None:
+        """Device-to-device copy of ``height`` rows of ``width`` bytes on this program's stream; complete on
+        return, or with ``queued`` only ordered before this program's later work (see ``synchronize``)."""
+        error = ctypes.create_string_buffer(256)
+        copy = self._lib.chroma_hip_copy_2d_queued if queued else self._lib.chroma_hip_copy_2d
+        native.check(copy(self._handle, dst, dst_pitch, src, src_pitch, width, height, error, len(error)), error)
+
+    def synchronize(self) -> None:
+        """Wait for everything queued on this program's stream."""
+        error = ctypes.create_string_buffer(256)
+        native.check(self._lib.chroma_hip_synchronize(self._handle, error, len(error)), error)
 
     # Device-resident helpers (benchmarks and tests): upload once, execute many times, download.
     def upload(self, inputs: Sequence[np.ndarray]) -> None:

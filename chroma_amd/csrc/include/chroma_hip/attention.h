@@ -277,9 +277,23 @@ __device__ __forceinline__ void attention_waves(uint32_t keys, float scale, Load
         const float s1 = storage_round<BF16>(s * scale);
         return storage_round<BF16>(s1 + load_mask(j, g));
     };
+    // Each lane takes keys lane, lane + 64, ... in that order; U of them per batch, their loads issued
+    // together (a batch's keys past the end read the last key and contribute nothing).
+    constexpr int U = D <= 16 ? 8 : (D <= 32 ? 4 : 2);
     float peak = neg_inf, total = 0.0f;
-    for (uint32_t j = lane; j < keys; j += kWave) {
-        softmax_stats_add(peak, total, score(j));
+    for (uint32_t j0 = lane; j0 < keys; j0 += U * kWave) {
+        float s[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t j = j0 + u * kWave;
+            s[u] = score(j < keys ? j : keys - 1);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (j0 + u * kWave < keys) {
+                softmax_stats_add(peak, total, s[u]);
+            }
+        }
     }
 #pragma unroll
     for (int offset = 1; offset < kWave; offset <<= 1) {
@@ -291,11 +305,22 @@ __device__ __forceinline__ void attention_waves(uint32_t keys, float scale, Load
     for (int d = 0; d < D; ++d) {
         acc[d] = 0.0f;
     }
-    for (uint32_t j = lane; j < keys; j += kWave) {
-        const float p = storage_round<BF16>(fast_exp(score(j) - peak) / total);
+    for (uint32_t j0 = lane; j0 < keys; j0 += U * kWave) {
+        float p[U];
 #pragma unroll
-        for (int d = 0; d < D; ++d) {
-            acc[d] += p * load_v(j, d);
+        for (int u = 0; u < U; ++u) {
+            const uint32_t j = j0 + u * kWave;
+            p[u] = storage_round<BF16>(fast_exp(score(j < keys ? j : keys - 1) - peak) / total);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t j = j0 + u * kWave;
+            if (j < keys) {
+#pragma unroll
+                for (int d = 0; d < D; ++d) {
+                    acc[d] += p[u] * load_v(j, d);
+                }
+            }
         }
     }
 #pragma unroll
@@ -309,6 +334,244 @@ __device__ __forceinline__ void attention_waves(uint32_t keys, float scale, Load
     for (int d = 0; d < D; ++d) {
         if (lane == uint32_t(d) % kWave) {
             store(g, d, acc[d]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Split-key attention for a few query rows over long key ranges (decode steps), reading the stored
+// key/value rows with 16-byte loads: rows [0, past) come from memory (row j of this key/value head at
+// rows + j * stride, elements contiguous and rows 16-byte aligned), rows [past, keys) from an LDS array
+// of floats (the new rows, evaluated by the caller). Same numerics as ``attention_rows`` (scores rounded
+// at each step, float statistics, probabilities rounded after the division by the row's sum, float
+// output sums) with the float sums in another order.
+template <class T> struct KeyRows {
+    const T* rows;
+    uint32_t stride, past;
+    const float* fresh;
+};
+
+// Workgroup: 4 waves over keys [begin, end) of one (query row, key/value head). A key's D elements are
+// LPK lanes x one 16-byte chunk each (N elements), so a wave takes 64 / LPK consecutive keys per load and
+// every load instruction reads whole rows. Query heads' dot products meet through a butterfly over the
+// LPK lanes. PHASE 1 writes the masked scores of the keys ([keys][G] at ``scores``) and the split's
+// statistics; PHASE 2 merges every split's statistics with the sink, then writes the split's partial
+// p . v sums (``attention_combine`` adds the splits in order). A split whose mask is -inf for every key
+// and head reads no rows and writes no scores (its statistics are (-inf, 0) and its partial sums 0:
+// exactly what its keys contribute as long as their rows are finite).
+template <int PHASE, int D, int G, bool BF16, class T, class LoadQ, class LoadMask, class LoadSink>
+__device__ __forceinline__ void attention_decode(uint32_t begin, uint32_t end, uint32_t keys, float scale, LoadQ load_q, KeyRows<T> k_rows,
+                                                 KeyRows<T> v_rows, LoadMask load_mask, LoadSink load_sink, AttentionSplit split,
+                                                 float* scores) {
+    using C = Chunk16<T>;
+    constexpr int N = C::N;
+    constexpr int LPK = D / N;
+    constexpr int KPW = kWave / LPK;
+    constexpr int WAVES = 4;
+    static_assert(D % N == 0 && LPK <= kWave && (LPK & (LPK - 1)) == 0, "attention_decode shape");
+    __shared__ float q_s[G][D];
+    __shared__ float wave_peak[WAVES][G], wave_total[WAVES][G];
+    __shared__ float peak_s[G], total_s[G];
+    __shared__ float acc_s[WAVES][G][D];
+    const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+    const uint32_t kq = lane / LPK, c = lane % LPK;
+    const float neg_inf = -__builtin_inff();
+
+    auto chunk = [&](const KeyRows<T>& source, uint32_t j, float (&out)[N]) {
+        if (j < source.past) {
+            const u32x4_t bits = C::load(source.rows + size_t(j) * source.stride + c * N);
+#pragma unroll
+            for (int e = 0; e < N; ++e) {
+                out[e] = C::get(bits, e);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < N; ++e) {
+                out[e] = source.fresh[(j - source.past) * D + c * N + e];
+            }
+        }
+    };
+
+    if constexpr (PHASE == 1) {
+        // Is any key of the split unmasked for any head? (The mask and query loads go out together; one
+        // barrier both publishes the staged queries and answers.)
+        bool live = false;
+        for (uint32_t i = tid; i < (end - begin) * G; i += blockDim.x) {
+            live |= load_mask(begin + i / G, i % G) != neg_inf;
+        }
+        for (uint32_t i = tid; i < uint32_t(G * D); i += blockDim.x) {
+            q_s[i / D][i % D] = load_q(i / D, i % D);
+        }
+        if (!__syncthreads_or(live)) {
+            if (tid < uint32_t(G)) {
+                split.stats[(split.split * G + tid) * 2] = neg_inf;
+                split.stats[(split.split * G + tid) * 2 + 1] = 0.0f;
+            }
+            return;
+        }
+        float q[G][N];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+#pragma unroll
+            for (int e = 0; e < N; ++e) {
+                q[g][e] = q_s[g][c * N + e];
+            }
+        }
+        float peak[G], total[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            peak[g] = neg_inf;
+            total[g] = 0.0f;
+        }
+        constexpr int U = 4;  // key steps whose rows are requested together
+        for (uint32_t j0 = begin + wave * KPW + kq; j0 < end; j0 += U * WAVES * KPW) {
+            float kv[U][N];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint32_t j = j0 + u * WAVES * KPW;
+                chunk(k_rows, j < end ? j : end - 1, kv[u]);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint32_t j = j0 + u * WAVES * KPW;
+                float s2[G];
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    float dot = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < N; ++e) {
+                        dot += q[g][e] * kv[u][e];
+                    }
+#pragma unroll
+                    for (int offset = 1; offset < LPK; offset <<= 1) {
+                        dot += __shfl_xor(dot, offset, kWave);
+                    }
+                    const float s = storage_round<BF16>(dot);
+                    const float s1 = storage_round<BF16>(s * scale);
+                    s2[g] = storage_round<BF16>(s1 + load_mask(j < end ? j : end - 1, g));
+                }
+                if (j < end) {
+#pragma unroll
+                    for (int g = 0; g < G; ++g) {
+                        softmax_stats_add(peak[g], total[g], s2[g]);
+                        if (uint32_t(g % LPK) == c) {
+                            scores[size_t(j) * G + g] = s2[g];
+                        }
+                    }
+                }
+            }
+        }
+        // The LPK lanes of a key group hold the same statistics: merge the key groups, then the waves.
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+#pragma unroll
+            for (int offset = LPK; offset < kWave; offset <<= 1) {
+                softmax_stats_merge(peak[g], total[g], __shfl_xor(peak[g], offset, kWave), __shfl_xor(total[g], offset, kWave));
+            }
+            if (lane == 0) {
+                wave_peak[wave][g] = peak[g];
+                wave_total[wave][g] = total[g];
+            }
+        }
+        __syncthreads();
+        if (tid < uint32_t(G)) {
+            float top = neg_inf, sum = 0.0f;
+            for (int w = 0; w < WAVES; ++w) {
+                softmax_stats_merge(top, sum, wave_peak[w][tid], wave_total[w][tid]);
+            }
+            split.stats[(split.split * G + tid) * 2] = top;
+            split.stats[(split.split * G + tid) * 2 + 1] = sum;
+        }
+    } else {
+        // The row's statistics: every split's, then the sink; the split is live if any head's own
+        // statistics are.
+        bool live = false;
+        if (tid < uint32_t(G)) {
+            float top = neg_inf, sum = 0.0f;
+            for (uint32_t w = 0; w < split.splits; ++w) {
+                softmax_stats_merge(top, sum, split.stats[(w * G + tid) * 2], split.stats[(w * G + tid) * 2 + 1]);
+            }
+            softmax_stats_add(top, sum, load_sink(tid));
+            peak_s[tid] = top;
+            total_s[tid] = sum;
+            live = split.stats[(split.split * G + tid) * 2] != neg_inf;
+        }
+        float* partial = split.partial + size_t(split.split) * G * D;
+        if (!__syncthreads_or(live)) {
+            for (uint32_t i = tid; i < uint32_t(G * D); i += blockDim.x) {
+                partial[i] = 0.0f;
+            }
+            return;
+        }
+        float peak[G], total[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            peak[g] = peak_s[g];
+            total[g] = total_s[g];
+        }
+        float acc[G][N];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+#pragma unroll
+            for (int e = 0; e < N; ++e) {
+                acc[g][e] = 0.0f;
+            }
+        }
+        constexpr int U = 4;
+        for (uint32_t j0 = begin + wave * KPW + kq; j0 < end; j0 += U * WAVES * KPW) {
+            float vv[U][N];
+            float sc[U][G];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint32_t j = j0 + u * WAVES * KPW;
+                const uint32_t jj = j < end ? j : end - 1;
+                chunk(v_rows, jj, vv[u]);
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    sc[u][g] = scores[size_t(jj) * G + g];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (j0 + u * WAVES * KPW < end) {
+#pragma unroll
+                    for (int g = 0; g < G; ++g) {
+                        const float p = storage_round<BF16>(fast_exp(sc[u][g] - peak[g]) / total[g]);
+#pragma unroll
+                        for (int e = 0; e < N; ++e) {
+                            acc[g][e] += p * vv[u][e];
+                        }
+                    }
+                }
+            }
+        }
+        // Sum the key groups of the wave, then the waves.
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+#pragma unroll
+            for (int e = 0; e < N; ++e) {
+#pragma unroll
+                for (int offset = LPK; offset < kWave; offset <<= 1) {
+                    acc[g][e] += __shfl_xor(acc[g][e], offset, kWave);
+                }
+            }
+        }
+        if (kq == 0) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+#pragma unroll
+                for (int e = 0; e < N; ++e) {
+                    acc_s[wave][g][c * N + e] = acc[g][e];
+                }
+            }
+        }
+        __syncthreads();
+        for (uint32_t i = tid; i < uint32_t(G * D); i += blockDim.x) {
+            float sum = 0.0f;
+            for (int w = 0; w < WAVES; ++w) {
+                sum += acc_s[w][i / D][i % D];
+            }
+            partial[i] = sum;
         }
     }
 }

@@ -297,8 +297,8 @@ public:
     }
 
     // Device-to-device rectangle copy on this program's stream (``height`` rows of ``width`` bytes),
-    // finished before returning.
-    void copy_2d(void* dst, size_t dst_pitch, const void* src, size_t src_pitch, size_t width, size_t height) {
+    // finished before returning unless ``queued`` (then ordered before this program's later work).
+    void copy_2d(void* dst, size_t dst_pitch, const void* src, size_t src_pitch, size_t width, size_t height, bool queued) {
         DeviceGuard guard(device_);
         if (!width || !height) {
             return;
@@ -307,7 +307,14 @@ public:
             throw std::runtime_error("copy_2d pitch smaller than the row width");
         }
         check(hipMemcpy2DAsync(dst, dst_pitch, src, src_pitch, width, height, hipMemcpyDeviceToDevice, stream_), "hipMemcpy2DAsync");
-        check(hipStreamSynchronize(stream_), "Device copy");
+        if (!queued) {
+            check(hipStreamSynchronize(stream_), "Device copy");
+        }
+    }
+
+    void synchronize() {
+        DeviceGuard guard(device_);
+        check(hipStreamSynchronize(stream_), "Synchronize");
     }
 
     float execute(int iterations, bool timed) {
@@ -578,6 +585,15 @@ __attribute__((visibility("default"))) void chroma_hip_host_free(void* pointer) 
 
 __attribute__((visibility("default"))) int chroma_hip_copy_2d(void* handle, void* dst, size_t dst_pitch, const void* src, size_t src_pitch,
                                                               size_t width, size_t height, char* error, size_t error_size) {
-    return guarded(error, error_size, [&] { program(handle)->copy_2d(dst, dst_pitch, src, src_pitch, width, height); });
+    return guarded(error, error_size, [&] { program(handle)->copy_2d(dst, dst_pitch, src, src_pitch, width, height, false); });
+}
+
+__attribute__((visibility("default"))) int chroma_hip_copy_2d_queued(void* handle, void* dst, size_t dst_pitch, const void* src, size_t src_pitch,
+                                                                     size_t width, size_t height, char* error, size_t error_size) {
+    return guarded(error, error_size, [&] { program(handle)->copy_2d(dst, dst_pitch, src, src_pitch, width, height, true); });
+}
+
+__attribute__((visibility("default"))) int chroma_hip_synchronize(void* handle, char* error, size_t error_size) {
+    return guarded(error, error_size, [&] { program(handle)->synchronize(); });
 }
 }

@@ -81,6 +81,14 @@ void* chroma_hip_output_pointer(void* handle, int index);
 int chroma_hip_copy_2d(void* handle, void* dst, size_t dst_pitch, const void* src, size_t src_pitch, size_t width, size_t height,
                        char* error, size_t error_size);
 
+/* The same copy, only queued: it runs before the program's later runs and copies, and
+ * ``chroma_hip_synchronize`` waits for it (and everything else queued on the program's stream). The
+ * decoder commits each step's new cache rows this way and synchronizes only when another program
+ * takes the cache over. */
+int chroma_hip_copy_2d_queued(void* handle, void* dst, size_t dst_pitch, const void* src, size_t src_pitch, size_t width,
+                              size_t height, char* error, size_t error_size);
+int chroma_hip_synchronize(void* handle, char* error, size_t error_size);
+
 /* Page-locked host memory for arrays that programs read and write: copies to and from it go straight to
  * the DMA engines, while other host arrays above 256 KiB move through two pinned staging slots of the
  * program. ``chroma_hip_host_free`` takes only pointers from ``chroma_hip_host_alloc``. No counterpart

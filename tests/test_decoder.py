@@ -14,7 +14,7 @@ import dataclasses
 import os
 import signal
 import threading
-from typing import List, Optional
+from typing import Any, List, Optional
 from unittest.mock import Mock, patch
 
 import numpy as np
@@ -171,6 +171,7 @@ class FakeNative:
         self.inputs = [device.allocate(int(np.prod(s["shape"])) * 8) for s in oracle.inputs]
         self.outputs = [device.allocate(int(np.prod(s["shape"])) * 8) for s in oracle.outputs]
         self.copies = 0
+        self.pending: List[Any] = []
 
     def input_pointer(self, index: int) -> int:
         return self.inputs[index]
@@ -178,13 +179,27 @@ class FakeNative:
     def output_pointer(self, index: int) -> int:
         return self.outputs[index]
 
-    def copy_2d(self, dst, dst_pitch, src, src_pitch, width, height) -> None:
+    def copy_2d(self, dst, dst_pitch, src, src_pitch, width, height, *, queued=False) -> None:
+        # A queued copy happens only when this program's stream reaches it: at its next run, copy or
+        # synchronize (so a reader on another program that skips ``synchronize`` sees stale rows).
         assert dst_pitch >= width and src_pitch >= width
-        for row in range(height):
-            self.device.memory[dst + row * dst_pitch : dst + row * dst_pitch + width] = self.device.memory[src + row * src_pitch : src + row * src_pitch + width]
+
+        def copy():
+            for row in range(height):
+                self.device.memory[dst + row * dst_pitch : dst + row * dst_pitch + width] = self.device.memory[src + row * src_pitch : src + row * src_pitch + width]
+
+        self.pending.append(copy)
         self.copies += 1
+        if not queued:
+            self.synchronize()
+
+    def synchronize(self) -> None:
+        for copy in self.pending:
+            copy()
+        self.pending.clear()
 
     def run(self, inputs: List[Optional[np.ndarray]], outputs: List[Optional[np.ndarray]], *, resident: bool) -> None:
+        self.synchronize()
         staged = [self.device.view(address, spec) for address, spec in zip(self.inputs, self.oracle.inputs)]
         for value, target in zip(inputs, staged):
             if value is not None:
@@ -219,6 +234,7 @@ def test_device_resident_cache_matches_host_cache(oracle_pairs, head_dim):
         assert resident.position == host.position == position
         np.testing.assert_array_equal(resident._state.slots, host._state.slots)
         owner = fake[resident._state.owner].native
+        owner.synchronize()  # the commit's copies are queued on the owner's stream
         for index, cache in ((2, host._state.keys), (3, host._state.values)):
             np.testing.assert_array_equal(device.view(owner.input_pointer(index), prefill.inputs[index]), cache)
     np.testing.assert_allclose(got, expected[position - 1 : position], rtol=2e-5, atol=2e-6)

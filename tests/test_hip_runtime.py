@@ -702,14 +702,15 @@ class FreshAttention(torch.nn.Module):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize(
-    "tokens, past, kv_heads, group, dim",
-    [(1, 257, 1, 8, 16), (5, 3, 2, 4, 64), (3, 700, 2, 2, 4), (16, 0, 1, 1, 8), (100, 60, 2, 4, 64), (130, 0, 1, 2, 128),
-     (1, 4096, 8, 8, 64), (2, 1500, 1, 8, 16)],
+    "tokens, past, kv_heads, group, dim, window",
+    [(1, 257, 1, 8, 16, 40), (5, 3, 2, 4, 64, 40), (3, 700, 2, 2, 4, 40), (16, 0, 1, 1, 8, 40), (100, 60, 2, 4, 64, 40),
+     (130, 0, 1, 2, 128, 40), (1, 4096, 8, 8, 64, 40), (2, 1500, 1, 8, 16, 40), (1, 1000, 2, 4, 32, None), (3, 2100, 1, 8, 64, 300)],
 )
-def test_fused_attention_matches_oracle(tmp_path, dtype, tokens, past, kv_heads, group, dim):
+def test_fused_attention_matches_oracle(tmp_path, dtype, tokens, past, kv_heads, group, dim, window):
     """The fused attention against the oracle's unfused chain: causal and windowed masks, a query row whose
     keys are all masked (only the sink remains), sinks of both signs; one launch per row, the matrix-core
-    kernel for long bfloat16 prefills, and keys split over workgroups (3 launches) for long caches."""
+    kernel for long bfloat16 prefills, and keys split over workgroups (3 launches) for long caches, with
+    splits that are wholly masked, partly masked and unmasked."""
     generator = torch.Generator().manual_seed(tokens * 31 + past)
 
     def rand(*shape, scale=1.0):
@@ -719,7 +720,8 @@ def test_fused_attention_matches_oracle(tmp_path, dtype, tokens, past, kv_heads,
     mask = torch.zeros(tokens, keys)
     for t in range(tokens):
         mask[t, past + t + 1 :] = -math.inf
-        mask[t, : max(0, past + t - 40)] = -math.inf
+        if window is not None:
+            mask[t, : max(0, past + t - window)] = -math.inf
     if tokens > 2:
         mask[1, :] = -math.inf
     inputs = (rand(tokens, kv_heads, group, dim), rand(past or 1, kv_heads, dim), rand(tokens, kv_heads, dim),
@@ -730,7 +732,7 @@ def test_fused_attention_matches_oracle(tmp_path, dtype, tokens, past, kv_heads,
         module = SinkAttention()
     exported = torch.export.export(module, inputs)
     with chroma_amd.compile(exported, tmp_path / "hip") as model:
-        split = past + tokens > 1024 and tokens * kv_heads < 64
+        split = past + tokens > 512 and tokens * kv_heads < 64
         assert model.stats["fused_attentions"] == 1 and model.stats["launches"] <= (4 if split else 2)
         # bfloat16 prefills of 64 or more queries take the matrix-core kernel
         assert model.stats["mfma_matmuls"] == int(dtype == torch.bfloat16 and tokens >= 64)
