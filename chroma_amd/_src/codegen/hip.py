@@ -69,6 +69,7 @@ SPREAD_BYTES = 8 << 20  # weight-streaming products up to this size take one row
 STAGED_FLOATS = 8192  # X rows up to this many floats are widened into LDS once per workgroup
 STAGED_ROWS = 4096  # new key/value rows of an attention up to this many floats are evaluated into LDS once
 FOLDED_NORM_ROWS = 16  # RMSNorms over at most this many rows are folded into the kernels that stage them
+LDS_STAGED_FLOATS = 12288  # floats a staging prologue may keep in LDS (X rows and evaluated operands)
 FOLDED_STAGING_BLOCKS = 1024  # staging kernels with more workgroups read a stored copy of an expression operand
 
 UNARY_OPS = {
@@ -203,6 +204,8 @@ class HIPCodegen(Codegen):
             for coord, stride, size in zip(coords, view.strides, value.shape):
                 if size != 1 and stride:
                     address = address + coord.scale(stride)
+            if root.name in k.staged_values:
+                return ("lds", k.staged_values[root.name], address)
             expression = k.unstored.get(root.name)
             if expression is not None:
                 if value.name == root.name:
@@ -781,26 +784,27 @@ class HIPCodegen(Codegen):
             self.pending_stores.discard(buffer)
             resolved.append(buffer)
             self.write_through_stores += 1
-        # A deferred norm over a computed operand (an expression, or a buffer computed in place) reads
-        # it twice (squares, then scaling): the operand's rows are evaluated once into LDS instead.
-        staged_sources = False
-        for name in sorted(self.pending_of.get(x.name, frozenset())):
-            if name in self.materialized:
-                continue
-            source = self.pending_norms[name][1]
-            computed = not source.stored or source.root.name in k.unstored
-            count = math.prod(_shape(source.shape))
-            if not computed or source.name in k.staged_values or count > STAGED_FLOATS:
-                continue
-            rows_array = k.fresh("hs")
-            k.line(f"__shared__ float {rows_array}[{count}];")
-            k.line("#pragma unroll 4")
+        budget = [LDS_STAGED_FLOATS - rows * inner]
+
+        def stage_rows(value: Value, key: str) -> bool:
+            """Evaluate ``value`` once into a __shared__ float array (row-major) read in its place."""
+            shape = _shape(value.shape)
+            count = math.prod(shape)
+            if count > budget[0]:
+                return False
+            budget[0] -= count
+            array = k.fresh("hs")
+            k.line(f"__shared__ float {array}[{count}];")
+            k.line(f"#pragma unroll {max(1, min(8, -(-count // threads)))}")
             with k.block(f"for (uint32_t i = threadIdx.x; i < {count}u; i += {threads}u) {{"):
                 i = Aff.of(Atom("i", count - 1))
-                k.line(f"{rows_array}[i] = {k.emit(self.read(k, source, k.unflatten(i, _shape(source.shape)) if source.shape else []))};")
-            k.staged_values[source.name] = rows_array
-            staged_sources = True
-        if staged_sources:
+                k.line(f"{array}[i] = {k.emit(self.read(k, value, k.unflatten(i, shape) if value.shape else []))};")
+            k.staged_values[key] = array
+            return True
+
+        # A buffer computed in place is evaluated once into LDS (every later read in this kernel, and
+        # the first workgroup's store of it, come from there) ...
+        if any([stage_rows(k.unstored[buffer], buffer) for buffer in resolved]):
             k.line("__syncthreads();")
         for buffer in resolved:
             expression = k.unstored[buffer]
@@ -810,9 +814,23 @@ class HIPCodegen(Codegen):
             with k.block("if (blockIdx.x == 0u && blockIdx.y == 0u && blockIdx.z == 0u) {"):
                 with k.block(f"for (uint32_t i = threadIdx.x; i < {count}u; i += {threads}u) {{"):
                     i = Aff.of(Atom("i", count - 1))
-                    target = next((v for v in (buffer, expression.name) if v in k.staged_values), None)
-                    node = ("lds", k.staged_values[target], i) if target else self.read(k, expression, k.unflatten(i, shape) if expression.shape else [])
+                    node = ("lds", k.staged_values[buffer], i) if buffer in k.staged_values else self.read(k, expression, k.unflatten(i, shape) if expression.shape else [])
                     k.store(slot, expression.dtype, i, node)
+        # ... and so is a deferred norm's operand that still costs loads (it is read twice: squares,
+        # then scaling).
+        staged_sources = False
+        for name in sorted(self.pending_of.get(x.name, frozenset())):
+            if name in self.materialized:
+                continue
+            source = self.pending_norms[name][1]
+            if source.name in k.staged_values or (source.stored and source.root.name in k.staged_values):
+                continue
+            loads = (source.stored and source.root.name in k.unstored) or (
+                not source.stored and any(buffer not in k.staged_values for buffer in self.sources[source.name]))
+            if loads and stage_rows(source, source.name):
+                staged_sources = True
+        if staged_sources:
+            k.line("__syncthreads();")
         k.norm_scales = {}
         for name in sorted(self.pending_of.get(x.name, frozenset())):
             if name in self.materialized:
