@@ -135,6 +135,8 @@ class HIPCodegen(Codegen):
         self.skinny_matmuls = 0
         self.mfma_matmuls = 0
         self.fused_attentions = 0
+        self.attention_epilogues = 0
+        self.retractable_attention: Dict[str, tuple] = {}  # wave attention output -> (launch index, operands, inputs)
         self.small_contractions = 0
         self.live_block_tables: Dict[tuple, Value] = {}
         self.pending_norms: Dict[str, tuple] = {}  # deferred RMSNorm value -> (meta, x, weight, epsilon)
@@ -1056,14 +1058,7 @@ class HIPCodegen(Codegen):
         count = values.shape[dim]
         if x.dtype not in (torch.float32, torch.bfloat16) or math.prod(values.shape) != rows * count:
             return False
-        popped = self.launches.pop()
-        self.kernels -= 1
-        for buffer in self.resolved_by_launch.pop(len(self.launches), []):
-            self.pending_stores.add(buffer)  # the replacement kernel stages the same operand and writes it
-        if all(launch.kernel != popped.kernel for launch in self.launches):
-            text = next(src for src, name in self.kernel_names.items() if name == popped.kernel)
-            del self.kernel_names[text]
-            self.kernel_sources = [text for text in self.kernel_sources if f" {popped.kernel}(" not in text]
+        self._retract_last_launch()  # the replacement kernel stages the same operand (and writes its pending stores)
         weights = self.allocate(tuple(values.shape), values.dtype)
         k = Kernel(1)
         row = Aff.of(k.atom("blockIdx.x", rows - 1, prefix="r"))
@@ -1105,6 +1100,9 @@ class HIPCodegen(Codegen):
         dtypes = {x.dtype, weight.dtype, meta.dtype} | ({bias.dtype} if bias is not None else set())
         if len(dtypes) != 1:
             raise NotImplementedError(f"mixed-dtype linear {dtypes}")
+        if self.blas and rows <= 16 and self._attention_epilogue(out, x, weight, bias, rows, columns, inner):
+            self.skinny_matmuls += 1
+            return out
         plan = self._stream_plan(rows, inner, meta.dtype, columns * inner * ITEMSIZE[meta.dtype])
         if (self.blas and rows <= 16 and plan is not None and rows * inner <= STAGED_FLOATS
                 and weight.view.offset % (16 // ITEMSIZE[weight.dtype]) == 0):
@@ -1255,10 +1253,12 @@ class HIPCodegen(Codegen):
         splits = -(-keys // SPLIT_KEYS) if keys > 4 * SPLIT_KEYS and tokens * kv_heads < 64 else 1
         if splits == 1 and keys <= WAVE_ATTENTION_KEYS and dim <= 64 and group <= 16:
             # Short key ranges: one wave per query head, wave-level reductions only.
-            k, _, _ = self._attention_kernel(out, q, k_past, k_new, v_past, v_new, mask, sinks, None)
-            k.line(f"chroma::attention_waves<{dim}, {group}, {str(bf16).lower()}>({keys}u, {float_literal(scale)}, "
-                   "load_q, load_k, load_v, load_mask, load_sink, store);")
+            operands = (out, q, k_past, k_new, v_past, v_new, mask, sinks, scale)
+            k = self._waves_attention(*operands)
             self.launch(k, (tokens, kv_heads, 1), 64 * group, inputs, kind="attention")
+            if kv_heads == 1:
+                # a following few-row linear of the whole row may become this kernel's epilogue
+                self.retractable_attention[out.name] = (len(self.launches) - 1, operands, inputs)
         elif splits == 1:
             k, split, _ = self._attention_kernel(out, q, k_past, k_new, v_past, v_new, mask, sinks, None)
             k.line(f"chroma::attention_rows<0, {dim}, {group}, 256, {str(bf16).lower()}>(0u, {keys}u, {float_literal(scale)}, "
@@ -1282,6 +1282,79 @@ class HIPCodegen(Codegen):
             self.launch(k, (tokens, kv_heads, 1), 256, [partial], kind="attention_combine")
         self.fused_attentions += 1
         return out
+
+    def _waves_attention(self, out, q, k_past, k_new, v_past, v_new, mask, sinks, scale, epilogue=None) -> Kernel:
+        """The one-wave-per-query-head attention kernel. ``epilogue`` = (weight, bias, linear output, lanes,
+        steps): the workgroup also multiplies its finished row (all heads, rounded as stored) by W^T from
+        LDS, with W's first step requested before the attention starts."""
+        tokens, kv_heads, group, dim = q.shape
+        keys = (k_past.shape[0] if k_past is not None else 0) + k_new.shape[0]
+        bf16 = out.dtype == torch.bfloat16
+        prelude: List = []
+        store_extra: List[str] = []
+        if epilogue is not None:
+            weight, bias, linear_out, lanes, steps = epilogue
+            ctype, inner, columns = ctype_of(out.dtype), group * dim, weight.shape[0]
+            prelude = [lambda k: f"chroma::StreamStep<{inner}, {lanes}, {steps}, {ctype}> prefetched;",
+                       lambda k: f"chroma::stream_block_fetch(prefetched, {self._matrix_slot(k, weight)}, {columns}u);",
+                       lambda k: f"__shared__ float attention_row[{inner}];"]
+            store_extra = [f"attention_row[g * {dim}u + d] = chroma::storage_round<{str(bf16).lower()}>(value);"]
+        k, _, _ = self._attention_kernel(out, q, k_past, k_new, v_past, v_new, mask, sinks, None, prelude=prelude, store_extra=store_extra)
+        k.line(f"chroma::attention_waves<{dim}, {group}, {str(bf16).lower()}>({keys}u, {float_literal(scale)}, "
+               "load_q, load_k, load_v, load_mask, load_sink, store);")
+        if epilogue is not None:
+            b_arg = self._matrix_slot(k, bias) if bias is not None else "nullptr"
+            out_slot = k.slot(linear_out.name, linear_out.dtype, writable=True, extent=self.extents[linear_out.name])
+            k.line("__syncthreads();")
+            k.line(f"chroma::stream_block_linear<1, {inner}, {lanes}, {steps}, true, {ctype}>(nullptr, attention_row, "
+                   f"{self._matrix_slot(k, weight)}, {b_arg}, {out_slot} + size_t(blockIdx.x) * {columns}u, {columns}u, prefetched);")
+        return k
+
+    def _attention_epilogue(self, out: Value, x: Value, weight: Value, bias: Optional[Value], rows: int, columns: int, inner: int) -> bool:
+        """A few-row linear whose X is exactly the rows of the last launch's wave attention (one workgroup
+        per query row holding every head): the attention launch is replaced by one that also computes this
+        product as its epilogue. False (nothing changed) otherwise."""
+        if not x.stored or x.view is None:
+            return False
+        entry = self.retractable_attention.get(x.root.name)
+        if entry is None or entry[0] != len(self.launches) - 1:
+            return False
+        index, operands, inputs = entry
+        attention_out, q = operands[0], operands[1]
+        tokens, _, group, dim = q.shape
+        natural = contiguous_strides(x.shape)
+        if (x.view.offset or rows != tokens or inner != group * dim or x.dtype not in (torch.float32, torch.bfloat16)
+                or any(size != 1 and a != b for size, a, b in zip(x.shape, x.view.strides, natural))):
+            return False
+        per_chunk = 16 // ITEMSIZE[x.dtype]
+        if inner % per_chunk or weight.view.offset % per_chunk:
+            return False
+        chunks = inner // per_chunk
+        lanes = next((l for l in (64, 32, 16, 8, 4, 2) if chunks % l == 0 and chunks // l >= 4), 1)
+        per_lane = chunks // lanes
+        if per_lane > 16:
+            return False
+        # rows of W per wave step: enough to cover W in one step, at most 16 chunks per lane held
+        steps = max(1, min(16 // per_lane, -(-columns // (64 // lanes * group))))
+        self._retract_last_launch()
+        k = self._waves_attention(*operands, epilogue=(weight, bias, out, lanes, steps))
+        self.launch(k, (tokens, 1, 1), 64 * group, inputs + [weight] + ([bias] if bias is not None else []), kind="attention_linear")
+        self.retractable_attention.pop(x.root.name, None)
+        self.attention_epilogues += 1
+        return True
+
+    def _retract_last_launch(self) -> Launch:
+        """Remove the last launch (its kernel source too when nothing else launches it); the write-through
+        stores it performed become pending again."""
+        popped = self.launches.pop()
+        self.kernels -= 1
+        for buffer in self.resolved_by_launch.pop(len(self.launches), []):
+            self.pending_stores.add(buffer)
+        if all(launch.kernel != popped.kernel for launch in self.launches):
+            text = next(src for src, name in self.kernel_names.items() if name == popped.kernel)
+            del self.kernel_names[text]
+            self.kernel_sources = [text for text in self.kernel_sources if f" {popped.kernel}(" not in text]
+        return popped
 
     def _decode_rows(self, k_past: Optional[Value], v_past: Optional[Value], fresh: int, dim: int) -> Optional[dict]:
         """The in-place layout of the stored key/value rows for ``attention_decode``: {"k"/"v": (stored
@@ -1344,7 +1417,8 @@ class HIPCodegen(Codegen):
         self.launch(k, (tokens, kv_heads, 1), 256, [partial], kind="attention_combine")
 
     def _attention_kernel(self, out, q, k_past, k_new, v_past, v_new, mask, sinks, split, loaders: bool = True,
-                          prelude: Sequence[str] = (), fresh: Optional[Tuple[Tuple[str, ...], str]] = None) -> Tuple[Kernel, str, str]:
+                          prelude: Sequence = (), fresh: Optional[Tuple[Tuple[str, ...], str]] = None,
+                          store_extra: Sequence[str] = ()) -> Tuple[Kernel, str, str]:
         """A kernel over (query row, key/value head) with the attention loaders and the result store
         declared as lambdas (operands read through generated code, so views and fused expressions are
         evaluated in place); returns it with the C expression of its ``AttentionSplit`` and the C
@@ -1358,7 +1432,7 @@ class HIPCodegen(Codegen):
         t = Aff.of(k.atom("blockIdx.x", tokens - 1, prefix="t"))
         h = Aff.of(k.atom("blockIdx.y", kv_heads - 1, prefix="h"))
         for line in prelude:
-            k.line(line)
+            k.line(line(k) if callable(line) else line)
         slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
         scores_shape = (kv_heads, group, tokens, keys)
 
@@ -1429,6 +1503,8 @@ class HIPCodegen(Codegen):
             g_atom, d_atom = Aff.of(Atom("g", group - 1)), Aff.of(Atom("d", dim - 1))
             node = self._lane_values(k, ["value"])
             k.store(slot, out.dtype, Kernel.flatten([t, h, g_atom, d_atom], out.shape), node)
+            for line in store_extra:
+                k.line(line)
         if split is None:
             return k, "", ""
         stats, partial, splits = split
@@ -1881,6 +1957,7 @@ class HIPCodegen(Codegen):
             fused_attentions=self.fused_attentions,
             fused_routers=self.fused_routers,
             small_contractions=self.small_contractions,
+            attention_epilogues=self.attention_epilogues,
             write_through_stores=self.write_through_stores,
             unique_kernels=len(self.kernel_sources),
             launches=len(self.launches),

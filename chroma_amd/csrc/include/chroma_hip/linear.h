@@ -294,6 +294,22 @@ __device__ __forceinline__ void stream_linear(const T* __restrict__ x, const flo
     stream_rows<M, K, LPR, ROWS, STAGED, true, T>(x, xs, w, bias, out, n, n, wave, gridDim.x * waves_per_block, &first);
 }
 
+// The same product by one workgroup alone (its waves split the rows of W), as the epilogue of a kernel
+// that has just produced X in LDS; ``stream_block_fetch`` requests each wave's first step early.
+template <int K, int LPR, int ROWS, class T>
+__device__ __forceinline__ void stream_block_fetch(StreamStep<K, LPR, ROWS, T>& first, const T* __restrict__ w, uint32_t n) {
+    const uint32_t base = threadIdx.x / kWave * StreamStep<K, LPR, ROWS, T>::G * ROWS;
+    if (base < n) {
+        first.fetch(w, base, n);
+    }
+}
+
+template <int M, int K, int LPR, int ROWS, bool STAGED, class T>
+__device__ __forceinline__ void stream_block_linear(const T* __restrict__ x, const float* xs, const T* __restrict__ w, const T* __restrict__ bias,
+                                                    T* __restrict__ out, uint32_t n, StreamStep<K, LPR, ROWS, T>& first) {
+    stream_rows<M, K, LPR, ROWS, STAGED, true, T>(x, xs, w, bias, out, n, n, threadIdx.x / kWave, blockDim.x / kWave, &first);
+}
+
 // Selected-expert products through ``stream_rows``: out[slot, :] = W[expert(slot)] . x[token or slot]^T,
 // reading the chosen expert's [C, K] slab in place (the reference's expert_linear,
 // chroma/_src/codegen/cpu/kernels.h:76-99). Indices wrap when negative; an index outside
