@@ -31,7 +31,7 @@ import numpy as np
 
 from chroma_amd._src import host
 from chroma_amd._src.dtypes import numpy_dtype
-from chroma_amd._src.program import Program
+from chroma_amd._src.program import NativeModel, Program
 
 
 @dataclass(frozen=True)
@@ -60,6 +60,39 @@ def _interrupts_deferred() -> Iterator[None]:
         signal.signal(signal.SIGINT, previous)
         if pending:
             os.kill(os.getpid(), signal.SIGINT)
+
+
+def _staging_mirror(model: Program) -> List[Optional[np.ndarray]]:
+    """The decoder's host input arrays (all but the caches, inputs 2 and 3) for a hip program: page-locked
+    and placed at the same distances from each other as the program's input staging regions, one block
+    per run of adjacent inputs."""
+    native = model.native
+    specs = model.inputs
+    arrays: List[Optional[np.ndarray]] = [None] * len(specs)
+    runs = [[0, 1], [i for i in range(4, len(specs))]]
+    for run in runs:
+        start = native.input_pointer(run[0])
+        sizes = [int(np.prod(specs[i]["shape"])) * numpy_dtype(specs[i]["dtype"]).itemsize for i in run]
+        span = native.input_pointer(run[-1]) - start + sizes[-1]
+        block = host.empty((span,), np.uint8)
+        for i, size in zip(run, sizes):
+            at = native.input_pointer(i) - start
+            arrays[i] = block[at : at + size].view(numpy_dtype(specs[i]["dtype"])).reshape(specs[i]["shape"])
+    return arrays
+
+
+def _fill_row(mask: np.ndarray, allowed: np.ndarray) -> None:
+    """A one-step mask [1, context + 1]: 0 where ``allowed`` over the cached keys, and 0 for the new key."""
+    if mask.dtype == np.float32:
+        row = mask[0]
+        np.copyto(row[:-1], np.float32(-np.inf))
+        row[:-1][allowed] = 0
+        row[-1] = 0
+    else:
+        bits = mask.view(np.uint16)[0]
+        bits[:-1] = 0xFF80
+        bits[:-1][allowed] = 0
+        bits[-1] = 0
 
 
 def _fill_mask(mask: np.ndarray, allowed: np.ndarray) -> None:
@@ -105,12 +138,14 @@ class Decoder:
         self._on_device = all(isinstance(model, Program) for model in self._models) and prefill.device == decode.device
         # Per program: the seven input arrays (the caches are bound at commit time, or stay on the
         # device) and the host arrays for the new K/V rows (device mode leaves those on the device).
-        # (With hip programs the host arrays are page-locked, so their copies go straight over the link.)
+        # (With hip programs the host arrays are page-locked, so their copies go straight over the link, and
+        # laid out like the program's input staging, so each run of them goes up as one copy.)
         empty = host.empty if self._on_device else np.empty
         self._empty_array = empty
         self._buffers: List[Tuple[List[Optional[np.ndarray]], List[Optional[np.ndarray]]]] = [
             (
-                [None if i in (2, 3) else empty(spec["shape"], numpy_dtype(spec["dtype"])) for i, spec in enumerate(model.inputs)],
+                _staging_mirror(model) if self._on_device and isinstance(model.native, NativeModel)
+                else [None if i in (2, 3) else empty(spec["shape"], numpy_dtype(spec["dtype"])) for i, spec in enumerate(model.inputs)],
                 [None if self._on_device else np.empty(spec["shape"], dtype=numpy_dtype(spec["dtype"])) for spec in model.outputs[1:]],
             )
             for model in self._models
@@ -205,15 +240,22 @@ class Decoder:
                 count = min(steps, remaining)
                 state = self._state
                 times = state.position + np.arange(steps, dtype=np.int64)
-                key_times = np.concatenate((state.slots, times))
-                valid = np.concatenate((state.slots >= 0, np.ones(steps, dtype=bool)))
-                causal = valid[None, :] & (key_times[None, :] <= times[:, None])
                 token_ids, positions, _, _, full_mask, window_mask, logit_index = args
                 token_ids.fill(0)
                 token_ids[:count] = ids[offset : offset + count]
                 positions[:] = times
-                for mask, window in ((full_mask, self.context), (window_mask, self._window)):
-                    _fill_mask(mask, causal & (key_times[None, :] > times[:, None] - window))
+                if steps == 1:
+                    # One new key at the current position: every committed key is older, so the causal
+                    # test reduces to validity and each window test to one comparison.
+                    valid = state.slots >= 0
+                    for mask, window in ((full_mask, self.context), (window_mask, self._window)):
+                        _fill_row(mask, valid & (state.slots > state.position - window))
+                else:
+                    key_times = np.concatenate((state.slots, times))
+                    valid = np.concatenate((state.slots >= 0, np.ones(steps, dtype=bool)))
+                    causal = valid[None, :] & (key_times[None, :] <= times[:, None])
+                    for mask, window in ((full_mask, self.context), (window_mask, self._window)):
+                        _fill_mask(mask, causal & (key_times[None, :] > times[:, None] - window))
                 logit_index[0] = count - 1
                 logits = self._empty_array((1, self.vocab_size), self._logit_dtype)
                 rows = times[:count] % self.context

@@ -267,12 +267,32 @@ public:
 
     // A null input pointer leaves that input's staging region as it is (device-resident data from an
     // earlier upload or device copy); a null output pointer skips that output's download.
+    // Consecutive inputs whose host arrays sit in one page-locked block at the same distances as their
+    // staging regions go up as one copy (the gaps are padding on both sides).
     void upload(const void* const* inputs) {
         DeviceGuard guard(device_);
-        for (size_t i = 0; i < plan_.inputs.size(); ++i) {
-            if (plan_.inputs[i].bytes && inputs[i]) {
-                to_device(static_cast<char*>(base_) + plan_.inputs[i].offset, inputs[i], plan_.inputs[i].bytes);
+        const size_t count = plan_.inputs.size();
+        for (size_t i = 0; i < count;) {
+            if (!plan_.inputs[i].bytes || !inputs[i]) {
+                ++i;
+                continue;
             }
+            const char* first = static_cast<const char*>(inputs[i]);
+            const size_t start = plan_.inputs[i].offset;
+            size_t end = i + 1;
+            while (end < count && plan_.inputs[end].bytes && inputs[end] &&
+                   static_cast<const char*>(inputs[end]) - first == std::ptrdiff_t(plan_.inputs[end].offset - start)) {
+                ++end;
+            }
+            const size_t span = plan_.inputs[end - 1].offset + plan_.inputs[end - 1].bytes - start;
+            if (end - i > 1 && is_pinned(first, span)) {
+                to_device(static_cast<char*>(base_) + start, first, span);
+            } else {
+                for (size_t k = i; k < end; ++k) {
+                    to_device(static_cast<char*>(base_) + plan_.inputs[k].offset, inputs[k], plan_.inputs[k].bytes);
+                }
+            }
+            i = end;
         }
     }
 

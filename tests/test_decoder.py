@@ -22,6 +22,7 @@ import pytest
 import torch
 
 from chroma_amd import Decoder, Program
+from chroma_amd._src.dtypes import BFLOAT16
 from chroma_amd._src.decoder import _interrupts_deferred
 from chroma_amd.models.cached import export_cached
 from chroma_amd.models.variants import dev
@@ -266,3 +267,27 @@ def test_interrupts_deferred_until_commit_ends():
             reached.append("inside")
     assert reached == ["inside"]
     assert signal.getsignal(signal.SIGINT) is signal.default_int_handler
+
+
+def test_one_step_masks_match_the_general_rule():
+    """The single-token mask path (validity and one window comparison per cached key) writes the same
+    float32 and bfloat16 masks as the general causal/window rule, over every cache state a decoder of
+    context 7 passes through, before and after wrapping."""
+    from chroma_amd._src.decoder import _fill_mask, _fill_row
+
+    context = 7
+    for position in range(40):
+        slots = np.full(context, -1, dtype=np.int64)
+        for t in range(max(0, position - context), position):
+            slots[t % context] = t
+        times = position + np.arange(1)
+        key_times = np.concatenate((slots, times))
+        valid = np.concatenate((slots >= 0, [True]))
+        causal = valid[None] & (key_times[None] <= times[:, None])
+        for window in range(1, context + 1):
+            for dtype in (np.float32, np.uint16):
+                general, fast = np.empty((1, context + 1), dtype), np.empty((1, context + 1), dtype)
+                as_mask = (lambda m: m) if dtype == np.float32 else (lambda m: m.view(BFLOAT16))
+                _fill_mask(as_mask(general), causal & (key_times[None] > times[:, None] - window))
+                _fill_row(as_mask(fast), (slots >= 0) & (slots > position - window))
+                np.testing.assert_array_equal(general.view(np.uint8), fast.view(np.uint8))
