@@ -431,10 +431,19 @@ class HIPCodegen(Codegen):
         self.kernels += 1
 
     def map_kernel(self, out: Value, value: Value, target: Optional[str] = None) -> None:
-        """out[i] = value[i] over a contiguous destination (an allocation or an output region)."""
+        """out[i] = value[i] over a contiguous destination (an allocation or an output region). bfloat16
+        results take 8 lanes per thread (16-byte accesses) unless some operand could not be read that
+        wide; then 4."""
+        shape = _shape(value.shape)
+        lanes = choose_lanes(shape[-1], value.dtype, 8 if value.dtype == torch.bfloat16 else 4)
+        k, grid = self._map_kernel(out, value, target, lanes)
+        if lanes == 8 and k.scalar_lane_loads:
+            k, grid = self._map_kernel(out, value, target, 4)
+        self.launch(k, grid, MAP_THREADS, [value], kind="map")
+
+    def _map_kernel(self, out: Value, value: Value, target: Optional[str], lanes: int) -> Tuple[Kernel, Union[int, Tuple[int, int, int]]]:
         shape = _shape(value.shape)
         count = math.prod(shape)
-        lanes = choose_lanes(shape[-1], value.dtype)
         k = Kernel(lanes)
         k.streaming = STREAMING_STORES and count * ITEMSIZE[value.dtype] >= STREAMING_BYTES
         k.streaming_loads = STREAMING_BYTES if k.streaming else 0
@@ -460,7 +469,7 @@ class HIPCodegen(Codegen):
             node = self.read(k, value, coords if value.shape else coords[:0])
             k.store(slot, value.dtype, Kernel.flatten(coords, shape), node)
         grid = max(1, min(-(-vectors // MAP_THREADS), MAP_GRID))
-        self.launch(k, (grid, shape[0], 1) if split else grid, MAP_THREADS, [value], kind="map")
+        return k, ((grid, shape[0], 1) if split else grid)
 
     # ==================================================================================== outputs
     def output(self, index: int, value: Value) -> None:

@@ -194,6 +194,7 @@ class Kernel:
         self.shared: List[str] = []
         # Arena buffers this kernel computes from their expressions instead of loading (buffer -> Value),
         # and the subset whose stores this kernel performs.
+        self.scalar_lane_loads = 0  # varying loads that could not be one vector access
         self.unstored: Dict[str, object] = {}
         self.resolved_stores: List[str] = []
         # Values whose elements this kernel has evaluated into a __shared__ float array (value -> array),
@@ -366,11 +367,12 @@ class Kernel:
             return Kernel.node_is_int(node[2][0])
         return False
 
-    def _vector_aligned(self, aff: Aff, vector: Atom) -> bool:
+    def _vector_aligned(self, aff: Aff, vector: Atom, lanes: int = 0) -> bool:
+        lanes = lanes or self.lanes
         rest = aff.without(vector)
         if rest.varying or aff.coefficient(vector) != 1:
             return False
-        return all(c % self.lanes == 0 for _, c in rest.terms) and rest.const % self.lanes == 0
+        return all(c % lanes == 0 for _, c in rest.terms) and rest.const % lanes == 0
 
     def emit(self, node: Node) -> Union[str, List[str]]:
         """Emit ``node`` (and its operands); returns one C name (uniform) or one per lane (varying)."""
@@ -481,11 +483,39 @@ class Kernel:
             self.line(f"const {ctype} {name} = {widen(f'{slot}[{aff.code(0, wide)}]')};")
             return name
         names = [self.fresh("l") for _ in range(self.lanes)]
+        if (vector is not None and self.lanes == 8 and not is_int(dtype) and not self._vector_aligned(aff, vector)
+                and self._vector_aligned(aff, vector, 4)):
+            # 8 lanes on a 4-element alignment: two 4-lane loads
+            base = aff.code(0, wide)
+            for half in range(2):
+                at = f"({base}) + 4u" if half else base
+                raw = self.fresh("v")
+                if dtype == torch.float32:
+                    self.line(f"const float4 {raw} = *reinterpret_cast<const float4*>({slot} + {at});")
+                    for lane in range(4):
+                        self.line(f"const float {names[4 * half + lane]} = {raw}.{'xyzw'[lane]};")
+                else:
+                    self.line(f"const uint2 {raw} = *reinterpret_cast<const uint2*>({slot} + {at});")
+                    for lane in range(4):
+                        word = f"{raw}.{'xy'[lane // 2]}"
+                        bits = f"(uint16_t)({word} & 0xffffu)" if lane % 2 == 0 else f"(uint16_t)({word} >> 16)"
+                        self.line(f"const float {names[4 * half + lane]} = chroma::bf16_to_f32({bits});")
+            return names
         if vector is not None and self.lanes > 1 and not is_int(dtype) and self._vector_aligned(aff, vector):
             base = aff.code(0, wide)
             raw = self.fresh("v")
             itemsize = 4 if dtype == torch.float32 else 2
             streaming = 0 < self.streaming_loads <= self.extents.get(slot, 0) * itemsize
+            if dtype == torch.float32 and self.lanes == 8:
+                # two 16-byte loads
+                halves = [self.fresh("v"), self.fresh("v")]
+                for half, name in enumerate(halves):
+                    at = f"{base} + {4 * half}u" if half else base
+                    load = f"chroma::load_streaming4({slot} + {at})" if streaming else f"*reinterpret_cast<const float4*>({slot} + {at})"
+                    self.line(f"const {'chroma::float4_nt' if streaming else 'float4'} {name} = {load};")
+                for lane, name in enumerate(names):
+                    self.line(f"const float {name} = {halves[lane // 4]}.{'xyzw'[lane % 4]};")
+                return names
             if dtype == torch.float32:
                 vtype = {2: "float2", 4: "float4"}[self.lanes]
                 if streaming:
@@ -494,9 +524,9 @@ class Kernel:
                 else:
                     load = f"*reinterpret_cast<const {vtype}*>({slot} + {base})"
             else:
-                vtype = {2: "uint32_t", 4: "uint2"}[self.lanes]
+                vtype = {2: "uint32_t", 4: "uint2", 8: "uint4"}[self.lanes]
                 if streaming:
-                    vtype = {2: "uint32_t", 4: "chroma::uint2_nt"}[self.lanes]
+                    vtype = {2: "uint32_t", 4: "chroma::uint2_nt", 8: "chroma::uint4_nt"}[self.lanes]
                     load = f"chroma::load_streaming_bf16x{self.lanes}({slot} + {base})"
                 else:
                     load = f"*reinterpret_cast<const {vtype}*>({slot} + {base})"
@@ -513,12 +543,13 @@ class Kernel:
                 for lane, name in enumerate(names):
                     self.line(f"const float {name} = {raw}.{fields[lane]};")
             else:
-                words = [f"{raw}"] if self.lanes == 2 else [f"{raw}.x", f"{raw}.y"]
+                words = [f"{raw}"] if self.lanes == 2 else [f"{raw}.{f}" for f in "xyzw"[: self.lanes // 2]]
                 for lane, name in enumerate(names):
                     word = words[lane // 2]
                     bits = f"(uint16_t)({word} & 0xffffu)" if lane % 2 == 0 else f"(uint16_t)({word} >> 16)"
                     self.line(f"const float {name} = chroma::bf16_to_f32({bits});")
             return names
+        self.scalar_lane_loads += 1
         for lane, name in enumerate(names):
             self.line(f"const {ctype} {name} = {widen(f'{slot}[{aff.code(lane, wide)}]')};")
         return names
@@ -536,6 +567,15 @@ class Kernel:
 
         if vector is not None and self.lanes > 1 and not is_int(dtype) and self._vector_aligned(aff, vector):
             base = aff.code(0, wide)
+            if dtype == torch.float32 and self.lanes == 8:
+                for half in range(2):
+                    at = f"{base} + {4 * half}u" if half else base
+                    quad = per_lane[4 * half : 4 * half + 4]
+                    if self.streaming:
+                        self.line(f"chroma::store_streaming4({slot} + {at}, {', '.join(quad)});")
+                    else:
+                        self.line(f"*reinterpret_cast<float4*>({slot} + {at}) = float4{{{', '.join(quad)}}};")
+                return
             if dtype == torch.float32:
                 if self.streaming:
                     self.line(f"chroma::store_streaming{self.lanes}({slot} + {base}, {', '.join(per_lane)});")
@@ -545,8 +585,8 @@ class Kernel:
             else:
                 bits = [f"uint32_t({narrow(v)})" for v in per_lane]
                 words = [f"({bits[i]} | ({bits[i + 1]} << 16))" for i in range(0, self.lanes, 2)]
-                vtype = {2: "uint32_t", 4: "uint2"}[self.lanes]
-                value = words[0] if self.lanes == 2 else f"uint2{{{words[0]}, {words[1]}}}"
+                vtype = {2: "uint32_t", 4: "uint2", 8: "uint4"}[self.lanes]
+                value = words[0] if self.lanes == 2 else f"{vtype}{{{', '.join(words)}}}"
                 self.line(f"*reinterpret_cast<{vtype}*>({slot} + {base}) = {value};")
             return
         lanes = range(self.lanes) if aff.varying else [0]
@@ -560,10 +600,11 @@ class Kernel:
 
 
 def choose_lanes(extent: int, dtype: torch.dtype, limit: int = 4) -> int:
-    """Lanes per thread along an innermost extent: 4 when it divides, else 2, else 1 (int64: 1)."""
+    """Lanes per thread along an innermost extent: the widest of ``limit`` (at most 8), 4 and 2 that
+    divides it, else 1 (int64: 1)."""
     if is_int(dtype):
         return 1
-    for lanes in (4, 2):
+    for lanes in (8, 4, 2):
         if lanes <= limit and extent % lanes == 0:
             return lanes
     return 1

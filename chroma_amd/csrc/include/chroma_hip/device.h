@@ -95,6 +95,12 @@ __device__ __forceinline__ float2_nt load_streaming2(const float* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const float2_nt*>(p));
 }
 
+typedef unsigned int uint4_nt __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4_nt load_streaming_bf16x8(const uint16_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint4_nt*>(p));
+}
+
 __device__ __forceinline__ uint2_nt load_streaming_bf16x4(const uint16_t* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const uint2_nt*>(p));
 }
