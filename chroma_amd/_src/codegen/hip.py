@@ -55,6 +55,7 @@ STREAMING_BYTES = 64 << 20  # smaller operands and results may stay in L2 / the 
 FUSED_CONCAT_ELEMENTS = 1 << 16  # smaller concatenations are fused into their consumers
 DEFERRED_ELEMENTS = 1 << 16  # smaller expressions the front end asks to store stay fused instead...
 DEFERRED_SOURCES = 4  # ...when they read at most this many buffers (a residual stream is stored every few adds)
+CHEAP_EXPRESSION_COST = 6  # larger expressions stay fused too when one element costs at most this much
 REUSED_EVALUATIONS = 1 << 18  # a contraction operand is stored when (elements x reuse) reaches this
 SMALL_REDUCTION = 8  # contractions summing at most this many products are fused expressions...
 SMALL_OPERAND_COST = 8  # ...over operands that cost at most this much per element (others are stored)
@@ -250,6 +251,10 @@ class HIPCodegen(Codegen):
         if value.name in self.pending_norms:
             return value  # consumers that stage their rows fold it; any other reader stores it
         if math.prod(value.shape) <= DEFERRED_ELEMENTS and len(self.sources[value.name]) <= DEFERRED_SOURCES:
+            return value
+        if math.prod(value.shape) > DEFERRED_ELEMENTS and value.name in self.closures and self.cost(value) <= CHEAP_EXPRESSION_COST:
+            # a large elementwise result that costs a few loads per element: each consumer re-reading its
+            # sources moves fewer bytes than writing it and reading it back
             return value
         if self.blas and value.name in self.closures and value.name not in self.materialized and math.prod(value.shape) <= STAGED_FLOATS:
             out = self.allocate(value.shape, value.dtype)
