@@ -56,6 +56,7 @@ FUSED_CONCAT_ELEMENTS = 1 << 16  # smaller concatenations are fused into their c
 DEFERRED_ELEMENTS = 1 << 16  # smaller expressions the front end asks to store stay fused instead...
 DEFERRED_SOURCES = 4  # ...when they read at most this many buffers (a residual stream is stored every few adds)
 CHEAP_EXPRESSION_COST = 6  # larger expressions stay fused too when one element costs at most this much
+MFMA_CUS = 256  # compute units of the target (MI355X), for the tile-round choice of the matrix-core products
 REUSED_EVALUATIONS = 1 << 18  # a contraction operand is stored when (elements x reuse) reaches this
 SMALL_REDUCTION = 8  # contractions summing at most this many products are fused expressions...
 SMALL_OPERAND_COST = 8  # ...over operands that cost at most this much per element (others are stored)
@@ -1214,8 +1215,12 @@ class HIPCodegen(Codegen):
         k = Kernel(1)
         args = [self._matrix_slot(k, x), self._matrix_slot(k, weight), self._matrix_slot(k, bias) if bias is not None else "nullptr"]
         out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
-        k.line(f"chroma::mfma_linear<{ctype_of(out.dtype)}>({args[0]}, {args[1]}, {args[2]}, {out_slot}, {rows}u, {columns}u, {inner}u);")
-        self.launch(k, (-(-columns // 128), -(-rows // 128), 1), 256, [x, weight] + ([bias] if bias is not None else []), kind="linear_mfma")
+        tiles = -(-columns // 128) * -(-rows // 128)
+        # the 64-deep body (two workgroups per CU) when every tile fits in one round of the chip, else the
+        # 32-deep body (three per CU), whose rounds quantize less
+        path = 0 if tiles <= 2 * MFMA_CUS else 1
+        k.line(f"chroma::mfma_linear<{ctype_of(out.dtype)}, {path}>({args[0]}, {args[1]}, {args[2]}, {out_slot}, {rows}u, {columns}u, {inner}u);")
+        self.launch(k, 8 * -(-tiles // 8), 256, [x, weight] + ([bias] if bias is not None else []), kind="linear_mfma")
 
     def _tiled_linear(self, out, x, weight, bias, rows, columns, inner) -> None:
         k = Kernel(1)
@@ -1828,7 +1833,8 @@ class HIPCodegen(Codegen):
         k.check_bounds(out_slot, out_offset + ((rows - 1) * out_strides[row] + columns - 1))
         k.line(
             f"chroma::mfma_gemm<{ctype_of(dtype)}, {str(k_contiguous).lower()}>({pointers[0]}, {left[row]}u, {pointers[1]}, {ldb}u, "
-            f"nullptr, {out_slot} + ({out_offset.code()}), {out_strides[row]}u, {rows}u, {columns}u, {depth}u, nullptr, nullptr, blockIdx.y * 128u);"
+            f"nullptr, {out_slot} + ({out_offset.code()}), {out_strides[row]}u, {rows}u, {columns}u, {depth}u, nullptr, nullptr, "
+            f"blockIdx.y * 128u, blockIdx.x * 128u);"
         )
         self.launch(k, (-(-columns // 128), -(-rows // 128), batches), 256, operands, kind="matmul_mfma")
         self.matrix_contractions += 1
@@ -1859,10 +1865,10 @@ class HIPCodegen(Codegen):
         table = k.slot(scratch.name, torch.int64, extent=self.extents[scratch.name])
         out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
         k.line(
-            f"chroma::grouped_expert_linear<{ctype_of(out.dtype)}, {str(per_slot).lower()}>({w}, {xs}, {out_slot}, "
+            f"chroma::grouped_expert_linear<{ctype_of(out.dtype)}, {str(per_slot).lower()}, 1>({w}, {xs}, {out_slot}, "
             f"reinterpret_cast<const int32_t*>({table}), {tokens * selected}u, {selected}u, {experts}u, {channels}u, {inner}u);"
         )
-        self.launch(k, (-(-channels // 128), tiles, 1), 256, [weight, x, scratch], kind="experts_mfma")
+        self.launch(k, 8 * -(-(-(-channels // 128) * tiles) // 8), 256, [weight, x, scratch], kind="experts_mfma")
         self.mfma_matmuls += 1
 
     def _loop_einsum(self, meta, labels, output, sizes, reduction, values) -> Value:

@@ -577,11 +577,143 @@ template <> struct Mfma<float> {
     using Chunk = float4;
 };
 
+// Store a wave's 4 x 4 accumulator tiles (rows m0 + wm 64 .., columns n0 + wn 64 ..), one rounding each.
+template <class T>
+__device__ __forceinline__ void mfma_store(const f32x4_t (&acc)[4][4], const T* __restrict__ bias, T* __restrict__ c,
+                                           uint32_t ldc, uint32_t m_total, uint32_t n_total,
+                                           const int32_t* __restrict__ c_rows, uint32_t m0, uint32_t n0) {
+    const uint32_t lane = threadIdx.x % 64u, wave = threadIdx.x / 64u;
+    const uint32_t wm = wave / 2u, wn = wave % 2u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t gn = n0 + wn * 64u + j * 16u + lane % 16u;
+            if (gn >= n_total) {
+                continue;
+            }
+            const float offset = bias ? load1<T>(bias + gn) : 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t gm = m0 + wm * 64u + i * 16u + (lane / 16u) * 4u + r;
+                if (gm < m_total) {
+                    const size_t crow = c_rows ? size_t(c_rows[gm]) : size_t(gm);
+                    store1<T>(c + crow * ldc + gn, acc[i][j][r] + offset);
+                }
+            }
+        }
+    }
+}
+
+// bfloat16 with a k-contiguous B and K a multiple of 64: 64-deep slices, so each slice feeds 32 MFMAs per
+// wave between the issue of the next slice's loads and the wait for them (twice the cover of 32-deep
+// slices, half the barriers). Every thread moves the same four A rows and four B rows at every slice, so
+// their addresses are formed once; rows past the edge of the tile repeat the last valid row (their
+// results are never stored), which keeps every load unconditional and in bounds. The MFMA sequence per
+// accumulator is the one of the 32-deep path, so both give the same bits.
+// LDS placement of 16-byte chunk ``chunk`` (0..7) of tile row ``row`` in the 64-deep path: unpadded
+// 128-byte rows with the chunk index XORed by the row's low bits, so the 16 rows one fragment read touches
+// and the 8 chunks one row write touches all fall in distinct banks (no LDS bank-conflict cycles on gfx950).
+__device__ __forceinline__ uint32_t deep_lds(uint32_t row, uint32_t chunk) { return row * 64u + ((chunk ^ (row & 7u)) * 8u); }
+
+__device__ __forceinline__ void mfma_gemm_deep(const uint16_t* __restrict__ a, uint32_t lda, const uint16_t* __restrict__ b,
+                                               uint32_t ldb, const uint16_t* __restrict__ bias, uint16_t* __restrict__ c,
+                                               uint32_t ldc, uint32_t m_total, uint32_t n_total, uint32_t k_total,
+                                               const int32_t* __restrict__ a_rows, const int32_t* __restrict__ c_rows,
+                                               uint32_t m_base, uint32_t n_base) {
+    constexpr int BM = 128, BN = 128, BK = 64, LD = 64, CH = 8;
+    constexpr int CHUNKS = BM * BK / CH / 256;  // 16-byte chunks per thread and operand per slice
+    __shared__ __attribute__((aligned(16))) uint16_t as[2][BM * LD];
+    __shared__ __attribute__((aligned(16))) uint16_t bs[2][BN * LD];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid % 64u, wave = tid / 64u;
+    const uint32_t wm = wave / 2u, wn = wave % 2u;
+    const uint32_t m0 = m_base, n0 = n_base;
+    if (m0 >= m_total) {
+        return;
+    }
+    const uint32_t kc = (tid % (BK / CH)) * CH;
+    const uint16_t* pa[CHUNKS];
+    const uint16_t* pb[CHUNKS];
+#pragma unroll
+    for (int i = 0; i < CHUNKS; ++i) {
+        const uint32_t row = tid / (BK / CH) + i * (256u / (BK / CH));
+        const uint32_t gm = m0 + row < m_total ? m0 + row : m_total - 1u;
+        const uint32_t gn = n0 + row < n_total ? n0 + row : n_total - 1u;
+        pa[i] = a + (a_rows ? size_t(a_rows[gm]) : size_t(gm)) * lda + kc;
+        pb[i] = b + size_t(gn) * ldb + kc;
+    }
+    uint32_t srow[CHUNKS];
+#pragma unroll
+    for (int i = 0; i < CHUNKS; ++i) {
+        srow[i] = deep_lds(tid / (BK / CH) + i * (256u / (BK / CH)), tid % (BK / CH));
+    }
+    uint4 ra[CHUNKS], rb[CHUNKS];
+#pragma unroll
+    for (int i = 0; i < CHUNKS; ++i) {
+        ra[i] = *reinterpret_cast<const uint4*>(pa[i]);
+        rb[i] = *reinterpret_cast<const uint4*>(pb[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < CHUNKS; ++i) {
+        *reinterpret_cast<uint4*>(&as[0][srow[i]]) = ra[i];
+        *reinterpret_cast<uint4*>(&bs[0][srow[i]]) = rb[i];
+    }
+    f32x4_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
+    const uint32_t steps = k_total / BK;
+    __syncthreads();
+    for (uint32_t step = 0; step < steps; ++step) {
+        const int buffer = step & 1;
+        const bool more = step + 1 < steps;
+        const uint32_t k_next = more ? (step + 1) * BK : 0u;  // the last slice re-reads slice 0, unused
+#pragma unroll
+        for (int i = 0; i < CHUNKS; ++i) {
+            ra[i] = *reinterpret_cast<const uint4*>(pa[i] + k_next);
+            rb[i] = *reinterpret_cast<const uint4*>(pb[i] + k_next);
+        }
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            bf16x8_t fa[4], fb[4];
+            const uint32_t chunk = half * 4u + lane / 16u;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint32_t ia = deep_lds(wm * 64u + t * 16u + lane % 16u, chunk);
+                const uint32_t ib = deep_lds(wn * 64u + t * 16u + lane % 16u, chunk);
+                fa[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(&as[buffer][ia]));
+                fb[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(&bs[buffer][ib]));
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < CHUNKS; ++i) {
+                *reinterpret_cast<uint4*>(&as[buffer ^ 1][srow[i]]) = ra[i];
+                *reinterpret_cast<uint4*>(&bs[buffer ^ 1][srow[i]]) = rb[i];
+            }
+        }
+        __syncthreads();
+    }
+    mfma_store<uint16_t>(acc, bias, c, ldc, m_total, n_total, c_rows, m0, n0);
+}
+
 template <class T, bool B_K_CONTIGUOUS>
-__device__ __forceinline__ void mfma_gemm(const T* __restrict__ a, uint32_t lda, const T* __restrict__ b, uint32_t ldb,
-                                          const T* __restrict__ bias, T* __restrict__ c, uint32_t ldc, uint32_t m_total,
-                                          uint32_t n_total, uint32_t k_total, const int32_t* __restrict__ a_rows,
-                                          const int32_t* __restrict__ c_rows, uint32_t m_base) {
+__device__ __forceinline__ void mfma_gemm_sliced(const T* __restrict__ a, uint32_t lda, const T* __restrict__ b, uint32_t ldb,
+                                                 const T* __restrict__ bias, T* __restrict__ c, uint32_t ldc, uint32_t m_total,
+                                                 uint32_t n_total, uint32_t k_total, const int32_t* __restrict__ a_rows,
+                                                 const int32_t* __restrict__ c_rows, uint32_t m_base, uint32_t n_base) {
     using M = Mfma<T>;
     using Chunk = typename M::Chunk;
     constexpr int BM = 128, BN = 128, BK = M::BK, LD = BK + M::PAD, CH = M::CHUNK;
@@ -591,7 +723,7 @@ __device__ __forceinline__ void mfma_gemm(const T* __restrict__ a, uint32_t lda,
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid % 64u, wave = tid / 64u;
     const uint32_t wm = wave / 2u, wn = wave % 2u;
-    const uint32_t m0 = m_base, n0 = blockIdx.x * BN;
+    const uint32_t m0 = m_base, n0 = n_base;
 
     Chunk ra[A_CHUNKS], rb[A_CHUNKS];
     auto fetch = [&](uint32_t k0) {
@@ -688,32 +820,55 @@ __device__ __forceinline__ void mfma_gemm(const T* __restrict__ a, uint32_t lda,
         }
         __syncthreads();
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t gn = n0 + wn * 64u + j * 16u + lane % 16u;
-            if (gn >= n_total) {
-                continue;
-            }
-            const float offset = bias ? load1<T>(bias + gn) : 0.0f;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t gm = m0 + wm * 64u + i * 16u + (lane / 16u) * 4u + r;
-                if (gm < m_total) {
-                    const size_t crow = c_rows ? size_t(c_rows[gm]) : size_t(gm);
-                    store1<T>(c + crow * ldc + gn, acc[i][j][r] + offset);
-                }
-            }
-        }
-    }
+    mfma_store<T>(acc, bias, c, ldc, m_total, n_total, c_rows, m0, n0);
 }
 
-// A linear layer on the matrix cores: Y[M, N] = X[M, K] . W[N, K]^T (+ bias).
-template <class T>
+// PATH 0 takes the 64-deep bfloat16 path whenever its conditions hold; PATH 1 always takes the sliced one.
+template <class T, bool B_K_CONTIGUOUS, int PATH = 0>
+__device__ __forceinline__ void mfma_gemm(const T* __restrict__ a, uint32_t lda, const T* __restrict__ b, uint32_t ldb,
+                                          const T* __restrict__ bias, T* __restrict__ c, uint32_t ldc, uint32_t m_total,
+                                          uint32_t n_total, uint32_t k_total, const int32_t* __restrict__ a_rows,
+                                          const int32_t* __restrict__ c_rows, uint32_t m_base, uint32_t n_base) {
+    if constexpr (sizeof(T) == 2 && B_K_CONTIGUOUS && PATH == 0) {
+        if (k_total % 64u == 0 && lda % 8u == 0 && ldb % 8u == 0) {
+            mfma_gemm_deep(a, lda, b, ldb, bias, c, ldc, m_total, n_total, k_total, a_rows, c_rows, m_base, n_base);
+            return;
+        }
+    }
+    mfma_gemm_sliced<T, B_K_CONTIGUOUS>(a, lda, b, ldb, bias, c, ldc, m_total, n_total, k_total, a_rows, c_rows, m_base, n_base);
+}
+
+// XCD-aware tile order. Workgroups are handed to the 8 XCDs (each with its own L2) round-robin by
+// workgroup id, so neighbouring ids land on different L2s. A launch of 8 * ceil(tiles / 8) workgroups
+// instead gives XCD j the contiguous logical tiles [j * per, (j + 1) * per): tiles that share operand rows
+// run on one L2, and each operand tile is fetched from HBM by one XCD instead of by all eight. Returns
+// false for the padding workgroups.
+__device__ __forceinline__ bool xcd_logical_tile(uint32_t tiles, uint32_t& logical) {
+    const uint32_t per = (tiles + 7u) / 8u;
+    const uint32_t p = blockIdx.x;
+    logical = (p % 8u) * per + p / 8u;
+    return p / 8u < per && logical < tiles;
+}
+
+// A linear layer on the matrix cores: Y[M, N] = X[M, K] . W[N, K]^T (+ bias). One-dimensional launch of
+// 8 * ceil(tiles / 8) workgroups (tiles = ceil(M / 128) * ceil(N / 128)); logical tiles run down groups of
+// 8 row tiles before moving to the next column tile, so an XCD's run of tiles covers a compact block of
+// X rows and W rows.
+template <class T, int PATH = 0>
 __device__ __forceinline__ void mfma_linear(const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias,
                                             T* __restrict__ out, uint32_t m_total, uint32_t n_total, uint32_t k_total) {
-    mfma_gemm<T, true>(x, k_total, w, k_total, bias, out, n_total, m_total, n_total, k_total, nullptr, nullptr, blockIdx.y * 128u);
+    const uint32_t gx = (n_total + 127u) / 128u, gy = (m_total + 127u) / 128u;
+    uint32_t logical;
+    if (!xcd_logical_tile(gx * gy, logical)) {
+        return;
+    }
+    constexpr uint32_t G = 8;
+    const uint32_t group = logical / (G * gx), first = group * G;
+    const uint32_t height = gy - first < G ? gy - first : G;
+    const uint32_t within = logical - group * G * gx;
+    const uint32_t ty = first + within % height, tx = within / height;
+    mfma_gemm<T, true, PATH>(x, k_total, w, k_total, bias, out, n_total, m_total, n_total, k_total, nullptr, nullptr, ty * 128u,
+                             tx * 128u);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -773,22 +928,61 @@ __device__ __forceinline__ void route_slots(const int64_t* __restrict__ indices,
     }
 }
 
+// Logical order of the grouped products: expert by expert, and inside an expert column tile by column
+// tile with that expert's row tiles adjacent, so the row tiles that share a slab of W[e] run together and
+// an XCD's run of logical tiles reads each slab once. Expert e owns logical tiles
+// [gx * first_e, gx * (first_e + n_e)), n_e = ceil(count_e / 128) row tiles starting at tile first_e of the
+// routing table. Every wave finds (row tile, column tile) of ``logical`` with a wave-wide scan of the
+// per-expert counts; ``logical`` < gx * (tile count) always has one.
+__device__ __forceinline__ void expert_tile_of(const int32_t* __restrict__ counts, uint32_t experts, uint32_t gx,
+                                               uint32_t logical, uint32_t& tile, uint32_t& column) {
+    const uint32_t lane = threadIdx.x % kWave;
+    uint32_t carry = 0;
+    tile = 0;
+    column = 0;
+    for (uint32_t e0 = 0; e0 < experts; e0 += kWave) {
+        const uint32_t e = e0 + lane;
+        const uint32_t n = e < experts ? (uint32_t(counts[e]) + 127u) / 128u : 0u;
+        uint32_t inclusive = n;
+#pragma unroll
+        for (int d = 1; d < kWave; d <<= 1) {
+            const uint32_t up = __shfl_up(inclusive, d, kWave);
+            inclusive += lane >= uint32_t(d) ? up : 0u;
+        }
+        const uint32_t first = carry + inclusive - n;
+        const unsigned long long hit = __ballot(n > 0 && gx * first <= logical && logical < gx * (first + n));
+        if (hit) {
+            const int source = __ffsll(hit) - 1;
+            const uint32_t f = __shfl(first, source, kWave), count = __shfl(n, source, kWave);
+            const uint32_t r = logical - gx * f;
+            column = r / count;
+            tile = f + r % count;
+            return;
+        }
+        carry += __shfl(inclusive, kWave - 1, kWave);
+    }
+}
+
 // Per-slot input rows (``PER_SLOT``: X is [slots, K]) or per-token rows (X is [tokens, K], token = slot /
-// selected). ``rows`` receives the A-row of each permuted slot and is filled by the first block of each
-// tile before its product; grid = (ceil(C / 128), max tiles).
-template <class T, bool PER_SLOT>
+// selected). ``rows`` receives the A-row of each permuted slot and is filled by each workgroup before its
+// product. One-dimensional launch of 8 * ceil(ceil(C / 128) * max tiles / 8) workgroups, mapped to tiles
+// in the expert-major, XCD-aware order above; workgroups past gx * (tile count) return at once.
+template <class T, bool PER_SLOT, int PATH = 0>
 __device__ __forceinline__ void grouped_expert_linear(const T* __restrict__ w, const T* __restrict__ x, T* __restrict__ out,
                                                       const int32_t* __restrict__ scratch, uint32_t slots, uint32_t selected,
                                                       uint32_t experts, uint32_t channels, uint32_t inner) {
     __shared__ int32_t a_rows[128], c_rows[128];
     const int32_t* offsets = scratch + experts;
-    const int32_t tile_count = scratch[2 * experts + 1];
+    const uint32_t tile_count = uint32_t(scratch[2 * experts + 1]);
     const int32_t* permutation = scratch + 2 * experts + 2;
     const int32_t* tiles = permutation + slots;
-    const int32_t tile = int32_t(blockIdx.y);
-    if (tile >= tile_count) {
+    const uint32_t gx = (channels + 127u) / 128u;
+    uint32_t logical;
+    if (!xcd_logical_tile(gx * tile_count, logical)) {
         return;
     }
+    uint32_t tile, column;
+    expert_tile_of(scratch, experts, gx, logical, tile, column);
     const uint32_t expert = uint32_t(tiles[2 * tile]);
     const uint32_t first = uint32_t(tiles[2 * tile + 1]);
     const uint32_t count = uint32_t(offsets[expert + 1] - offsets[expert]);
@@ -799,8 +993,8 @@ __device__ __forceinline__ void grouped_expert_linear(const T* __restrict__ w, c
         c_rows[r] = slot;
     }
     __syncthreads();
-    mfma_gemm<T, true>(x, inner, w + size_t(expert) * channels * inner, inner, nullptr, out, channels, rows, channels, inner,
-                       a_rows, c_rows, 0u);
+    mfma_gemm<T, true, PATH>(x, inner, w + size_t(expert) * channels * inner, inner, nullptr, out, channels, rows, channels, inner,
+                             a_rows, c_rows, 0u, column * 128u);
 }
 
 }  // namespace chroma

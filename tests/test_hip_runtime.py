@@ -181,9 +181,13 @@ def test_weight_streaming_linear(tmp_path, dtype, rows, inner, columns):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("rows, inner, columns", [(300, 200, 384), (129, 64, 130), (17, 2888, 96)])
+@pytest.mark.parametrize(
+    "rows, inner, columns", [(300, 200, 384), (129, 64, 130), (17, 2888, 96), (1100, 192, 260), (2100, 64, 4000)]
+)
 def test_matrix_core_linear(tmp_path, dtype, rows, inner, columns):
-    """MFMA products with partial 128 x 128 tiles and a partial last K step, against the oracle."""
+    """MFMA products with partial 128 x 128 tiles and a partial last K step, against the oracle. 1100 rows
+    make 9 row tiles (a second, one-tile-high group of the XCD-aware order); 2100 x 4000 makes 544 tiles,
+    past one round of the 64-deep body."""
     generator = torch.Generator().manual_seed(rows + inner)
     layer = torch.nn.Linear(inner, columns).eval()
     with torch.no_grad():
@@ -228,10 +232,12 @@ def test_matrix_core_contractions(tmp_path, dtype):
         compare(got, compile_cpu(exported, tmp_path / f"{name}-cpu")(*[numpy_of(v) for v in inputs]))
 
 
+@pytest.mark.parametrize("experts", [6, 70])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_grouped_expert_products(tmp_path, dtype):
+def test_grouped_expert_products(tmp_path, dtype, experts):
     """Many-token selected-expert contractions take the routed, expert-grouped MFMA path; negative ids wrap
-    and an out-of-range id raises IndexError without poisoning the next call."""
+    and an out-of-range id raises IndexError without poisoning the next call. 70 experts span two 64-wide
+    chunks of the tile lookup and leave most experts without a tile."""
 
     class Experts(torch.nn.Module):
         def forward(self, weights, indices, x, per_slot):
@@ -239,8 +245,8 @@ def test_grouped_expert_products(tmp_path, dtype):
             return torch.einsum("beck,bk->bec", selected, x), torch.einsum("beck,bek->bec", selected, per_slot)
 
     generator = torch.Generator().manual_seed(3)
-    weights = (torch.randn(6, 160, 72, generator=generator) * 0.2).to(dtype)
-    indices = torch.randint(-6, 6, (40, 3), generator=generator)
+    weights = (torch.randn(experts, 160, 72, generator=generator) * 0.2).to(dtype)
+    indices = torch.randint(-experts, experts, (40, 3), generator=generator)
     x = torch.randn(40, 72, generator=generator).to(dtype)
     per_slot = torch.randn(40, 3, 72, generator=generator).to(dtype)
     inputs = (weights, indices, x, per_slot)
@@ -250,7 +256,7 @@ def test_grouped_expert_products(tmp_path, dtype):
         assert model.stats["expert_contractions"] == 2 and model.stats["mfma_matmuls"] == 2
         compare(model(*inputs), oracle(*[numpy_of(v) for v in inputs]))
         bad = indices.clone()
-        bad[7, 1] = 6
+        bad[7, 1] = experts
         with pytest.raises(IndexError):
             model(weights, bad, x, per_slot)
         compare(model(*inputs), oracle(*[numpy_of(v) for v in inputs]))
