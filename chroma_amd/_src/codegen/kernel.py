@@ -181,6 +181,9 @@ class Kernel:
         self.indent = 1
         self.definitions: Dict[str, Tuple[str, "Aff", int]] = {}  # opaque atom -> (op, operand, constant)
         self.uses_error = False
+        # Waves per SIMD the register allocation must leave room for (0: the compiler's choice); a
+        # latency-bound kernel trades a few registers for more resident workgroups.
+        self.min_waves = 0
         self.streaming = False  # vector float stores bypass the caches (results read by later kernels only)
         # Vector loads from buffers of at least this many bytes bypass the caches too (0: never). Set on
         # kernels that read each element of their large operands once.
@@ -594,7 +597,8 @@ class Kernel:
             self.line(f"{slot}[{aff.code(lane, wide)}] = {narrow(per_lane[lane])};")
 
     def render(self, name: str, launch_bounds: int, prologue: Sequence[str] = ()) -> str:
-        head = f'extern "C" __global__ void __launch_bounds__({launch_bounds}) {name}({", ".join(self.parameters())}) {{'
+        bounds = f"{launch_bounds}, {self.min_waves}" if self.min_waves else f"{launch_bounds}"
+        head = f'extern "C" __global__ void __launch_bounds__({bounds}) {name}({", ".join(self.parameters())}) {{'
         body = [f"    {line}" for line in prologue] + self.lines
         return "\n".join([head, *body, "}"])
 

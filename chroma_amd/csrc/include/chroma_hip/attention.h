@@ -620,32 +620,45 @@ struct AttentionOperands {
     const uint8_t* live_blocks;  // [query blocks][key blocks]: 0 where the mask is -inf throughout (or nullptr)
 };
 
-// live_blocks[qb * key_blocks + kb] = whether any mask value of queries [64 qb, 64 qb + 64) and keys
-// [32 kb, 32 kb + 32) is not -inf, for a mask shared by every head (grid: query blocks x key blocks).
+// live_blocks[qb * key_blocks + kb] for queries [64 qb, 64 qb + 64) and keys [32 kb, 32 kb + 32) of a mask
+// shared by every head: 0 when every mask value there is -inf, 2 when every one is +0.0 (the block needs
+// no mask reads: adding +0.0 to a score changes no bit), 1 otherwise (grid: query blocks x key blocks).
 __device__ __forceinline__ void attention_live_blocks(const uint16_t* __restrict__ mask, uint32_t mt, uint32_t tokens, uint32_t keys,
                                                       uint8_t* __restrict__ live_blocks) {
     const uint32_t qb = blockIdx.x, kb = blockIdx.y;
-    bool any = false;
+    bool any = false, zero = true;
     for (uint32_t i = threadIdx.x; i < 64u * 32u; i += blockDim.x) {
         const uint32_t t = qb * 64u + i / 32u, j = kb * 32u + i % 32u;
         if (t < tokens && j < keys) {
-            any |= mask[size_t(t) * mt + j] != 0xff80u;
+            const uint16_t bits = mask[size_t(t) * mt + j];
+            any |= bits != 0xff80u;
+            zero &= bits == 0u;
         }
     }
     any = __syncthreads_or(any);
+    zero = __syncthreads_and(zero);
     if (threadIdx.x == 0) {
-        live_blocks[qb * gridDim.y + kb] = any ? 1 : 0;
+        live_blocks[qb * gridDim.y + kb] = any ? (zero ? 2 : 1) : 0;
     }
 }
+
+// Longest live-block list a workgroup keeps in LDS (key blocks of 32, so 64K keys); longer key ranges
+// scan the table in place.
+constexpr uint32_t kLiveListMax = 2048;
 
 template <int D> __device__ __forceinline__ void attention_mfma_bf16(const AttentionOperands& a) {
     static_assert(D % 32 == 0 && D <= 128, "head dimension");
     constexpr int KB = 32, KPAD = D + 8, VPAD = KB + 8;
+    constexpr uint32_t CHUNKS = (KB * D / 8 + 255) / 256;  // 16-byte K (and V) chunks each thread stages per block
     __shared__ __attribute__((aligned(16))) uint16_t k_s[KB * KPAD];
     __shared__ __attribute__((aligned(16))) uint16_t v_s[D * VPAD];
+    __shared__ uint16_t live_list[kLiveListMax];
+    __shared__ uint32_t live_total;
     const uint32_t tid = threadIdx.x, lane = tid % 64u, wave = tid / 64u, quad = lane / 16u, col = lane % 16u;
     const uint32_t head = blockIdx.y, kv = head / a.group, g = head % a.group;
-    const uint32_t block_q0 = blockIdx.x * 64u;
+    // Later query blocks see more keys under a causal mask: they are dispatched first.
+    const uint32_t query_block = gridDim.x - 1u - blockIdx.x;
+    const uint32_t block_q0 = query_block * 64u;
     const uint32_t query = block_q0 + wave * 16u + col;
     const bool live = query < a.tokens;
     const uint32_t qrow = live ? query : a.tokens - 1u;
@@ -658,36 +671,68 @@ template <int D> __device__ __forceinline__ void attention_mfma_bf16(const Atten
     const uint16_t* mask_row = a.mask + size_t(qrow) * a.mt + kv * a.mh + g * a.mg;
     const float neg_inf = -__builtin_inff();
 
-    // The mask values of this lane's 8 scores in key block kb (-inf past the last key or query).
-    auto masks = [&](uint32_t kb, float (&m)[8]) -> bool {
+    // Every global read below is unconditional, its index clamped into range, and what lies out of range
+    // is replaced when the data is consumed: a guarded load would end its own branch with a wait for every
+    // outstanding load, the prefetched block's included.
+    // Mask words of this lane's 8 scores in key block kb, and their values (-inf past the last key or query).
+    auto mask_fetch = [&](uint32_t kb, uint32_t (&raw)[8]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t j = kb * KB + (i < 4 ? quad * 4u + i : 16u + quad * 4u + (i - 4));
+            raw[i] = mask_row[j < a.keys ? j : a.keys - 1u];
+        }
+    };
+    auto mask_values = [&](uint32_t kb, const uint32_t (&raw)[8], float (&m)[8], bool zero = false) -> bool {
         bool any = false;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const uint32_t j = kb * KB + (i < 4 ? quad * 4u + i : 16u + quad * 4u + (i - 4));
-            m[i] = (live && j < a.keys) ? bf16_to_f32(mask_row[j]) : neg_inf;
+            m[i] = (live && j < a.keys) ? (zero ? 0.0f : __uint_as_float(raw[i] << 16)) : neg_inf;
             any |= m[i] != neg_inf;
         }
         return any;
     };
-    auto stage = [&](uint32_t kb, bool values) {
-        for (uint32_t c = tid; c < uint32_t(KB * D / 8); c += 256u) {
-            const uint32_t r = c / (D / 8), dc = (c % (D / 8)) * 8u, j = kb * KB + r;
-            uint4 kv_k = uint4{0, 0, 0, 0}, kv_v = uint4{0, 0, 0, 0};
-            if (j < a.keys) {
-                const bool old = j < a.past;
-                const size_t kr = old ? size_t(j) * a.kpj + kv * a.kph : size_t(j - a.past) * a.knj + kv * a.knh;
-                kv_k = *reinterpret_cast<const uint4*>((old ? a.k_past : a.k_new) + kr + dc);
-                if (values) {
-                    const size_t vr = old ? size_t(j) * a.vpj + kv * a.vph : size_t(j - a.past) * a.vnj + kv * a.vnh;
-                    kv_v = *reinterpret_cast<const uint4*>((old ? a.v_past : a.v_new) + vr + dc);
-                }
-            }
-            *reinterpret_cast<uint4*>(&k_s[r * KPAD + dc]) = kv_k;
-            if (values) {
-                const uint16_t* e = reinterpret_cast<const uint16_t*>(&kv_v);
+    auto masks = [&](uint32_t kb, float (&m)[8]) -> bool {
+        uint32_t raw[8];
+        mask_fetch(kb, raw);
+        return mask_values(kb, raw, m);
+    };
+    // Global -> registers: this thread's K (and V) chunks of key block kb; bit i of ``valid`` says whether
+    // chunk i is a real key row (``put`` writes zeros for the others).
+    auto fetch = [&](uint32_t kb, bool values, uint4 (&rk)[CHUNKS], uint4 (&rv)[CHUNKS], uint32_t& valid) {
+        valid = 0;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    v_s[(dc + i) * VPAD + r] = e[i];
+        for (uint32_t i = 0; i < CHUNKS; ++i) {
+            const uint32_t c = tid + i * 256u;
+            const uint32_t cc = c < uint32_t(KB * D / 8) ? c : 0u;
+            const uint32_t r = cc / (D / 8), dc = (cc % (D / 8)) * 8u, j = kb * KB + r;
+            const uint32_t jj = j < a.keys ? j : a.keys - 1u;
+            const bool old = jj < a.past;
+            const size_t kr = old ? size_t(jj) * a.kpj + kv * a.kph : size_t(jj - a.past) * a.knj + kv * a.knh;
+            rk[i] = *reinterpret_cast<const uint4*>((old ? a.k_past : a.k_new) + kr + dc);
+            if (values) {
+                const size_t vr = old ? size_t(jj) * a.vpj + kv * a.vph : size_t(jj - a.past) * a.vnj + kv * a.vnh;
+                rv[i] = *reinterpret_cast<const uint4*>((old ? a.v_past : a.v_new) + vr + dc);
+            }
+            valid |= uint32_t(c < uint32_t(KB * D / 8) && j < a.keys) << i;
+        }
+    };
+    // Registers -> LDS: K row-major, V transposed.
+    auto put = [&](bool values, const uint4 (&rk)[CHUNKS], const uint4 (&rv)[CHUNKS], uint32_t valid) {
+#pragma unroll
+        for (uint32_t i = 0; i < CHUNKS; ++i) {
+            const uint32_t c = tid + i * 256u;
+            if (c < uint32_t(KB * D / 8)) {
+                const uint32_t r = c / (D / 8), dc = (c % (D / 8)) * 8u;
+                const bool ok = (valid >> i) & 1u;
+                *reinterpret_cast<uint4*>(&k_s[r * KPAD + dc]) = ok ? rk[i] : uint4{0, 0, 0, 0};
+                if (values) {
+                    const uint4 v = ok ? rv[i] : uint4{0, 0, 0, 0};
+                    const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
+#pragma unroll
+                    for (int x = 0; x < 8; ++x) {
+                        v_s[(dc + x) * VPAD + r] = e[x];
+                    }
                 }
             }
         }
@@ -712,35 +757,87 @@ template <int D> __device__ __forceinline__ void attention_mfma_bf16(const Atten
         }
     };
 
+    // The key blocks this workgroup visits: from the live-block table, compacted into LDS by wave 0 with a
+    // ballot per 64 blocks (in key order); without a table (or past the list's capacity) every block, each
+    // checked against its mask values with a workgroup-wide vote.
     const uint32_t blocks = (a.keys + KB - 1) / KB;
-    const uint8_t* live_row = a.live_blocks ? a.live_blocks + size_t(blockIdx.x) * blocks : nullptr;
-    // Whether key block kb has any unmasked score in this workgroup (a uniform answer for every thread).
-    auto active = [&](uint32_t kb, float (&m)[8]) -> bool {
-        if (live_row) {
-            if (!live_row[kb]) {
-                return false;
+    const bool listed = a.live_blocks != nullptr && blocks <= kLiveListMax;
+    if (listed) {
+        if (wave == 0) {
+            const uint8_t* row = a.live_blocks + size_t(query_block) * blocks;
+            uint32_t n = 0;
+            for (uint32_t base = 0; base < blocks; base += 64u) {
+                const uint32_t kb = base + lane;
+                const uint8_t state = kb < blocks ? row[kb] : 0;
+                const unsigned long long bits = __ballot(state != 0);
+                if (state != 0) {
+                    live_list[n + uint32_t(__popcll(bits & ((1ull << lane) - 1ull)))] = uint16_t(kb | (state == 2 ? 0x8000u : 0u));
+                }
+                n += uint32_t(__popcll(bits));
             }
-            masks(kb, m);
-            __syncthreads();  // the previous block's LDS reads are done before the tile is restaged
-            return true;
+            if (lane == 0) {
+                live_total = n;
+            }
         }
-        return __syncthreads_or(masks(kb, m));
-    };
-    float peak = neg_inf, total = 0.0f;
-    for (uint32_t kb = 0; kb < blocks; ++kb) {
-        float m[8];
-        if (!active(kb, m)) {
-            continue;
-        }
-        stage(kb, false);
         __syncthreads();
+    }
+    const uint32_t visits = listed ? live_total : 0u;
+
+    // One pass over the visited blocks. A listed block's K (and V) chunks and mask values are fetched one
+    // block ahead, into registers, while the current block is scored; ``body`` gets the block's mask values.
+    auto sweep = [&](bool values, auto&& body) {
+        uint4 rk[CHUNKS], rv[CHUNKS];
+        uint32_t valid = 0;
+        if (listed) {
+            // separate loops for the two cases: a join of both inside one loop makes the compiler copy
+            // the prefetched registers at the join, which waits for the loads
+            // (the fetch after the last block re-reads that block, so no branch joins the prefetched registers)
+            // Blocks flagged all-zero read no mask words.
+            uint32_t raw[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (visits > 0) {
+                const uint32_t first = live_list[0];
+                fetch(first & 0x7fffu, values, rk, rv, valid);
+                if (!(first & 0x8000u)) {
+                    mask_fetch(first, raw);
+                }
+            }
+            for (uint32_t i = 0; i < visits; ++i) {
+                const uint32_t entry = live_list[i];
+                float m[8];
+                mask_values(entry & 0x7fffu, raw, m, (entry & 0x8000u) != 0);
+                __syncthreads();  // every wave is done reading the previous block's tiles
+                put(values, rk, rv, valid);
+                const uint32_t next = live_list[i + 1 < visits ? i + 1 : i];
+                fetch(next & 0x7fffu, values, rk, rv, valid);
+                if (!(next & 0x8000u)) {
+                    mask_fetch(next & 0x7fffu, raw);
+                }
+                __syncthreads();
+                body(m);
+            }
+        } else {
+            for (uint32_t kb = 0; kb < blocks; ++kb) {
+                float m[8];
+                if (!__syncthreads_or(masks(kb, m))) {
+                    continue;
+                }
+                fetch(kb, values, rk, rv, valid);
+                put(values, rk, rv, valid);
+                __syncthreads();
+                body(m);
+            }
+        }
+    };
+
+    float peak = neg_inf, total = 0.0f;
+    sweep(false, [&](const float (&m)[8]) {
         float s2[8];
         scores(m, s2);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             softmax_stats_add(peak, total, s2[i]);
         }
-    }
+    });
     // Combine the four lane groups that share a query, then fold in the sink.
 #pragma unroll
     for (int offset = 16; offset < 64; offset <<= 1) {
@@ -759,13 +856,7 @@ template <int D> __device__ __forceinline__ void attention_mfma_bf16(const Atten
     for (int dt = 0; dt < D / 16; ++dt) {
         o[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    for (uint32_t kb = 0; kb < blocks; ++kb) {
-        float m[8];
-        if (!active(kb, m)) {
-            continue;
-        }
-        stage(kb, true);
-        __syncthreads();
+    sweep(true, [&](const float (&m)[8]) {
         float s2[8];
         scores(m, s2);
         bf16x8_t pf;
@@ -781,7 +872,7 @@ template <int D> __device__ __forceinline__ void attention_mfma_bf16(const Atten
             const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, uint4{lo.x, lo.y, hi.x, hi.y});
             o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[dt], 0, 0, 0);
         }
-    }
+    });
     if (live) {
         uint16_t* dst = a.out + ((size_t(query) * a.kv_heads + kv) * a.group + g) * D;
 #pragma unroll

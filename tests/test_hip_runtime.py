@@ -711,7 +711,7 @@ class FreshAttention(torch.nn.Module):
     "tokens, past, kv_heads, group, dim, window",
     [(1, 257, 1, 8, 16, 40), (5, 3, 2, 4, 64, 40), (3, 700, 2, 2, 4, 40), (16, 0, 1, 1, 8, 40), (100, 60, 2, 4, 64, 40),
      (130, 0, 1, 2, 128, 40), (1, 4096, 8, 8, 64, 40), (2, 1500, 1, 8, 16, 40), (1, 1000, 2, 4, 32, None), (3, 2100, 1, 8, 64, 300),
-     (2, 300, 1, 4, 64, None)],
+     (2, 300, 1, 4, 64, None), (300, 2100, 1, 8, 64, 300)],
 )
 def test_fused_attention_matches_oracle(tmp_path, dtype, tokens, past, kv_heads, group, dim, window):
     """The fused attention against the oracle's unfused chain: causal and windowed masks, a query row whose
