@@ -55,7 +55,7 @@ STREAMING_BYTES = 64 << 20  # smaller operands and results may stay in L2 / the 
 FUSED_CONCAT_ELEMENTS = 1 << 16  # smaller concatenations are fused into their consumers
 DEFERRED_ELEMENTS = 1 << 16  # smaller expressions the front end asks to store stay fused instead...
 DEFERRED_SOURCES = 4  # ...when they read at most this many buffers (a residual stream is stored every few adds)
-CHEAP_EXPRESSION_COST = 6  # larger expressions stay fused too when one element costs at most this much
+CHEAP_EXPRESSION_COST = 8  # larger expressions stay fused too when one element costs at most this much
 MFMA_CUS = 256  # compute units of the target (MI355X), for the tile-round choice of the matrix-core products
 REUSED_EVALUATIONS = 1 << 18  # a contraction operand is stored when (elements x reuse) reaches this
 SMALL_REDUCTION = 8  # contractions summing at most this many products are fused expressions...
