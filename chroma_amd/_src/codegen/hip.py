@@ -56,6 +56,7 @@ FUSED_CONCAT_ELEMENTS = 1 << 16  # smaller concatenations are fused into their c
 DEFERRED_ELEMENTS = 1 << 16  # smaller expressions the front end asks to store stay fused instead...
 DEFERRED_SOURCES = 4  # ...when they read at most this many buffers (a residual stream is stored every few adds)
 CHEAP_EXPRESSION_COST = 8  # larger expressions stay fused too when one element costs at most this much
+WIDE_TOPK_LANE_VALUES = 32  # rows needing more values per lane take the two-stage top-k
 MFMA_CUS = 256  # compute units of the target (MI355X), for the tile-round choice of the matrix-core products
 REUSED_EVALUATIONS = 1 << 18  # a contraction operand is stored when (elements x reuse) reaches this
 SMALL_REDUCTION = 8  # contractions summing at most this many products are fused expressions...
@@ -577,6 +578,91 @@ class HIPCodegen(Codegen):
         inner_coords = k.unflatten(k.mod(row, inner), inner_shape) if inner_shape else []
         return [*outer_coords, along, *inner_coords]
 
+    topk_width_limit = 64 * 64 * 64  # rows up to this wide: the two-stage selection below
+
+    def _wide_topk(self, meta, x: Value, dim: int, largest: bool, values: Value, indices: Value) -> None:
+        """Top-k of rows too wide to hold in one wave's registers (a vocabulary row of logits). Stage 1: one
+        wave per chunk of 64 x P elements (at most 64 chunks per row) selects its chunk's k largest keys
+        in order into a scratch list. Stage 2: one wave per row, lane c holding the head of chunk c's list,
+        takes the wave-wide largest head k times. Keys order by value, then by lower index first
+        (``topk_key``), and are unique, so the result is the single-pass selection's bit for bit."""
+        shape = tuple(x.shape)
+        width, inner, outer = self._row_layout(shape, dim)
+        count = meta[0].shape[dim]
+        rows = outer * inner
+        per_lane = -(-width // (64 * 64))
+        if per_lane > 64:
+            raise NotImplementedError(f"topk over rows of {width} elements (at most {64 * 64 * 64})")
+        chunk = 64 * per_lane
+        chunks = -(-width // chunk)
+        keys = self.allocate((rows * chunks * count,), torch.int64)
+        vals = self.allocate((rows * chunks * count,), torch.float32)
+        groups = 4
+        k = Kernel(1)
+        key_slot = k.slot(keys.name, torch.int64, writable=True, extent=self.extents[keys.name])
+        val_slot = k.slot(vals.name, torch.float32, writable=True, extent=self.extents[vals.name])
+        k.line(f"const uint32_t w = blockIdx.x * {groups}u + threadIdx.x / 64u;")
+        k.line(f"if (w >= {rows * chunks}u) return;")
+        k.line(f"const uint32_t r = w / {chunks}u, c = w % {chunks}u;")
+        k.line("const uint32_t lane = threadIdx.x % 64u;")
+        k.line(f"uint64_t keys[{per_lane}];")
+        k.line(f"float vals[{per_lane}];")
+        row = Aff.of(Atom("r", rows - 1))
+        k.line("#pragma unroll")
+        with k.block(f"for (uint32_t p = 0; p < {per_lane}u; ++p) {{"):
+            k.line(f"const uint32_t j = c * {chunk}u + p * 64u + lane;")
+            k.line(f"if (j < {width}u) {{")
+            k.indent += 1
+            j = Aff.of(Atom("j", width - 1))
+            name = k.emit(self.read(k, x, self._row_coords(k, row, shape, dim, j)))
+            k.line(f"vals[p] = {name}; keys[p] = chroma::topk_key({name}, j, {str(bool(largest)).lower()});")
+            k.indent -= 1
+            k.line("} else { vals[p] = 0.0f; keys[p] = 0; }")
+        with k.block(f"for (uint32_t s = 0; s < {count}u; ++s) {{"):
+            k.line("uint64_t best = 0;")
+            k.line("#pragma unroll")
+            k.line(f"for (uint32_t p = 0; p < {per_lane}u; ++p) best = keys[p] > best ? keys[p] : best;")
+            k.line("const uint64_t top = chroma::wave_max_u64(best);")
+            k.line(f"const size_t at = (size_t(r) * {chunks}u + c) * {count}u + s;")
+            k.line("if (top == 0) { if (lane == 0) { " + key_slot + "[at] = 0; " + val_slot + "[at] = 0.0f; } continue; }")
+            k.line("const uint32_t winner = 0xffffffffu - uint32_t(top);")
+            k.line(f"if ((winner - c * {chunk}u) % 64u == lane) {{")
+            k.indent += 1
+            k.line("float chosen = 0.0f;")
+            k.line("#pragma unroll")
+            k.line(f"for (uint32_t p = 0; p < {per_lane}u; ++p) if (p == (winner - c * {chunk}u) / 64u) {{ chosen = vals[p]; keys[p] = 0; }}")
+            k.line(f"{key_slot}[at] = int64_t(top); {val_slot}[at] = chosen;")
+            k.indent -= 1
+            k.line("}")
+        self.launch(k, -(-(rows * chunks) // groups), 64 * groups, [x], kind="topk_chunks")
+
+        k = Kernel(1)
+        key_slot = k.slot(keys.name, torch.int64, extent=self.extents[keys.name])
+        val_slot = k.slot(vals.name, torch.float32, extent=self.extents[vals.name])
+        value_slot = k.slot(values.name, values.dtype, writable=True, extent=self.extents[values.name])
+        index_slot = k.slot(indices.name, indices.dtype, writable=True, extent=self.extents[indices.name])
+        k.line(f"const uint32_t r = blockIdx.x * {groups}u + threadIdx.x / 64u;")
+        k.line(f"if (r >= {rows}u) return;")
+        k.line("const uint32_t lane = threadIdx.x % 64u;")
+        k.line(f"const size_t base = (size_t(r) * {chunks}u + lane) * {count}u;")
+        k.line("uint32_t head = 0;")
+        k.line(f"uint64_t key = lane < {chunks}u ? uint64_t({key_slot}[base]) : 0;")
+        with k.block(f"for (uint32_t s = 0; s < {count}u; ++s) {{"):
+            k.line("const uint64_t top = chroma::wave_max_u64(key);")
+            k.line("if (top != 0 && key == top) {")
+            k.indent += 1
+            k.line(f"const float chosen = {val_slot}[base + head];")
+            s_atom = Aff.of(Atom("s", count - 1))
+            out_coords = self._row_coords(k, Aff.of(Atom("r", rows - 1)), tuple(meta[0].shape), dim, s_atom)
+            address = Kernel.flatten(out_coords, tuple(meta[0].shape))
+            k.store(value_slot, values.dtype, address, self._lane_values(k, ["chosen"]))
+            k.line(f"{index_slot}[{address.code()}] = int64_t(0xffffffffu - uint32_t(top));")
+            k.line("++head;")
+            k.line(f"key = head < {count}u ? uint64_t({key_slot}[base + head]) : 0;")
+            k.indent -= 1
+            k.line("}")
+        self.launch(k, -(-rows // groups), 64 * groups, [keys, vals], kind="topk_merge")
+
     def softmax(self, meta, x: Value, dim: int) -> Value:
         routed = self.router_weights.get(x.name)
         if routed is not None and dim == len(x.shape) - 1 and routed.dtype == meta.dtype:
@@ -1020,6 +1106,9 @@ class HIPCodegen(Codegen):
         count = meta[0].shape[dim]
         rows = outer * inner
         per_lane = -(-width // 64)
+        if per_lane > WIDE_TOPK_LANE_VALUES:
+            self._wide_topk(meta, x, dim, largest, values, indices)
+            return values, indices
         groups = 4
         k = Kernel(1)
         value_slot = k.slot(values.name, values.dtype, writable=True, extent=self.extents[values.name])

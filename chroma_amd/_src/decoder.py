@@ -22,15 +22,18 @@ from __future__ import annotations
 
 import contextlib
 import os
+import shutil
 import signal
+import tempfile
 import threading
 from dataclasses import dataclass
+from pathlib import Path
 from typing import Any, Iterator, List, Optional, Sequence, Tuple
 
 import numpy as np
 
 from chroma_amd._src import host
-from chroma_amd._src.dtypes import numpy_dtype
+from chroma_amd._src.dtypes import BFLOAT16, numpy_dtype
 from chroma_amd._src.program import NativeModel, Program
 
 
@@ -122,6 +125,41 @@ def _validate(prefill: Program, decode: Program) -> Tuple[dict, dict]:
     return cache, logits
 
 
+def _select_host(row: np.ndarray, k: int, ids: Optional[np.ndarray]) -> Tuple[np.ndarray, np.ndarray]:
+    """The top-k rule of ``Decoder.append_top`` on a downloaded logits row: NaN first, then values
+    descending, ties to the lower id (a stable sort)."""
+    candidates = row if ids is None else row[ids]
+    wide = candidates.astype(np.float32)
+    order = np.argsort(np.where(np.isnan(wide), -np.inf, -wide), kind="stable")[:k]
+    return candidates[order].copy(), (order if ids is None else ids[order]).astype(np.int64)
+
+
+class _TopK:
+    """Selection program of ``append_top``: top-k of the logits row."""
+
+    def __new__(cls, k: int):
+        import torch
+
+        class TopK(torch.nn.Module):
+            def forward(self, logits):
+                return torch.topk(logits, k, dim=-1)
+
+        return TopK()
+
+
+class _GatheredTopK:
+    """Selection program of ``append_top`` with ``allowed``: top-k among the gathered candidate ids."""
+
+    def __new__(cls, k: int):
+        import torch
+
+        class GatheredTopK(torch.nn.Module):
+            def forward(self, logits, ids):
+                return torch.topk(logits.reshape(-1)[ids].reshape(1, -1), k, dim=-1)
+
+        return GatheredTopK()
+
+
 class Decoder:
     def __init__(self, prefill: Program, decode: Program, *, sliding_window: int = 0) -> None:
         if sliding_window < 0:
@@ -151,7 +189,9 @@ class Decoder:
             for model in self._models
         ]
         self._row_bytes = int(np.prod(self._shape[2:])) * self._cache_dtype.itemsize
-        self._lock = threading.Lock()
+        self._selectors: dict = {}  # (k, gathered ids or None) -> top-k selection program (hip pairs)
+        self._selector_dir: Optional[str] = None
+        self._lock = threading.RLock()  # re-entered by append_top around its step and selection
         self._closed = False
         self._commit(self._empty())
 
@@ -221,6 +261,79 @@ class Decoder:
 
     def append(self, tokens: Any) -> np.ndarray:
         """Consume new token ids and return the logits [1, vocab] after the last one."""
+        logits, _ = self._consume(tokens, keep_logits=False)
+        return logits
+
+    def append_top(self, tokens: Any, k: int = 1, *, allowed: Any = None) -> Tuple[np.ndarray, np.ndarray]:
+        """Consume new token ids like ``append`` and return the ``k`` largest logits after the last one
+        with their token ids, largest first: NaN outranks every number and ties go to the lower id (the
+        reference GPU backend's top-k rule). ``allowed`` (token ids) restricts the choice to those ids.
+
+        With hip programs the logits never leave the device: a small selection program (the top-k kernel,
+        after a gather of the allowed ids) reads the step's logits by a device-to-device copy, and only
+        the ``k`` values and ids are downloaded instead of the vocabulary row. Other programs select on
+        the host by the same rule. (An addition to the reference API: its chat script samples from the
+        downloaded row, scripts/chat.py:82-98.)"""
+        if not isinstance(k, (int, np.integer)) or k < 1:
+            raise ValueError(f"k must be a positive integer, got {k!r}")
+        ids = None
+        if allowed is not None:
+            ids = np.unique(np.asarray(allowed))
+            if ids.ndim != 1 or not np.issubdtype(ids.dtype, np.integer):
+                raise TypeError("allowed must be a 1-D sequence of integer token ids")
+            if len(ids) and (ids[0] < 0 or ids[-1] >= self.vocab_size):
+                raise IndexError(f"allowed token ids must lie in [0, {self.vocab_size})")
+            ids = ids.astype(np.int64)
+        if k > (len(ids) if ids is not None else self.vocab_size):
+            raise ValueError(f"k = {k} exceeds the number of candidate tokens")
+        device = self._on_device and isinstance(self._models[1].native, NativeModel)
+        with self._lock:  # the step's device logits stay this step's until the selection has read them
+            logits, which = self._consume(tokens, keep_logits=device)
+            if not device:
+                return _select_host(logits[0], int(k), ids)
+            selector = self._selector(int(k), None if ids is None else len(ids))
+            native = selector.native
+            row = self.vocab_size * self._logit_dtype.itemsize
+            native.copy_2d(native.input_pointer(0), row, self._models[which].native.output_pointer(0), row, row, 1)
+            values = host.empty((1, int(k)), self._logit_dtype)
+            picks = host.empty((1, int(k)), np.int64)
+            if ids is None:
+                selector.run_resident([None], [values, picks])
+                return values[0].copy(), picks[0].copy()
+            selector.run_resident([None, ids], [values, picks])
+            return values[0].copy(), ids[picks[0]]
+
+    def greedy(self, tokens: Any, *, allowed: Any = None) -> int:
+        """Consume new token ids and return the id of the largest logit after the last one (``append_top``
+        with k = 1)."""
+        return int(self.append_top(tokens, 1, allowed=allowed)[1][0])
+
+    def _selector(self, k: int, candidates: Optional[int]) -> Program:
+        """The hip program selecting the top ``k`` of a logits row (of ``candidates`` gathered ids), compiled
+        on first use next to the decoder's programs and kept until ``close``."""
+        key = (k, candidates)
+        program = self._selectors.get(key)
+        if program is None:
+            import torch
+
+            from chroma_amd._src.compiler import compile_for_backend
+
+            dtype = torch.bfloat16 if self._logit_dtype == BFLOAT16 else getattr(torch, np.dtype(self._logit_dtype).name)
+            logits = torch.zeros(1, self.vocab_size, dtype=dtype)
+            if candidates is None:
+                example, module = (logits,), _TopK(k)
+            else:
+                example, module = (logits, torch.zeros(candidates, dtype=torch.int64)), _GatheredTopK(k)
+            if self._selector_dir is None:
+                self._selector_dir = tempfile.mkdtemp(prefix="chroma-select-")
+            target = Path(self._selector_dir) / f"top{k}-{candidates or 'all'}"
+            program = compile_for_backend(torch.export.export(module, example), target, backend="hip")
+            self._selectors[key] = program
+        return program
+
+    def _consume(self, tokens: Any, *, keep_logits: bool) -> Tuple[Optional[np.ndarray], int]:
+        """Run the steps for ``tokens``; return the last step's logits (None when ``keep_logits`` leaves
+        them in the device output of the program that ran it) and that program's index."""
         ids = np.asarray(tokens)
         if ids.ndim != 1 or not len(ids):
             raise ValueError(f"append wants a nonempty 1-D sequence of token IDs, got shape {ids.shape}")
@@ -232,6 +345,7 @@ class Decoder:
                 raise RuntimeError("Decoder is closed")
             offset = 0
             logits = None
+            which = 1
             while offset < len(ids):
                 remaining = len(ids) - offset
                 which = 1 if remaining == 1 else 0
@@ -257,7 +371,7 @@ class Decoder:
                     for mask, window in ((full_mask, self.context), (window_mask, self._window)):
                         _fill_mask(mask, causal & (key_times[None, :] > times[:, None] - window))
                 logit_index[0] = count - 1
-                logits = self._empty_array((1, self.vocab_size), self._logit_dtype)
+                logits = None if keep_logits else self._empty_array((1, self.vocab_size), self._logit_dtype)
                 rows = times[:count] % self.context
                 slots = state.slots.copy()
                 slots[rows] = times[:count]
@@ -274,12 +388,18 @@ class Decoder:
                     values[:, rows] = updates[1][:, :count]
                     self._commit(CacheState(keys, values, slots, state.position + count))
                 offset += count
-            return logits
+            return logits, which
 
     def close(self) -> None:
         with self._lock:
             for model in self._models:
                 model.close()
+            for program in self._selectors.values():
+                program.close()
+            self._selectors.clear()
+            if self._selector_dir is not None:
+                shutil.rmtree(self._selector_dir, ignore_errors=True)
+                self._selector_dir = None
             self._closed = True
             self._buffers.clear()
 

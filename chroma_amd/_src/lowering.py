@@ -275,7 +275,8 @@ def lower(codegen, target: Any, meta: Any, args: Tuple[Any, ...], kwargs: Dict[s
         x = args[0]
         dim = axis(_arg(args, kwargs, 2, "dim", -1), len(x.shape))
         width = x.shape[dim] if x.shape else 1
-        if x.dtype not in FLOAT_DTYPES or width > 4096:
+        # the reference's limit (lowering.py:262-264) unless the backend selects over wider rows
+        if x.dtype not in FLOAT_DTYPES or width > getattr(codegen, "topk_width_limit", 4096):
             raise NotImplementedError(f"topk axis {width}")
         largest = _arg(args, kwargs, 3, "largest", True)
         sort = _arg(args, kwargs, 4, "sorted", True)

@@ -291,3 +291,40 @@ def test_one_step_masks_match_the_general_rule():
                 _fill_mask(as_mask(general), causal & (key_times[None] > times[:, None] - window))
                 _fill_row(as_mask(fast), (slots >= 0) & (slots > position - window))
                 np.testing.assert_array_equal(general.view(np.uint8), fast.view(np.uint8))
+
+
+def test_top_k_selection_rule():
+    """``append_top``'s rule: NaN first, values descending, ties to the lower id; ``allowed`` restricts the
+    candidates and its ids come back, ties still to the lower id."""
+    from chroma_amd._src.decoder import _select_host
+
+    row = np.array([1.0, 3.0, np.nan, 3.0, -np.inf, 2.0, 3.0], dtype=np.float32)
+    values, ids = _select_host(row, 4, None)
+    np.testing.assert_array_equal(ids, [2, 1, 3, 6])
+    np.testing.assert_array_equal(values[1:], [3.0, 3.0, 3.0])
+    assert np.isnan(values[0])
+    values, ids = _select_host(row, 3, np.array([0, 4, 5, 6]))
+    np.testing.assert_array_equal(ids, [6, 5, 0])
+    np.testing.assert_array_equal(values, [3.0, 2.0, 1.0])
+
+
+def test_append_top_on_host_programs_matches_logits(oracle_pairs):
+    """Programs that are not hip programs select on the host: ``append_top`` / ``greedy`` agree with the
+    logits ``append`` returns for the same tokens, and bad arguments are rejected."""
+    from chroma_amd._src.decoder import _select_host
+
+    _, (prefill, decode), tokens, _ = oracle_pairs[8]
+    selecting, full = Decoder(prefill, decode, sliding_window=3), Decoder(prefill, decode, sliding_window=3)
+    values, ids = selecting.append_top(tokens[:3], 4)
+    want = _select_host(full.append(tokens[:3])[0], 4, None)
+    np.testing.assert_array_equal(ids, want[1])
+    np.testing.assert_array_equal(values, want[0])
+    assert selecting.greedy([int(tokens[3])]) == int(_select_host(full.append([int(tokens[3])])[0], 1, None)[1][0])
+    values, ids = selecting.append_top([int(tokens[4])], 2, allowed=[7, 3, 3, 20])
+    want = _select_host(full.append([int(tokens[4])])[0], 2, np.array([3, 7, 20]))
+    np.testing.assert_array_equal(ids, want[1])
+    for bad, error in (({"k": 0}, ValueError), ({"k": 4, "allowed": [1, 2]}, ValueError), ({"allowed": [31]}, IndexError)):
+        with pytest.raises(error):
+            selecting.append_top([1], **bad)
+    assert selecting.position == 5
+

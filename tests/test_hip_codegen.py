@@ -75,6 +75,21 @@ def test_dev_model_reuses_kernels_across_layers():
     assert len(shared) >= 2 and stats["unique_kernels"] == len(set(plan)) < stats["launches"] * 2 // 3
 
 
+def test_wide_topk_takes_two_stages():
+    """A top-k over a vocabulary-wide row cannot hold the row in one wave's registers: per-chunk selection,
+    then a merge of the chunk lists (two launches, scratch for the lists)."""
+    class TopK(torch.nn.Module):
+        def forward(self, x):
+            return torch.topk(x, 40, dim=-1)
+
+    generated = lower(TopK(), torch.randn(2, 201088))
+    source = generated.files["model.hip"]
+    assert "chroma_topk_chunks" in source and "chroma_topk_merge" in source
+    assert generated.stats["launches"] == 2
+    narrow = lower(TopK(), torch.randn(2, 2048)).files["model.hip"]
+    assert "chroma_topk_chunks" not in narrow
+
+
 def test_linear_kernel_selection():
     module = torch.nn.Linear(16, 7).eval()
     for blas, rows, kind in ((True, 3, "linear_stream"), (True, 40, "linear_mfma"), (False, 3, "linear_scalar")):

@@ -352,6 +352,34 @@ def test_topk_matches_oracle_exactly_without_ties(tmp_path, width):
     np.testing.assert_array_equal(values, expected_values)
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("largest", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_wide_topk_selects_like_the_reference_gpu_backend(tmp_path, dtype, largest):
+    """Rows wider than a wave's registers (a vocabulary row of logits) take the two-stage top-k. The
+    selection follows the reference GPU backend's rule (gpu.py:300-337): NaN outranks every number when
+    selecting the largest and loses otherwise, and ties go to the lowest index (a run of equal values,
+    and bfloat16's many repeats). Checked bit for bit against a stable sort."""
+    generator = torch.Generator().manual_seed(7)
+    x = torch.randn(3, 201088, generator=generator) * 4
+    x[0, 5] = float("nan")
+    x[1, 100000] = float("inf")
+    x[2, 7] = -float("inf")
+    x[1, 150000:150064] = 30.0  # runs of ties that the selection cuts through
+    x[1, 160000:160064] = -30.0
+    x = x.to(dtype)
+    module = Function(lambda x: torch.topk(x, 40, dim=-1, largest=largest))
+    with chroma_amd.compile(torch.export.export(module, (x,)), tmp_path / "hip") as model:
+        assert model.stats["launches"] == 2
+        values, indices = model(x)
+    wide = x.float().numpy()
+    key = np.where(np.isnan(wide), -np.inf, -wide) if largest else np.where(np.isnan(wide), np.inf, wide)
+    expected = np.argsort(key, axis=-1, kind="stable")[:, :40]
+    np.testing.assert_array_equal(indices, expected)
+    # values exact (NaN equal to NaN: a bfloat16 store writes the canonical NaN, as the reference's does)
+    np.testing.assert_array_equal(as_float(values), np.take_along_axis(wide, expected, axis=-1))
+
+
 def test_wave_reductions_norm_and_general_contractions(tmp_path):
     from chroma_amd.models.gpt_oss import RMSNorm
 
@@ -552,6 +580,36 @@ def test_dev_decoder_with_wraparound(tmp_path, dev_model):
             got, want = decoder.append(tokens[start:end]), reference.append(tokens[start:end])
             np.testing.assert_allclose(got, want, **F32)
         assert decoder.position == 48
+
+
+def test_dev_decoder_selects_on_device(tmp_path, dev_model):
+    """On-device selection over the dev model's 201,088 logits: ``append_top`` and ``greedy`` of a decoder of
+    hip programs (the logits stay on the device; a selection program copies them and returns k values and
+    ids) against the host rule applied to the logits a twin decoder downloads, with and without an allowed
+    set of ids."""
+    from chroma_amd._src.decoder import _select_host
+    from chroma_amd.models.cached import export_cached
+
+    context = 32
+    directories = [tmp_path / "prefill", tmp_path / "step"]
+    for graph, directory in zip((export_cached(dev_model, context, 8), export_cached(dev_model, context, 1)), directories):
+        chroma_amd.compile(graph, directory).close()
+    tokens = ((np.arange(16) * 7919 + 17) % 201088).astype(np.int64)
+    allowed = np.arange(5, 201088, 3)
+    with Decoder(*[Program(d) for d in directories]) as selecting, Decoder(*[Program(d) for d in directories]) as full:
+        values, ids = selecting.append_top(tokens[:8], 40)
+        want_values, want_ids = _select_host(full.append(tokens[:8])[0], 40, None)
+        np.testing.assert_array_equal(ids, want_ids)
+        np.testing.assert_array_equal(values, want_values)
+        for token in tokens[8:12]:
+            assert selecting.greedy([token]) == int(_select_host(full.append([token])[0], 1, None)[1][0])
+        for token in tokens[12:16]:
+            values, ids = selecting.append_top([token], 5, allowed=allowed)
+            want_values, want_ids = _select_host(full.append([token])[0], 5, allowed)
+            np.testing.assert_array_equal(ids, want_ids)
+            np.testing.assert_array_equal(values, want_values)
+            assert np.all(ids % 3 == 2)
+        assert selecting.position == full.position == 16
 
 
 def test_device_resident_execution(tmp_path):
