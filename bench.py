@@ -224,6 +224,19 @@ def bench_decode(work: Path, steps: int) -> dict:
             start = time.perf_counter()
             decoder.append(tokens[i : i + 1])
             samples.append((time.perf_counter() - start) * 1e3)
+        greedy = None
+        if name == "hip":
+            # the same steps through Decoder.greedy: the logits stay on the device and a selection program
+            # returns the chosen id (8 bytes down instead of the 804 KB row)
+            decoder.reset()
+            decoder.append(tokens[:8])
+            decoder.greedy(tokens[8:9])  # compiles the selection program
+            greedy = []
+            for i in range(9, 8 + count):
+                start = time.perf_counter()
+                decoder.greedy(tokens[i : i + 1])
+                greedy.append((time.perf_counter() - start) * 1e3)
+            decoder.close()
         padded = np.zeros(256, dtype=np.int64)
         padded[:16] = tokens[:16]
         last = np.array([15], dtype=np.int64)
@@ -233,6 +246,8 @@ def bench_decode(work: Path, steps: int) -> dict:
             "uncached_256": timed(lambda: full(padded, last), 2, 10 if name == "hip" else 3),
             "uncached_logits": full(padded, last),
         }
+        if greedy:
+            results[name]["decode_step_greedy"] = {"median_ms": round(statistics.median(greedy), 4), "steps": len(greedy)}
     np.testing.assert_allclose(results["hip"]["uncached_logits"], results["cpu_oracle"]["uncached_logits"], rtol=1e-4, atol=1e-5)
     for entry in results.values():
         entry.pop("uncached_logits")
