@@ -294,7 +294,9 @@ class Decoder:
             selector = self._selector(int(k), None if ids is None else len(ids))
             native = selector.native
             row = self.vocab_size * self._logit_dtype.itemsize
-            native.copy_2d(native.input_pointer(0), row, self._models[which].native.output_pointer(0), row, row, 1)
+            # queued on the selection program's stream, so its run comes after the copy without a wait here
+            # (the step's run has finished; the next step cannot start before this call returns)
+            native.copy_2d(native.input_pointer(0), row, self._models[which].native.output_pointer(0), row, row, 1, queued=True)
             values = host.empty((1, int(k)), self._logit_dtype)
             picks = host.empty((1, int(k)), np.int64)
             if ids is None:
