@@ -1699,7 +1699,9 @@ class HIPCodegen(Codegen):
         else:
             k.line("a.live_blocks = nullptr;")
         k.line(f"chroma::attention_mfma_bf16<{dim}>(a);")
-        k.min_waves = 5  # every key block's loads are a round trip; more resident workgroups hide them
+        # every key block's loads are a round trip and more resident workgroups hide them; five waves per
+        # SIMD fit without spills up to D = 64 (D = 128 would spill)
+        k.min_waves = 5 if dim <= 64 else 0
         operands = [entry[0] for entry in plan.values() if entry is not None] + ([live] if live is not None else [])
         self.launch(k, (-(-tokens // 64), kv_heads * group, 1), 256, operands, kind="attention_mfma")
         self.fused_attentions += 1
