@@ -57,6 +57,8 @@ DEFERRED_ELEMENTS = 1 << 16  # smaller expressions the front end asks to store s
 DEFERRED_SOURCES = 4  # ...when they read at most this many buffers (a residual stream is stored every few adds)
 CHEAP_EXPRESSION_COST = 8  # larger expressions stay fused too when one element costs at most this much
 WIDE_TOPK_LANE_VALUES = 32  # rows needing more values per lane take the two-stage top-k
+TRANSCENDENTAL_OPS = frozenset({"sin", "cos", "exp", "tanh", "sigmoid", "silu", "pow"})
+STORED_TABLE_ELEMENTS = 4096  # multi-consumer expressions with such ops and at least this many elements are stored
 MFMA_CUS = 256  # compute units of the target (MI355X), for the tile-round choice of the matrix-core products
 REUSED_EVALUATIONS = 1 << 18  # a contraction operand is stored when (elements x reuse) reaches this
 SMALL_REDUCTION = 8  # contractions summing at most this many products are fused expressions...
@@ -123,6 +125,7 @@ class HIPCodegen(Codegen):
         self.blas = blas
         self.closures: Dict[str, Closure] = {}
         self.costs: Dict[str, int] = {}
+        self.transcendental: Set[str] = set()  # expressions containing a libm call
         self.sources: Dict[str, frozenset] = {}
         self.bindings: Dict[str, Binding] = {}
         self.dtypes: Dict[str, torch.dtype] = {}
@@ -181,11 +184,14 @@ class HIPCodegen(Codegen):
         return Value(name, shape, meta.dtype, root.deps, stored=True, view=View(root, contiguous_strides(shape), offset))
 
     # ================================================================================= expressions
-    def expr(self, meta: torch.Tensor, closure: Closure, inputs: Sequence[Value], cost: Optional[int] = None) -> Value:
+    def expr(self, meta: torch.Tensor, closure: Closure, inputs: Sequence[Value], cost: Optional[int] = None,
+             transcendental: bool = False) -> Value:
         name = f"e{next(self.counter)}"
         self.closures[name] = closure
         # rough count of the loads and operations one element costs (stored inputs count one load)
         self.costs[name] = cost if cost is not None else 1 + sum(self.cost(v) for v in inputs)
+        if transcendental or any(v.name in self.transcendental for v in inputs if not v.stored):
+            self.transcendental.add(name)
         self.sources[name] = frozenset().union(*(self.sources[v.name] for v in inputs)) if inputs else frozenset()
         pending = frozenset().union(*(self.pending_of.get(v.name, frozenset()) for v in inputs)) if inputs else frozenset()
         if pending:
@@ -252,6 +258,10 @@ class HIPCodegen(Codegen):
             return Value(value.name, value.shape, value.dtype, value.deps, stored=True, view=value.view)
         if value.name in self.pending_norms:
             return value  # consumers that stage their rows fold it; any other reader stores it
+        if value.name in self.transcendental and STORED_TABLE_ELEMENTS <= math.prod(value.shape) <= DEFERRED_ELEMENTS:
+            # a table of libm calls (the rotary cos/sin at a long prefill) that several consumers read,
+            # typically broadcast over heads: computed once instead of once per consumer element
+            return self.store(value)
         if math.prod(value.shape) <= DEFERRED_ELEMENTS and len(self.sources[value.name]) <= DEFERRED_SOURCES:
             return value
         if math.prod(value.shape) > DEFERRED_ELEMENTS and value.name in self.closures and self.cost(value) <= CHEAP_EXPRESSION_COST:
@@ -368,7 +378,7 @@ class HIPCodegen(Codegen):
                 node = ("un", UNARY_OPS[op], a)
             return rounded(node)
 
-        return self.expr(meta, closure, [v for v in args if isinstance(v, Value)])
+        return self.expr(meta, closure, [v for v in args if isinstance(v, Value)], transcendental=op in TRANSCENDENTAL_OPS)
 
     def gather(self, meta, x: Value, indices: Value, negative: bool) -> Value:
         index_rank = len(indices.shape)
