@@ -317,10 +317,13 @@ def bench_c5(work: Path, steps: int) -> dict:
     del model
     tokens = torch.randint(0, 201088, (C5_PREFILL + steps,), generator=torch.Generator().manual_seed(2)).numpy()
     result = {"workload": "GPT-OSS-20B-shaped bf16 MoE (24 layers, hidden 2880, 64/8 heads of 64, 32 experts top-4, vocab 201088), "
-              "weights N(0,0.02) seed 2; 2048-token prefill then decode, cache 4096 positions",
+              "weights N(0,0.02) seed 2; 2048-token prefill (timed after one untimed prefill and a reset) then decode, cache 4096 positions",
               "weight_bytes": programs["prefill"].stats["weight_bytes"]}
     flops = c5_flops(gpt_oss_20b, C5_PREFILL, C5_CONTEXT)
     with Decoder(programs["prefill"], programs["decode"], sliding_window=gpt_oss_20b.sliding_window) as decoder:
+        # one untimed prefill first: the host staging's first touch and the decoder's mask-band cache
+        decoder.append(tokens[:C5_PREFILL])
+        decoder.reset()
         start = time.perf_counter()
         logits = decoder.append(tokens[:C5_PREFILL])
         result["prefill_decoder_ms"] = round((time.perf_counter() - start) * 1e3, 3)

@@ -21,6 +21,7 @@ either before the commit (state and device cache untouched) or after it.
 from __future__ import annotations
 
 import contextlib
+import functools
 import os
 import shutil
 import signal
@@ -107,6 +108,47 @@ def _fill_mask(mask: np.ndarray, allowed: np.ndarray) -> None:
         bits = mask.view(np.uint16)
         bits.fill(0xFF80)
         bits[allowed] = 0
+
+
+@functools.lru_cache(maxsize=8)
+def _band(steps: int, window: int, bits: str) -> np.ndarray:
+    """Mask bits over the new keys of a multi-step call: key c (time position + c) is blocked for query t
+    when c > t or c <= t - window, whatever the position. Read-only, shared by every call of this shape."""
+    c = np.arange(steps)
+    blocked = (c[None, :] > c[:, None]) | (c[None, :] <= c[:, None] - window)
+    dtype = np.dtype(bits)
+    out = np.multiply(blocked, dtype.type(0xFF800000 if dtype.itemsize == 4 else 0xFF80), dtype=dtype)
+    out.setflags(write=False)
+    return out
+
+
+def _fill_masks(masks: Sequence[Tuple[np.ndarray, int]], key_times: np.ndarray, valid: np.ndarray, times: np.ndarray) -> None:
+    """Multi-step masks [steps, keys], one per (mask, window): 0 where key j is valid, not after query t
+    (key_times[j] <= times[t]) and inside the window (key_times[j] > times[t] - window), -inf elsewhere.
+    The keys are the cached ones followed by the new ones, whose times are ``times`` (always valid): that
+    block is a band fixed by (steps, window) and copied from a cache. Cached keys are all blocked when none
+    is valid (a fresh prefill); otherwise invalid keys take the largest time, so "after the query" covers
+    them, and the block is the blocked indicator times the -inf bit pattern (two comparisons and a
+    multiply, no boolean index assignment)."""
+    steps = len(times)
+    past = len(key_times) - steps
+    valid_past = valid[:past]
+    any_valid = bool(valid_past.any())
+    if any_valid:
+        kt = np.where(valid_past, key_times[:past], np.iinfo(np.int64).max)
+        late = kt[None, :] > times[:, None]
+        blocked = np.empty_like(late)
+    for mask, window in masks:
+        bits = np.uint32 if mask.dtype == np.float32 else np.uint16
+        view = mask.view(bits)
+        neg = bits(0xFF800000 if bits is np.uint32 else 0xFF80)
+        if any_valid:
+            np.less_equal(kt[None, :], (times - window)[:, None], out=blocked)
+            np.logical_or(blocked, late, out=blocked)
+            np.multiply(blocked, neg, out=view[:, :past])
+        else:
+            view[:, :past] = neg
+        view[:, past:] = _band(steps, window, np.dtype(bits).str)
 
 
 def _validate(prefill: Program, decode: Program) -> Tuple[dict, dict]:
@@ -367,11 +409,8 @@ class Decoder:
                     for mask, window in ((full_mask, self.context), (window_mask, self._window)):
                         _fill_row(mask, valid & (state.slots > state.position - window))
                 else:
-                    key_times = np.concatenate((state.slots, times))
-                    valid = np.concatenate((state.slots >= 0, np.ones(steps, dtype=bool)))
-                    causal = valid[None, :] & (key_times[None, :] <= times[:, None])
-                    for mask, window in ((full_mask, self.context), (window_mask, self._window)):
-                        _fill_mask(mask, causal & (key_times[None, :] > times[:, None] - window))
+                    _fill_masks(((full_mask, self.context), (window_mask, self._window)), np.concatenate((state.slots, times)),
+                                np.concatenate((state.slots >= 0, np.ones(steps, dtype=bool))), times)
                 logit_index[0] = count - 1
                 logits = None if keep_logits else self._empty_array((1, self.vocab_size), self._logit_dtype)
                 rows = times[:count] % self.context

@@ -328,3 +328,29 @@ def test_append_top_on_host_programs_matches_logits(oracle_pairs):
             selecting.append_top([1], **bad)
     assert selecting.position == 5
 
+
+def test_multi_step_masks_match_the_general_rule():
+    """The multi-step mask writer (blocked indicator times the -inf bits) equals the general rule
+    (valid, causal, inside the window -> 0; else -inf) in float32 and bfloat16, over random cache states
+    with invalid, old, wrapped and new keys."""
+    from chroma_amd._src.decoder import _fill_mask, _fill_masks
+
+    rng = np.random.default_rng(3)
+    for trial in range(40):
+        context, steps = int(rng.integers(2, 12)), int(rng.integers(1, 9))
+        position = int(rng.integers(0, 30))
+        slots = np.where(rng.random(context) < 0.3, -1, rng.integers(0, max(position, 1), context)).astype(np.int64)
+        times = position + np.arange(steps, dtype=np.int64)
+        key_times = np.concatenate((slots, times))
+        valid = np.concatenate((slots >= 0, np.ones(steps, dtype=bool)))
+        causal = valid[None] & (key_times[None] <= times[:, None])
+        for dtype in (np.float32, np.uint16):
+            as_mask = (lambda m: m) if dtype == np.float32 else (lambda m: m.view(BFLOAT16))
+            windows = (context, int(rng.integers(1, context + 1)))
+            fast = [np.empty((steps, context + steps), dtype) for _ in windows]
+            _fill_masks([(as_mask(m), w) for m, w in zip(fast, windows)], key_times, valid, times)
+            for mask, window in zip(fast, windows):
+                general = np.empty_like(mask)
+                _fill_mask(as_mask(general), causal & (key_times[None] > times[:, None] - window))
+                np.testing.assert_array_equal(general.view(np.uint8), mask.view(np.uint8))
+
