@@ -1452,11 +1452,15 @@ class HIPCodegen(Codegen):
         per_lane = chunks // lanes
         if per_lane > 16:
             return False
+        # W split over grid.z parts of about 16 KiB each (one workgroup streams only ~15 GB/s), as far as
+        # every part keeps rows at this lane layout; each part recomputes the (few-key) attention row
+        rows_per_step = 64 // lanes  # rows of W one wave covers per step
+        parts = max(1, min(-(-columns * inner * ITEMSIZE[x.dtype] // (16 << 10)), -(-columns // (rows_per_step * group)), 8))
         # rows of W per wave step: enough to cover W in one step, at most 16 chunks per lane held
-        steps = max(1, min(16 // per_lane, -(-columns // (64 // lanes * group))))
+        steps = max(1, min(16 // per_lane, -(-columns // (rows_per_step * group * parts))))
         self._retract_last_launch()
         k = self._waves_attention(*operands, epilogue=(weight, bias, out, lanes, steps))
-        self.launch(k, (tokens, 1, 1), 64 * group, inputs + [weight] + ([bias] if bias is not None else []), kind="attention_linear")
+        self.launch(k, (tokens, 1, parts), 64 * group, inputs + [weight] + ([bias] if bias is not None else []), kind="attention_linear")
         self.retractable_attention.pop(x.root.name, None)
         self.attention_epilogues += 1
         return True

@@ -297,8 +297,11 @@ __device__ __forceinline__ void stream_linear(const T* __restrict__ x, const flo
 // The same product by one workgroup alone (its waves split the rows of W), as the epilogue of a kernel
 // that has just produced X in LDS; ``stream_block_fetch`` requests each wave's first step early.
 template <int K, int LPR, int ROWS, class T>
+// The waves of the grid.z parts of one workgroup position share W's rows: wave w of part p is wave
+// p * (waves per workgroup) + w of gridDim.z * (waves per workgroup).
 __device__ __forceinline__ void stream_block_fetch(StreamStep<K, LPR, ROWS, T>& first, const T* __restrict__ w, uint32_t n) {
-    const uint32_t base = threadIdx.x / kWave * StreamStep<K, LPR, ROWS, T>::G * ROWS;
+    const uint32_t wave = blockIdx.z * (blockDim.x / kWave) + threadIdx.x / kWave;
+    const uint32_t base = wave * StreamStep<K, LPR, ROWS, T>::G * ROWS;
     if (base < n) {
         first.fetch(w, base, n);
     }
@@ -307,7 +310,9 @@ __device__ __forceinline__ void stream_block_fetch(StreamStep<K, LPR, ROWS, T>& 
 template <int M, int K, int LPR, int ROWS, bool STAGED, class T>
 __device__ __forceinline__ void stream_block_linear(const T* __restrict__ x, const float* xs, const T* __restrict__ w, const T* __restrict__ bias,
                                                     T* __restrict__ out, uint32_t n, StreamStep<K, LPR, ROWS, T>& first) {
-    stream_rows<M, K, LPR, ROWS, STAGED, true, T>(x, xs, w, bias, out, n, n, threadIdx.x / kWave, blockDim.x / kWave, &first);
+    const uint32_t per_block = blockDim.x / kWave;
+    stream_rows<M, K, LPR, ROWS, STAGED, true, T>(x, xs, w, bias, out, n, n, blockIdx.z * per_block + threadIdx.x / kWave,
+                                                  gridDim.z * per_block, &first);
 }
 
 // Selected-expert products through ``stream_rows``: out[slot, :] = W[expert(slot)] . x[token or slot]^T,
