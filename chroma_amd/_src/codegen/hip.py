@@ -674,6 +674,10 @@ class HIPCodegen(Codegen):
         self.launch(k, -(-rows // groups), 64 * groups, [keys, vals], kind="topk_merge")
 
     def softmax(self, meta, x: Value, dim: int) -> Value:
+        """Row softmax (gpu.py:275-298). The statistics are float, as in the reference; the quotient is
+        exp(x - max) times the float reciprocal of the row's sum, one multiply per element instead of a
+        division (a correctly rounded division costs about ten VALU operations, which would make the C2
+        chain compute-bound), which keeps every result within one ulp of the correctly rounded quotient."""
         routed = self.router_weights.get(x.name)
         if routed is not None and dim == len(x.shape) - 1 and routed.dtype == meta.dtype:
             return routed

@@ -172,7 +172,10 @@ def _select_host(row: np.ndarray, k: int, ids: Optional[np.ndarray]) -> Tuple[np
     descending, ties to the lower id (a stable sort)."""
     candidates = row if ids is None else row[ids]
     wide = candidates.astype(np.float32)
-    order = np.argsort(np.where(np.isnan(wide), -np.inf, -wide), kind="stable")[:k]
+    nan = np.isnan(wide)
+    # lexsort is stable and sorts by its last key first: NaN before any number (+inf included), then
+    # larger values first, ties in id order.
+    order = np.lexsort((np.where(nan, 0, -wide), ~nan))[:k]
     return candidates[order].copy(), (order if ids is None else ids[order]).astype(np.int64)
 
 

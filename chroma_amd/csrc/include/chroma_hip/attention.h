@@ -9,7 +9,9 @@
 // storing the [heads, queries, keys] scores. Every rounding point of the chain is kept: the scores, the
 // scaled scores and the masked scores are rounded to the storage type, the softmax statistics are float,
 // each probability is exp(x - max) / sum rounded to the storage type before it meets V, and the output
-// sum is float. Only the order of the float sums differs from the reference.
+// sum is float. Two things differ from the reference: the order of the float sums, and, in the
+// matrix-core kernel only, the quotient, which is exp(x - max) times the float reciprocal of the sum
+// (within one ulp of the correctly rounded quotient before the rounding to the storage type).
 #pragma once
 
 #include "device.h"

@@ -152,6 +152,9 @@ Plan read_plan(const std::string& path) {
             throw std::runtime_error("Unknown launch plan entry: " + key);
         }
     }
+    // Every region the runtime copies to or from, and every kernel argument, must lie inside the one
+    // allocation, so a stale or edited plan cannot make a copy or a launch reach outside it.
+    auto inside = [&](size_t offset, size_t bytes) { return offset <= plan.arena && bytes <= plan.arena - offset; };
     for (const auto& launch : plan.launches) {
         for (size_t offset : launch.offsets) {
             if (offset >= plan.arena) {
@@ -159,48 +162,91 @@ Plan read_plan(const std::string& path) {
             }
         }
     }
+    for (const auto* list : {&plan.inputs, &plan.outputs}) {
+        for (const auto& region : *list) {
+            if (!inside(region.offset, region.bytes)) {
+                throw std::runtime_error("Launch plan input or output region outside the program allocation");
+            }
+        }
+    }
+    if (!inside(plan.error, sizeof(unsigned)) || !inside(0, plan.weight_bytes)) {
+        throw std::runtime_error("Launch plan error word or weights outside the program allocation");
+    }
     return plan;
+}
+
+// Byte size of a file, or -1 when it cannot be opened.
+long file_size(const std::string& path) {
+    std::FILE* file = std::fopen(path.c_str(), "rb");
+    if (!file) {
+        return -1;
+    }
+    long size = -1;
+    if (std::fseek(file, 0, SEEK_END) == 0) {
+        size = std::ftell(file);
+    }
+    std::fclose(file);
+    return size;
 }
 
 class Program {
 public:
     Program(const std::string& directory) {
         plan_ = read_plan(directory + "/model.plan");
+        // Checked before anything is allocated: a wrong weights file is the common load failure.
+        const long weights = file_size(directory + "/" + plan_.weights_file);
+        if (weights < 0 || static_cast<size_t>(weights) != plan_.weight_bytes) {
+            throw std::runtime_error("Missing weights file or incorrect byte size");
+        }
         check(hipGetDevice(&device_), "hipGetDevice");
-        hipDeviceProp_t properties{};
-        check(hipGetDeviceProperties(&properties, device_), "hipGetDeviceProperties");
-        name_ = std::string(properties.name) + " (" + properties.gcnArchName + ")";
-        check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreateWithFlags");
-        check(hipEventCreate(&start_), "hipEventCreate");
-        check(hipEventCreate(&stop_), "hipEventCreate");
-        check(hipHostMalloc(reinterpret_cast<void**>(&error_host_), sizeof(unsigned), hipHostMallocDefault), "hipHostMalloc");
-        check(hipMalloc(&base_, plan_.arena ? plan_.arena : 1), "hipMalloc program allocation");
-        check(hipMemset(static_cast<char*>(base_) + plan_.error, 0, sizeof(unsigned)), "Clear index error");
-        upload_weights(directory + "/" + plan_.weights_file);
-        check(hipModuleLoad(&module_, (directory + "/" + plan_.code_object).c_str()), "hipModuleLoad");
-        std::map<std::string, hipFunction_t> functions;
-        for (auto& launch : plan_.launches) {
-            auto found = functions.find(launch.kernel);
-            if (found == functions.end()) {
-                hipFunction_t function = nullptr;
-                check(hipModuleGetFunction(&function, module_, launch.kernel.c_str()), "hipModuleGetFunction");
-                found = functions.emplace(launch.kernel, function).first;
+        try {
+            hipDeviceProp_t properties{};
+            check(hipGetDeviceProperties(&properties, device_), "hipGetDeviceProperties");
+            name_ = std::string(properties.name) + " (" + properties.gcnArchName + ")";
+            check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+            check(hipEventCreate(&start_), "hipEventCreate");
+            check(hipEventCreate(&stop_), "hipEventCreate");
+            check(hipHostMalloc(reinterpret_cast<void**>(&error_host_), sizeof(unsigned), hipHostMallocDefault), "hipHostMalloc");
+            check(hipMalloc(&base_, plan_.arena ? plan_.arena : 1), "hipMalloc program allocation");
+            check(hipMemset(static_cast<char*>(base_) + plan_.error, 0, sizeof(unsigned)), "Clear index error");
+            upload_weights(directory + "/" + plan_.weights_file);
+            check(hipModuleLoad(&module_, (directory + "/" + plan_.code_object).c_str()), "hipModuleLoad");
+            std::map<std::string, hipFunction_t> functions;
+            for (auto& launch : plan_.launches) {
+                auto found = functions.find(launch.kernel);
+                if (found == functions.end()) {
+                    hipFunction_t function = nullptr;
+                    check(hipModuleGetFunction(&function, module_, launch.kernel.c_str()), "hipModuleGetFunction");
+                    found = functions.emplace(launch.kernel, function).first;
+                }
+                launch.function = found->second;
+                launch.pointers.resize(launch.offsets.size());
+                launch.arguments.resize(launch.offsets.size());
+                for (size_t i = 0; i < launch.offsets.size(); ++i) {
+                    launch.pointers[i] = static_cast<char*>(base_) + launch.offsets[i];
+                    launch.arguments[i] = &launch.pointers[i];
+                }
             }
-            launch.function = found->second;
-            launch.pointers.resize(launch.offsets.size());
-            launch.arguments.resize(launch.offsets.size());
-            for (size_t i = 0; i < launch.offsets.size(); ++i) {
-                launch.pointers[i] = static_cast<char*>(base_) + launch.offsets[i];
-                launch.arguments[i] = &launch.pointers[i];
-            }
+        } catch (...) {
+            release();  // a constructor that throws runs no destructor
+            throw;
         }
         // The whole plan replays as one captured hipGraph unless CHROMA_HIP_GRAPH=0.
         const char* graph = std::getenv("CHROMA_HIP_GRAPH");
         use_graph_ = graph == nullptr || std::strcmp(graph, "0") != 0;
     }
 
-    ~Program() {
-        DeviceGuard guard(device_);
+    ~Program() { release(); }
+
+    // Frees whatever exists so far (every handle starts null) after the stream has drained. Never throws:
+    // it runs from the destructor and from a failed constructor.
+    void release() noexcept {
+        if (device_ < 0) {
+            return;
+        }
+        int previous = device_;
+        hipGetDevice(&previous);
+        hipSetDevice(device_);
         if (stream_) {
             hipStreamSynchronize(stream_);
         }
@@ -226,6 +272,8 @@ public:
             if (staged_[slot]) {
                 hipEventDestroy(staged_[slot]);
             }
+            staging_[slot] = nullptr;
+            staged_[slot] = nullptr;
         }
         if (start_) {
             hipEventDestroy(start_);
@@ -236,6 +284,17 @@ public:
         if (stream_) {
             hipStreamDestroy(stream_);
         }
+        graph_exec_ = nullptr;
+        graph_ = nullptr;
+        module_ = nullptr;
+        base_ = nullptr;
+        error_host_ = nullptr;
+        start_ = stop_ = nullptr;
+        stream_ = nullptr;
+        if (previous != device_) {
+            hipSetDevice(previous);
+        }
+        device_ = -1;
     }
 
     const std::string& name() const { return name_; }

@@ -306,6 +306,11 @@ def test_top_k_selection_rule():
     values, ids = _select_host(row, 3, np.array([0, 4, 5, 6]))
     np.testing.assert_array_equal(ids, [6, 5, 0])
     np.testing.assert_array_equal(values, [3.0, 2.0, 1.0])
+    # NaN outranks +inf even when the +inf has the lower id; NaNs among themselves go by id
+    row = np.array([np.inf, 1.0, np.nan, np.inf, np.nan], dtype=np.float32)
+    values, ids = _select_host(row, 5, None)
+    np.testing.assert_array_equal(ids, [2, 4, 0, 3, 1])
+    np.testing.assert_array_equal(values[2:], [np.inf, np.inf, 1.0])
 
 
 def test_append_top_on_host_programs_matches_logits(oracle_pairs):

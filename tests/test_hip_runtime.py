@@ -804,3 +804,45 @@ def test_fused_attention_matches_oracle(tmp_path, dtype, tokens, past, kv_heads,
         got = model(*inputs)
     want = compile_cpu(exported, tmp_path / "cpu")(*[numpy_of(v) for v in inputs])
     compare(got, want)
+
+
+class PerHeadAttention(torch.nn.Module):
+    """Attention whose mask differs per query head ([kv, group, queries, keys])."""
+
+    def forward(self, q, k, v, mask, sinks):
+        tokens, kv_heads, group, dim = q.shape
+        k = k[:, :, None, :].expand(-1, -1, group, -1)
+        v = v[:, :, None, :].expand(-1, -1, group, -1)
+        scores = torch.einsum("qhmd,khmd->hmqk", q, k) * (1 / math.sqrt(dim)) + mask
+        s = sinks.reshape(kv_heads, group, 1, 1).expand(-1, -1, tokens, -1)
+        weights = torch.softmax(torch.cat([scores, s], dim=-1), dim=-1)[..., :-1]
+        return torch.einsum("hmqk,khmd->qhmd", weights, v)
+
+
+@pytest.mark.parametrize("tokens, kv_heads, group, dim", [(96, 2, 4, 64), (160, 1, 2, 64)])
+def test_fused_attention_per_head_mask(tmp_path, tokens, kv_heads, group, dim):
+    """A mask that differs per query head (causal with a different window per head, one head with a fully
+    masked query row) takes the matrix-core kernel's path without a live-block table, which votes on each
+    key block in the workgroup; checked against the oracle's unfused chain in bfloat16."""
+    generator = torch.Generator().manual_seed(tokens + 7 * group)
+    dtype = torch.bfloat16
+
+    def rand(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=generator) * scale).to(dtype)
+
+    mask = torch.zeros(kv_heads, group, tokens, tokens)
+    for h in range(kv_heads):
+        for m in range(group):
+            window = 8 + 24 * (h * group + m)
+            for t in range(tokens):
+                mask[h, m, t, t + 1 :] = -math.inf
+                mask[h, m, t, : max(0, t - window)] = -math.inf
+    mask[0, group - 1, 5, :] = -math.inf
+    inputs = (rand(tokens, kv_heads, group, dim), rand(tokens, kv_heads, dim), rand(tokens, kv_heads, dim), mask.to(dtype),
+              rand(kv_heads * group, scale=2.0))
+    exported = torch.export.export(PerHeadAttention(), inputs)
+    with chroma_amd.compile(exported, tmp_path / "hip") as model:
+        assert model.stats["fused_attentions"] == 1 and model.stats["mfma_matmuls"] == 1
+        got = model(*inputs)
+    want = compile_cpu(exported, tmp_path / "cpu")(*[numpy_of(v) for v in inputs])
+    compare(got, want)

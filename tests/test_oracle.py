@@ -217,3 +217,27 @@ def test_dev_model_matches_eager(tmp_path):
         program(np.full(8, 201088, dtype=np.int64))
     with pytest.raises(IndexError):
         program(np.full(8, -1, dtype=np.int64))
+
+
+@pytest.mark.parametrize("name", ["tanh", "silu"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_extension_unaries_match_eager(tmp_path, name, dtype):
+    """The two operators the oracle adds to the reference's table (``aten.tanh``: ``std::tanh``;
+    ``aten.silu``: ``x * (1 / (1 + exp(-x)))``, the reference's sigmoid form times x) against eager torch:
+    +-inf, NaN, signed zeros, |x| < 0.05 (where tanh is x to first order), |x| > 20 (saturation, and
+    exp(-x) overflowing for silu), the float extremes and a normal sample. fp32 within 2 ulp; bfloat16,
+    whose inputs and outputs both round, within one bfloat16 ulp."""
+    special = [np.inf, -np.inf, np.nan, 0.0, -0.0, 1e-8, -3e-4, 0.049, -0.0499, 0.051, 20.5, -20.5, 45.0, -88.0, -104.0,
+               3.0e38, -3.0e38, 1e-38, 0.5, -1.0]
+    x = torch.cat([torch.tensor(special), torch.randn(200, generator=torch.Generator().manual_seed(3)) * 6]).to(dtype)
+    fn = getattr(torch, name) if name == "tanh" else torch.nn.functional.silu
+    _, out = run(tmp_path, Function(fn), x)
+    got = as_float(out)
+    want = fn(x).float().numpy()
+    assert np.array_equal(np.isnan(got), np.isnan(want)), name
+    finite = np.isfinite(want)
+    np.testing.assert_array_equal(got[~finite & ~np.isnan(want)], want[~finite & ~np.isnan(want)])
+    rtol = 2.4e-7 if dtype == torch.float32 else 7.9e-3
+    np.testing.assert_allclose(got[finite], want[finite], rtol=rtol, atol=1e-37)
+    # sign of zero and of tiny results is kept
+    np.testing.assert_array_equal(np.signbit(got[finite & (want == 0)]), np.signbit(want[finite & (want == 0)]))
