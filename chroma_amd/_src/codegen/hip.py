@@ -50,6 +50,9 @@ SPLIT_MAP_ROWS = 1024
 # same kernel reads again are written with non-temporal (streaming) stores.
 ROW_THREADS = 256
 ROW_RESIDENT = 32
+ROW_UNROLL = 4  # vector loads per thread in flight in the one-pass row statistics
+SPLIT_ROW_LIMIT = 256  # rows of a reduction below this count are split over workgroups when wide
+SPLIT_ROW_BLOCKS = 1024  # workgroups a split row reduction aims for
 STREAMING_STORES = True
 STREAMING_BYTES = 64 << 20  # smaller operands and results may stay in L2 / the last-level cache
 FUSED_CONCAT_ELEMENTS = 1 << 16  # smaller concatenations are fused into their consumers
@@ -57,7 +60,7 @@ DEFERRED_ELEMENTS = 1 << 16  # smaller expressions the front end asks to store s
 DEFERRED_SOURCES = 4  # ...when they read at most this many buffers (a residual stream is stored every few adds)
 CHEAP_EXPRESSION_COST = 8  # larger expressions stay fused too when one element costs at most this much
 WIDE_TOPK_LANE_VALUES = 32  # rows needing more values per lane take the two-stage top-k
-TRANSCENDENTAL_OPS = frozenset({"sin", "cos", "exp", "tanh", "sigmoid", "silu", "pow"})
+TRANSCENDENTAL_OPS = frozenset({"sin", "cos", "exp", "tanh", "sigmoid", "silu", "pow", "log"})
 STORED_TABLE_ELEMENTS = 4096  # multi-consumer expressions with such ops and at least this many elements are stored
 MFMA_CUS = 256  # compute units of the target (MI355X), for the tile-round choice of the matrix-core products
 REUSED_EVALUATIONS = 1 << 18  # a contraction operand is stored when (elements x reuse) reaches this
@@ -89,6 +92,7 @@ UNARY_OPS = {
     "square": "square",
     "tanh": "tanh",
     "silu": "silu",
+    "log": "log",
 }
 
 
@@ -686,7 +690,11 @@ class HIPCodegen(Codegen):
         width, inner, outer = self._row_layout(shape, dim)
         rows = outer * inner
         if inner == 1 and width >= 64:
-            self._row_softmax(out, x, shape, dim, width, rows)
+            splits, chunk, lanes = self._row_splits(rows, width, x.dtype)
+            if splits > 1 and not self._row_plan(width, x.dtype)[3]:
+                self._split_softmax(out, x, shape, dim, width, rows, splits, chunk, lanes)
+            else:
+                self._row_softmax(out, x, shape, dim, width, rows)
             self.parallel_reductions += 1
         else:
             self._thread_softmax(out, x, shape, dim, width, rows)
@@ -834,6 +842,213 @@ class HIPCodegen(Codegen):
                 value = self._lane_values(k, [f"chroma::fast_exp({k.emit(element())} - peak) * inverse"])
                 k.store(slot, out.dtype, Kernel.flatten(self._row_coords(k, row, shape, dim, Aff.of(j_atom)), shape), value)
         self.launch(k, max(1, min(-(-rows // 256), MAX_GRID)), 256, [x], kind="softmax_lines")
+
+    # -------------------------------------------------------------------------------- row statistics
+    # A row's softmax statistics in one HBM pass: each thread keeps an online maximum ``peak``, the sum
+    # ``total`` of exp(x - peak) over the elements it read (rescaled when the maximum grows) and a NaN
+    # flag; the workgroup then combines its threads'. Rows too few to fill the chip are split over
+    # workgroups (``_row_partials``), whose (peak, total) pairs a later launch combines in the same way.
+
+    @staticmethod
+    def _row_splits(rows: int, width: int, dtype: torch.dtype) -> Tuple[int, int, int]:
+        """(splits per row, elements per split, lanes): one workgroup per row when there are at least
+        ``SPLIT_ROW_LIMIT`` rows or a row is narrow; otherwise enough splits for about ``SPLIT_ROW_BLOCKS``
+        workgroups, each at least ``ROW_UNROLL`` vectors per thread (one round of loads in flight)."""
+        lanes = choose_lanes(width, dtype, 8 if dtype == torch.bfloat16 else 4)
+        step = ROW_THREADS * lanes
+        if rows >= SPLIT_ROW_LIMIT or width < 2 * ROW_UNROLL * step:
+            return 1, width, lanes
+        wanted = -(-SPLIT_ROW_BLOCKS // rows)
+        chunk = -(-(-(-width // wanted)) // step) * step
+        chunk = max(chunk, ROW_UNROLL * step)
+        return -(-width // chunk), chunk, lanes
+
+    def _row_stats(self, k: Kernel, x: Value, shape, dim: int, row: Aff, width: int, begin: str, end: str) -> None:
+        """Declare ``row_peak``, ``row_total`` and ``row_bad`` (1 when a NaN was read) for elements [begin,
+        end) of row ``row`` (``begin`` a multiple of the workgroup's step; ``end`` a multiple of the lanes).
+        ``ROW_UNROLL`` vector loads per thread are requested before their arithmetic."""
+        lanes, threads = k.lanes, ROW_THREADS
+        step = threads * lanes
+        neg_inf = float_literal(-math.inf)
+
+        def names_of(j: Aff) -> List[str]:
+            names = k.emit(self.read(k, x, self._row_coords(k, row, shape, dim, j)))
+            return names if isinstance(names, list) else [names] * lanes
+
+        def accumulate(names: List[str]) -> None:
+            level = list(names)
+            while len(level) > 1:
+                level = [f"__builtin_fmaxf({a}, {b})" for a, b in zip(level[::2], level[1::2])] + level[len(level) // 2 * 2 :]
+            terms = " + ".join(f"chroma::fast_exp({name} - top)" for name in names)
+            k.line(f"{{ const float top = __builtin_fmaxf(peak, {level[0]});")
+            k.line("  bad = bad | " + " | ".join(f"__builtin_isnan({name})" for name in names) + ";")
+            k.line(f"  if (top != {neg_inf}) total = total * chroma::fast_exp(peak - top) + ({terms});")
+            k.line("  peak = top; }")
+
+        k.line(f"float peak = {neg_inf}, total = 0.0f;")
+        k.line("bool bad = false;")
+        k.line(f"uint32_t base = {begin} + threadIdx.x * {lanes}u;")
+        with k.block(f"for (; base + {(ROW_UNROLL - 1) * step}u < {end}; base += {ROW_UNROLL * step}u) {{"):
+            groups = [names_of(Aff.of(k.vector_atom(f"base + {u * step}u", width - 1))) for u in range(ROW_UNROLL)]
+            for names in groups:
+                accumulate(names)
+        with k.block(f"for (; base < {end}; base += {step}u) {{"):
+            accumulate(names_of(Aff.of(k.vector_atom("base", width - 1))))
+        waves = threads // 64
+        k.line(f"const float row_peak = chroma::block_max<{waves}>(peak, scratch);")
+        k.line(f"const float row_total = chroma::block_sum<{waves}>(peak == {neg_inf} ? 0.0f : total * chroma::fast_exp(peak - row_peak), scratch);")
+        k.line(f"const bool row_bad = chroma::block_max<{waves}>(bad ? 1.0f : 0.0f, scratch) != 0.0f;")
+
+    def _row_partials(self, x: Value, shape, dim: int, width: int, rows: int, splits: int, chunk: int, lanes: int) -> Value:
+        """One workgroup per (row, split): the split's (peak, total) into a float pair of a scratch buffer;
+        a split that read a NaN stores NaN as its peak."""
+        partials = self.allocate((rows * splits * 2,), torch.float32)
+        k = Kernel(lanes)
+        slot = k.slot(partials.name, torch.float32, writable=True, extent=self.extents[partials.name])
+        row = Aff.of(k.atom(f"blockIdx.x / {splits}u", rows - 1, prefix="r"))
+        k.line(f"const uint32_t begin = blockIdx.x % {splits}u * {chunk}u;")
+        k.line(f"const uint32_t end = begin + {chunk}u < {width}u ? begin + {chunk}u : {width}u;")
+        self._row_stats(k, x, shape, dim, row, width, "begin", "end")
+        k.line("if (threadIdx.x == 0) {")
+        k.line(f"    {slot}[2u * blockIdx.x] = row_bad ? __builtin_nanf(\"\") : row_peak;")
+        k.line(f"    {slot}[2u * blockIdx.x + 1u] = row_total;")
+        k.line("}")
+        self.launch(k, rows * splits, ROW_THREADS, [x], kind="row_partials", prologue=[f"__shared__ float scratch[{ROW_THREADS // 64}];"])
+        return partials
+
+    @staticmethod
+    def _combine_partials(k: Kernel, slot: str, splits: int, first: str, stride: int, threads: int, reduce: str) -> None:
+        """Declare ``row_peak``, ``row_total``, ``row_bad`` from the ``splits`` (peak, total) pairs at
+        ``slot[2 * (first + s)]`` read by ``threads`` threads (``reduce``: "wave" or "block")."""
+        neg_inf = float_literal(-math.inf)
+        lane = "threadIdx.x % 64u" if reduce == "wave" else "threadIdx.x"
+        k.line(f"float peak = {neg_inf}, total = 0.0f;")
+        k.line("bool bad = false;")
+        with k.block(f"for (uint32_t s = {lane}; s < {splits}u; s += {stride}u) {{"):
+            k.line(f"const float p = {slot}[2u * ({first} + s)], t = {slot}[2u * ({first} + s) + 1u];")
+            k.line("bad = bad | __builtin_isnan(p);")
+            k.line("const float top = __builtin_fmaxf(peak, p);")
+            k.line(f"if (top != {neg_inf}) total = total * chroma::fast_exp(peak - top) + (p == {neg_inf} || __builtin_isnan(p) ? 0.0f : t * chroma::fast_exp(p - top));")
+            k.line("peak = top;")
+        scaled = f"peak == {neg_inf} ? 0.0f : total * chroma::fast_exp(peak - row_peak)"
+        if reduce == "wave":
+            k.line("const float row_peak = chroma::wave_max(peak);")
+            k.line(f"const float row_total = chroma::wave_sum({scaled});")
+            k.line("const bool row_bad = chroma::wave_max(bad ? 1.0f : 0.0f) != 0.0f;")
+        else:
+            waves = threads // 64
+            k.line(f"const float row_peak = chroma::block_max<{waves}>(peak, scratch);")
+            k.line(f"const float row_total = chroma::block_sum<{waves}>({scaled}, scratch);")
+            k.line(f"const bool row_bad = chroma::block_max<{waves}>(bad ? 1.0f : 0.0f, scratch) != 0.0f;")
+
+    @staticmethod
+    def _lse_of_stats() -> str:
+        """C expression of torch's log-sum-exp from the row statistics: NaN if a NaN was read, +inf for a
+        +inf maximum, -inf for an all -inf row, else log(total) + peak."""
+        inf = float_literal(math.inf)
+        return (f"row_bad ? __builtin_nanf(\"\") : (row_peak == {inf} ? {inf} : "
+                f"(row_peak == -{inf} ? -{inf} : logf(row_total) + row_peak))")
+
+    def _split_softmax(self, out: Value, x: Value, shape, dim: int, width: int, rows: int, splits: int, chunk: int, lanes: int) -> None:
+        """Softmax of few wide rows (a vocabulary row of logits): ``_row_partials`` gives each split's
+        statistics; then each (row, split) workgroup combines its row's pairs and writes its split of the
+        row as exp(x - max) times the reciprocal of the sum (the second read of the split mostly hits the
+        last-level cache). A row with a NaN, a +inf or only -inf gives NaN everywhere, as the reference's
+        exp(x - max) / sum does."""
+        partials = self._row_partials(x, shape, dim, width, rows, splits, chunk, lanes)
+        k = Kernel(lanes)
+        k.streaming = STREAMING_STORES and math.prod(shape) * ITEMSIZE[out.dtype] >= STREAMING_BYTES
+        part_slot = k.slot(partials.name, torch.float32, extent=self.extents[partials.name])
+        slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        row_atom = k.atom(f"blockIdx.x / {splits}u", rows - 1, prefix="r")
+        row = Aff.of(row_atom)
+        self._combine_partials(k, part_slot, splits, f"{row_atom.name} * {splits}u", ROW_THREADS, ROW_THREADS, "block")
+        k.line('const float inverse = row_bad || __builtin_isinf(row_peak) ? __builtin_nanf("") : 1.0f / row_total;')
+        k.line(f"const uint32_t begin = blockIdx.x % {splits}u * {chunk}u;")
+        k.line(f"const uint32_t end = begin + {chunk}u < {width}u ? begin + {chunk}u : {width}u;")
+        step = ROW_THREADS * lanes
+
+        def write(j: Aff, names: List[str]) -> None:
+            result = self._lane_values(k, [f"chroma::fast_exp({name} - row_peak) * inverse" for name in names])
+            k.store(slot, out.dtype, Kernel.flatten(self._row_coords(k, row, shape, dim, j), shape), result)
+
+        def names_of(j: Aff) -> List[str]:
+            names = k.emit(self.read(k, x, self._row_coords(k, row, shape, dim, j)))
+            return names if isinstance(names, list) else [names] * lanes
+
+        k.line(f"uint32_t base = begin + threadIdx.x * {lanes}u;")
+        with k.block(f"for (; base + {(ROW_UNROLL - 1) * step}u < end; base += {ROW_UNROLL * step}u) {{"):
+            js = [Aff.of(k.vector_atom(f"base + {u * step}u", width - 1)) for u in range(ROW_UNROLL)]
+            loaded = [names_of(j) for j in js]
+            for j, names in zip(js, loaded):
+                write(j, names)
+        with k.block(f"for (; base < end; base += {step}u) {{"):
+            j = Aff.of(k.vector_atom("base", width - 1))
+            write(j, names_of(j))
+        self.launch(k, rows * splits, ROW_THREADS, [x, partials], kind="softmax_split",
+                    prologue=[f"__shared__ float scratch[{ROW_THREADS // 64}];"])
+
+    # -------------------------------------------------------------------------------- log-sum-exp
+    def logsumexp(self, meta, x: Value, dim: int) -> Value:
+        """log(sum(exp(x))) along ``dim``: an extension (the reference's operator table has no
+        ``aten.logsumexp``) with torch's definition: m = the maximum along the axis (0 when infinite),
+        m + log(sum(exp(x - m))), float statistics, rounded once to the output type; a NaN element gives
+        NaN and a +inf element (without NaN) +inf. Rows of 64 or more contiguous elements take one HBM pass
+        (``_row_stats``): one workgroup per row, or, when there are fewer rows than fill the chip (a few
+        vocabulary rows of logits), a split of each row over workgroups and a small combining launch."""
+        out = self.allocate(tuple(meta.shape), meta.dtype)
+        shape = tuple(x.shape)
+        width, inner, outer = self._row_layout(shape, dim)
+        rows = outer * inner
+        if inner != 1 or width < 64:
+            self._thread_lse(out, x, shape, dim, width, rows)
+            return out
+        splits, chunk, lanes = self._row_splits(rows, width, x.dtype)
+        self.parallel_reductions += 1
+        if splits == 1:
+            k = Kernel(lanes)
+            slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+            row_atom = k.atom("blockIdx.x", rows - 1, prefix="r")
+            self._row_stats(k, x, shape, dim, Aff.of(row_atom), width, "0u", f"{width}u")
+            with k.block("if (threadIdx.x == 0) {"):
+                k.store(slot, out.dtype, Aff.of(row_atom), self._lane_values(k, [self._lse_of_stats()]))
+            self.launch(k, rows, ROW_THREADS, [x], kind="logsumexp_rows", prologue=[f"__shared__ float scratch[{ROW_THREADS // 64}];"])
+            return out
+        partials = self._row_partials(x, shape, dim, width, rows, splits, chunk, lanes)
+        k = Kernel(1)
+        part_slot = k.slot(partials.name, torch.float32, extent=self.extents[partials.name])
+        slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        k.line("const uint32_t r = blockIdx.x * 4u + threadIdx.x / 64u;")
+        k.line(f"if (r >= {rows}u) return;  // whole waves leave together")
+        self._combine_partials(k, part_slot, splits, f"r * {splits}u", 64, 256, "wave")
+        with k.block("if (threadIdx.x % 64u == 0) {"):
+            k.store(slot, out.dtype, Aff.of(Atom("r", rows - 1)), self._lane_values(k, [self._lse_of_stats()]))
+        self.launch(k, -(-rows // 4), 256, [partials], kind="logsumexp_combine")
+        return out
+
+    def _thread_lse(self, out: Value, x: Value, shape, dim: int, width: int, rows: int) -> None:
+        """One thread per row (narrow or strided rows): the maximum, then the sum, then the result."""
+        k = Kernel(1)
+        slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        neg_inf = float_literal(-math.inf)
+        with k.block(f"for (uint32_t r = blockIdx.x * 256u + threadIdx.x; r < {rows}u; r += gridDim.x * 256u) {{"):
+            row = Aff.of(Atom("r", rows - 1))
+            j_atom = Atom("j", width - 1)
+
+            def element() -> tuple:
+                return self.read(k, x, self._row_coords(k, row, shape, dim, Aff.of(j_atom)))
+
+            k.line(f"float row_peak = {neg_inf};")
+            k.line("bool row_bad = false;")
+            with k.block(f"for (uint32_t j = 0; j < {width}u; ++j) {{"):
+                name = k.emit(element())
+                k.line(f"row_peak = __builtin_fmaxf(row_peak, {name}); row_bad = row_bad | __builtin_isnan({name});")
+            k.line("const float shift = __builtin_isinf(row_peak) ? 0.0f : row_peak;")
+            k.line("float row_total = 0.0f;")
+            with k.block(f"for (uint32_t j = 0; j < {width}u; ++j) {{"):
+                k.line(f"row_total += chroma::fast_exp({k.emit(element())} - shift);")
+            k.store(slot, out.dtype, row, self._lane_values(k, [self._lse_of_stats()]))
+        self.launch(k, max(1, min(-(-rows // 256), MAX_GRID)), 256, [x], kind="logsumexp_lines")
 
     # -------------------------------------------------------------------------------- RMSNorm
     def norm(self, meta, x: Value, weight: Value, epsilon: float) -> Value:

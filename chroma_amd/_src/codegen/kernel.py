@@ -144,6 +144,7 @@ UNARY_CODE = {
     "tanh": "chroma::fast_tanh({x})",
     "silu": "chroma::fast_silu({x})",
     "square": "({x} * {x})",
+    "log": "logf({x})",
 }
 BINARY_CODE = {
     "add": "({a} + {b})",

@@ -3,7 +3,10 @@
 The accepted operators and their families follow the reference table (chroma/_src/lowering.py:34-86).
 Two elementwise operators are added as extensions because torch 2.10's export emits them where the
 reference's torch emitted in-table decompositions: ``aten.silu.default`` and ``aten.tanh.default``.
-Both backends evaluate them as ``x * (1 / (1 + exp(-x)))`` and ``tanh(x)``.
+Both backends evaluate them as ``x * (1 / (1 + exp(-x)))`` and ``tanh(x)``. Two more extensions serve
+vocabulary-wide log-probabilities: ``aten.log.default`` (``log(x)``) and ``aten.logsumexp.default``
+over one axis, with torch's definition ``m + log(sum(exp(x - m)))``, m the maximum along the axis
+(0 when it is infinite), float statistics, the result rounded once.
 
 Per-family behaviour (reference lowering.py:112-284):
 
@@ -49,6 +52,7 @@ ELEMENTWISE = (
     # extensions (see module docstring)
     "aten.silu.default",
     "aten.tanh.default",
+    "aten.log.default",
 )
 LAYOUT = (
     "aten.view.default",
@@ -80,6 +84,7 @@ OPERATIONS.update(
         "aten.sum.default": "reduction",
         "aten.sum.dim_IntList": "reduction",
         "aten.softmax.int": "softmax",
+        "aten.logsumexp.default": "logsumexp",  # extension (see module docstring)
         "aten.topk.default": "topk",
         "aten.cat.default": "cat",
         "aten.arange.default": "constant",
@@ -271,6 +276,16 @@ def lower(codegen, target: Any, meta: Any, args: Tuple[Any, ...], kwargs: Dict[s
             return codegen.softmax(meta, x, dim)
         vector = meta.new_empty((1,))
         return codegen.reshape(meta, codegen.softmax(vector, codegen.reshape(vector, x), 0))
+    if family == "logsumexp":
+        x = args[0]
+        if x.dtype not in FLOAT_DTYPES or meta.dtype not in FLOAT_DTYPES or not x.shape:
+            raise NotImplementedError(name)
+        dims = list(_arg(args, kwargs, 1, "dim", []))
+        if len(dims) != 1:
+            raise NotImplementedError("logsumexp over one axis")
+        if x.dtype != meta.dtype:
+            x = codegen.cast(meta.new_empty(x.shape), x)
+        return codegen.logsumexp(meta, x, axis(dims[0], len(x.shape)))
     if family == "topk":
         x = args[0]
         dim = axis(_arg(args, kwargs, 2, "dim", -1), len(x.shape))

@@ -110,21 +110,33 @@ __device__ __forceinline__ uint32_t load_streaming_bf16x2(const uint16_t* p) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Wave64 reductions (butterfly over all 64 lanes; every lane receives the result).
+// Wave64 reductions; every lane receives the result. Within each 16-lane row the partners come from DPP
+// (quad_perm [1,0,3,2] and [2,3,0,1], then row_half_mirror and row_mirror), so the exchange is folded
+// into the add or max itself (``v_add_f32_dpp``) instead of a separate permute through the LDS
+// crossbar; across rows gfx950's ``v_permlane16_swap`` and ``v_permlane32_swap`` exchange whole rows and
+// half-waves in registers. Each step combines two equal-sized partial results, and both partners
+// combine the same two values, so all 64 lanes end with bit-identical results.
+template <int Control> __device__ __forceinline__ float dpp_partner(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), Control, 0xF, 0xF, true));
+}
+
+template <class Op> __device__ __forceinline__ float wave_reduce(float v, Op op) {
+    v = op(v, dpp_partner<0xB1>(v));   // quad_perm [1,0,3,2]: lane ^ 1
+    v = op(v, dpp_partner<0x4E>(v));   // quad_perm [2,3,0,1]: lane ^ 2
+    v = op(v, dpp_partner<0x141>(v));  // row_half_mirror: the other quad of each 8 lanes
+    v = op(v, dpp_partner<0x140>(v));  // row_mirror: the other half of each 16-lane row
+    const auto rows = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = op(__uint_as_float(rows[0]), __uint_as_float(rows[1]));  // rows 0+1 and 2+3
+    const auto halves = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return op(__uint_as_float(halves[0]), __uint_as_float(halves[1]));  // lanes 0-31 + 32-63
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) {
-        v += __shfl_xor(v, offset, kWave);
-    }
-    return v;
+    return wave_reduce(v, [](float a, float b) { return a + b; });
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) {
-        v = __builtin_fmaxf(v, __shfl_xor(v, offset, kWave));
-    }
-    return v;
+    return wave_reduce(v, [](float a, float b) { return __builtin_fmaxf(a, b); });
 }
 
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {

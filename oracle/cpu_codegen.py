@@ -43,6 +43,7 @@ UNARY = {
     # extensions (chroma_amd/_src/lowering.py)
     "aten.tanh.default": "std::tanh(x)",
     "aten.silu.default": "x * (1.0f / (1.0f + std::exp(-x)))",
+    "aten.log.default": "std::log(x)",
 }
 BINARY = {"aten.add.Tensor": "+", "aten.sub.Tensor": "-", "aten.mul.Tensor": "*", "aten.div.Tensor": "/"}
 
@@ -87,6 +88,7 @@ class CPUCodegen(Codegen):
         self.expert_contractions = 0
         self.lines: List[Union[str, Value]] = []
         self.gathers = {}
+        self.extensions = False  # the program uses a kernel of extensions.h
 
     # -- storage -------------------------------------------------------------------------------------
     def extern(self, tensor: torch.Tensor, kind: str, offset: int) -> Value:
@@ -196,6 +198,13 @@ class CPUCodegen(Codegen):
     def softmax(self, meta, x: Value, dim: int) -> Value:
         out = self.allocate(tuple(meta.shape), meta.dtype)
         self.record(f"softmax<{dim}>({out.name}, {x.name});", [x])
+        return out
+
+    def logsumexp(self, meta, x: Value, dim: int) -> Value:
+        """Extension (no reference counterpart): ``extensions.h`` ``logsumexp``."""
+        out = self.allocate(tuple(meta.shape), meta.dtype)
+        self.extensions = True
+        self.record(f"logsumexp<{dim}>({out.name}, {x.name});", [x])
         return out
 
     def topk(self, meta, x: Value, dim: int, largest: bool, sort: bool):
@@ -342,6 +351,8 @@ class CPUCodegen(Codegen):
         stats = dict(stats, expert_contractions=self.expert_contractions, backend="cpu", math_library="cblas" if self.blas else "portable")
         body = "\n".join(self.render(line) for line in self.lines)
         source = TEMPLATE.format(weight_bytes=stats["weight_bytes"], workspace_bytes=stats["workspace_bytes"], body=body)
+        if self.extensions:
+            source = '#include "codegen/cpu/extensions.h"\n' + source
         return GeneratedCode({"model.cc": source}, "model.cc", flags, stats, inputs, outputs, self.weights)
 
 

@@ -582,6 +582,42 @@ def test_dev_decoder_with_wraparound(tmp_path, dev_model):
         assert decoder.position == 48
 
 
+def test_dev_decoder_c4_config(tmp_path, dev_model):
+    """C4 at its own configuration: ``Decoder(export_cached(m, 256, 256), export_cached(m, 256, 1))`` on hip
+    and on the oracle, a prefill of 8 tokens ~U[0, 201088) (seed 0) and 32 single-token steps. Every step is
+    held to fp32 rel 1e-4 / abs 1e-5 against the oracle's decoder, with equal argmax wherever the top two
+    logits differ by more than 1e-4; at every position the cached logits also match the padded uncached
+    graph ``export_uncached(m, 256)`` run by hip on the same prefix, at the reference decode benchmark's own
+    bar, rtol 2e-5 / atol 2e-6 (scripts/benchmark_decode.py:96-106); and the uncached graph matches the
+    oracle's at the first, a middle and the last position."""
+    from chroma_amd.models.cached import export_cached, export_uncached
+
+    context, prompt, steps = 256, 8, 32
+    graphs = [export_cached(dev_model, context, context), export_cached(dev_model, context, 1), export_uncached(dev_model, context)]
+    hip = [chroma_amd.compile(g, tmp_path / f"hip{i}") for i, g in enumerate(graphs)]
+    cpu = [compile_cpu(g, tmp_path / f"cpu{i}") for i, g in enumerate(graphs)]
+    tokens = torch.randint(0, 201088, (prompt + steps,), generator=torch.Generator().manual_seed(0)).numpy()
+    padded = np.zeros(context, dtype=np.int64)
+    last = np.zeros(1, dtype=np.int64)
+    uncached_checks = {prompt - 1, prompt + steps // 2, prompt + steps - 1}
+    with Decoder(hip[0], hip[1]) as decoder, Decoder(cpu[0], cpu[1]) as reference:
+        for start, end in ((0, prompt), *((i, i + 1) for i in range(prompt, prompt + steps))):
+            got, want = decoder.append(tokens[start:end]), reference.append(tokens[start:end])
+            np.testing.assert_allclose(got, want, **F32)
+            top = np.sort(want, axis=-1)[:, -2:]
+            if top[0, 1] - top[0, 0] > 1e-4:
+                assert got.argmax() == want.argmax(), end
+            padded[start:end] = tokens[start:end]
+            last[0] = end - 1
+            uncached = hip[2](padded, last)
+            np.testing.assert_allclose(got, uncached, rtol=2e-5, atol=2e-6)
+            if end - 1 in uncached_checks:
+                np.testing.assert_allclose(uncached, cpu[2](padded, last), **F32)
+        assert decoder.position == prompt + steps
+    for program in (*hip, *cpu):
+        program.close()
+
+
 def test_dev_decoder_selects_on_device(tmp_path, dev_model):
     """On-device selection over the dev model's 201,088 logits: ``append_top`` and ``greedy`` of a decoder of
     hip programs (the logits stay on the device; a selection program copies them and returns k values and
@@ -846,3 +882,67 @@ def test_fused_attention_per_head_mask(tmp_path, tokens, kv_heads, group, dim):
         got = model(*inputs)
     want = compile_cpu(exported, tmp_path / "cpu")(*[numpy_of(v) for v in inputs])
     compare(got, want)
+
+
+# ------------------------------------------------------------------------- vocabulary-wide row reductions
+class RowLogSumExp(torch.nn.Module):
+    def forward(self, x):
+        return torch.logsumexp(x, -1)
+
+
+class RowSoftmax(torch.nn.Module):
+    def forward(self, x):
+        return torch.softmax(x, -1)
+
+
+def vocabulary_rows(rows: int, width: int, dtype, seed: int) -> torch.Tensor:
+    """Logit-like rows N(0, 3) with a NaN row, a +inf row, a row of -inf and a row with -inf runs."""
+    x = torch.randn(rows, width, generator=torch.Generator().manual_seed(seed)) * 3
+    if rows >= 5:
+        x[1, width // 3] = float("nan")
+        x[2, width - 1] = float("inf")
+        x[3] = -float("inf")
+        x[4, : width // 2] = -float("inf")
+    return x.to(dtype)
+
+
+@pytest.mark.parametrize("rows, width, dtype", [(8, 201088, torch.float32), (8, 201088, torch.bfloat16), (2048, 201088, torch.float32),
+                                                (5, 100003, torch.float32), (300, 4096, torch.bfloat16)])
+def test_vocabulary_logsumexp(tmp_path, rows, width, dtype):
+    """log-sum-exp over vocabulary rows against the oracle (fp32 rel 1e-4 / abs 1e-5, bf16 rel 2e-2) and,
+    on ordinary rows, against float64: split rows (few rows: partial statistics and a combining launch),
+    one workgroup per row (2048 rows), a width that is not a multiple of the vector width, and NaN, +inf
+    and -inf rows (NaN, +inf, -inf exactly)."""
+    x = vocabulary_rows(rows, width, dtype, rows + width)
+    exported = torch.export.export(RowLogSumExp(), (x,))
+    with chroma_amd.compile(exported, tmp_path / "hip") as model:
+        assert model.stats["launches"] == (1 if rows >= 256 else 2)
+        got = as_float(model(x))
+    want = as_float(compile_cpu(exported, tmp_path / "cpu")(numpy_of(x)))
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    special = ~np.isfinite(want)
+    np.testing.assert_array_equal(got[special & ~np.isnan(want)], want[special & ~np.isnan(want)])
+    assert_close(got[~special], want[~special], **(BF16 if dtype == torch.bfloat16 else F32))
+    if rows >= 5:
+        assert np.isnan(got[1]) and got[2] == np.inf and got[3] == -np.inf
+    ordinary = [r for r in range(min(rows, 16)) if r not in (1, 2, 3)] if rows >= 5 else list(range(rows))
+    exact = x[ordinary].double().numpy()
+    peak = np.max(exact, axis=1)
+    closed = peak + np.log(np.exp(exact - peak[:, None]).sum(axis=1))
+    np.testing.assert_allclose(got[ordinary], closed, rtol=1e-4 if dtype == torch.float32 else 8e-3)
+
+
+@pytest.mark.parametrize("rows, width, dtype", [(8, 201088, torch.float32), (8, 201088, torch.bfloat16), (3, 100003, torch.float32)])
+def test_vocabulary_softmax_split_rows(tmp_path, rows, width, dtype):
+    """Softmax of a few vocabulary rows splits each row over workgroups (partial statistics, then each
+    split normalises its part) and matches the oracle, NaN/+inf/-inf rows included (all NaN, as the
+    reference's exp(x - max) / sum gives)."""
+    x = vocabulary_rows(rows, width, dtype, 7 * rows + width)
+    exported = torch.export.export(RowSoftmax(), (x,))
+    with chroma_amd.compile(exported, tmp_path / "hip") as model:
+        assert model.stats["launches"] == 2
+        got = model(x)
+    want = compile_cpu(exported, tmp_path / "cpu")(numpy_of(x))
+    compare(got, want)
+    ordinary = [r for r in range(rows) if r not in (1, 2, 3)] if rows >= 5 else list(range(rows))
+    np.testing.assert_allclose(as_float(got)[ordinary].astype(np.float64).sum(axis=1), 1.0, rtol=1e-3 if dtype == torch.float32 else 2e-2)

@@ -241,3 +241,39 @@ def test_extension_unaries_match_eager(tmp_path, name, dtype):
     np.testing.assert_allclose(got[finite], want[finite], rtol=rtol, atol=1e-37)
     # sign of zero and of tiny results is kept
     np.testing.assert_array_equal(np.signbit(got[finite & (want == 0)]), np.signbit(want[finite & (want == 0)]))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_logsumexp_and_log_match_eager(tmp_path, dtype):
+    """The oracle's ``logsumexp`` (an extension: torch's m + log(sum(exp(x - m))), m the maximum, 0 when
+    infinite) and ``log`` against eager torch: ordinary rows, a row with NaN, a row with +inf, a row of
+    -inf, a row with -inf among finite values, a constant row (exactly m + log(n)); the last axis, the
+    first axis and a middle axis of a 3-d tensor; and the closed form on the constant row."""
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(9, 300, generator=g) * 4
+    x[1, 17] = float("nan")
+    x[2, 5] = float("inf")
+    x[3] = -float("inf")
+    x[4, ::3] = -float("inf")
+    x[5] = 2.5
+    x = x.to(dtype)
+    cube = (torch.randn(3, 70, 5, generator=g) * 3).to(dtype)
+
+    def fn(x, cube):
+        return (torch.logsumexp(x, -1), torch.logsumexp(x, 0, keepdim=True), torch.logsumexp(cube, 1),
+                torch.log(x.abs() + 0.5), torch.logsumexp(x * 0.5, dim=1, keepdim=True))
+
+    _, out = run(tmp_path, Function(fn), x, cube)
+    for got, want in zip(out, Function(fn)(x, cube)):
+        got, want = as_float(got), want.float().numpy()
+        assert np.array_equal(np.isnan(got), np.isnan(want))
+        finite = np.isfinite(want)
+        np.testing.assert_array_equal(got[~finite & ~np.isnan(want)], want[~finite & ~np.isnan(want)])
+        np.testing.assert_allclose(got[finite], want[finite], rtol=2e-6 if dtype == torch.float32 else 8e-3, atol=1e-6)
+    lse = as_float(out[0])
+    assert np.isnan(lse[1]) and lse[2] == np.inf and lse[3] == -np.inf
+    # a constant row of 2.5: 2.5 + log(300) (float64), within the float sum's rounding
+    assert abs(lse[5] - (2.5 + np.log(300.0))) <= (1e-6 if dtype == torch.float32 else 0.04)
+    # brute force in float64 on an ordinary row
+    row = x[0].double().numpy()
+    assert abs(lse[0] - (row.max() + np.log(np.exp(row - row.max()).sum()))) <= 2e-6 * abs(lse[0]) + (0 if dtype == torch.float32 else 0.05)
