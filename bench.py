@@ -1,4 +1,4 @@
-"""Benchmark of the hip backend on one MI355X.
+"""Benchmark of the hip backend on one MI355X: every BASELINE configuration in one JSON line.
 
 Headline (``value``): the fused-kernel HBM throughput of BASELINE config C2 - the fp32 bandwidth graph
 ``softmax(tanh(x*0.5+y)*sigmoid(y) - exp(clamp(x,-8,8))*1e-3, -1)`` over x, y in U(-4, 4) [16384, 8192]
@@ -6,15 +6,21 @@ Headline (``value``): the fused-kernel HBM throughput of BASELINE config C2 - th
 execution of the compiled program on inputs already resident in HBM; GB/s counts the algorithmic bytes
 (read x, read y, write the output: 3 x 16384 x 8192 x 4 = 1,610,612,736 B per step).
 
-Beside it the same JSON line reports:
+Beside it the same line reports:
 
-* ``roofline``: the dominant kernel's algorithmic bytes over its average duration from hipEvents recorded
-  on the runtime's own stream around the timed launches, against MI355X's 8 TB/s; ``traffic`` comes from
+* ``roofline``: the C2 kernel's algorithmic bytes over its average duration from hipEvents recorded on
+  the runtime's own stream around the timed launches, against MI355X's 8 TB/s; ``traffic`` comes from
   the committed rocprofv3 FETCH_SIZE/WRITE_SIZE measurement (profiles/) when present;
-* ``cpu_baseline``: the CPU restatement of Chroma's CPU backend (oracle/, single thread, BLAS pinned to one
-  thread) timed on this host on a bounded sample of the same graph;
-* ``dev_forward`` / ``decode``: the dev MoE model's 8-token forward and its 256-position KV-cached decode
-  step (BASELINE configs C3 and C4), end-to-end from host arrays to host arrays, with the oracle's times.
+* ``cpu_baseline``: the CPU restatement of Chroma's CPU backend (oracle/, one thread) timed on this host
+  on a bounded sample of the same graph;
+* ``hbm_copy``: a plain copy kernel's GB/s, the practical HBM ceiling the fractions can be read against;
+* ``rows``: row reductions (RMSNorm, softmax, log-sum-exp) at the widths of C1, C5 and the vocabulary;
+* ``c1``: the MLP block; ``dev_forward`` (C3) and ``decode`` (C4): the dev MoE model's 8-token forward and
+  256-position KV-cached decode, end to end (host arrays in and out) in the reference's interleaved
+  method, with device-only times and rooflines; ``c5``: the GPT-OSS-20B-shaped bf16 model's 2048-token
+  prefill (matrix-core fraction on the work actually performed) and its decode step at a full
+  4096-position cache (HBM fraction), with the oracle's time and parity on a reduced slice;
+* ``host``: CPU model, core counts, ROCm version and GPU name.
 """
 
 from __future__ import annotations
@@ -22,6 +28,8 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import platform
+import random
 import statistics
 import sys
 import tempfile
@@ -34,33 +42,105 @@ sys.path.insert(0, str(ROOT))
 METRIC = "dev-model 8-tok fwd ms; 256-KV decode ms; fused-kernel HBM GB/s"
 C2_SHAPE = (16384, 8192)
 C2_BYTES = 3 * C2_SHAPE[0] * C2_SHAPE[1] * 4
+C1_BYTES = 3 * 4096 * 1024 * 4 + 2 * 8 * 1024 * 4
+C1_FLOPS = 2 * 8 * 1024 * 4096 * 3
+# C3: unembedding 102,957,056 + 12 x (dense 155,856 + all 12 experts' weights and biases 2,377,728)
+# + embedding rows 4,096 + logits 6,434,816.
+C3_BYTES = 102_957_056 + 12 * (155_856 + 2_377_728) + 4_096 + 6_434_816
+# C4 step: unembedding + 12 x (dense + 4 selected experts x (131,072 + 1,024 + 65,536 + 512)) + K/V cache
+# 393,216 + one logits row 804,352.
+C4_BYTES = 102_957_056 + 12 * (155_856 + 4 * (131_072 + 1_024 + 65_536 + 512)) + 393_216 + 804_352
 HBM_PEAK_GBS = 8000.0
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = ROOT / "profiles" / "c2_fused_softmax_traffic.txt"
+VOCAB = 201088
 
 
 def log(message: str) -> None:
     print(f"[bench] {message}", file=sys.stderr, flush=True)
 
 
-def c2_module():
+def host_info() -> dict:
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    rocm = "unknown"
+    for candidate in (Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / ".info" / "version",):
+        if candidate.exists():
+            rocm = candidate.read_text().strip()
     import torch
 
-    class BandwidthGraph(torch.nn.Module):
-        def forward(self, x, y):
-            z = torch.tanh(x * 0.5 + y) * torch.sigmoid(y) - torch.exp(torch.clamp(x, -8, 8)) * 1e-3
-            return torch.softmax(z, -1)
+    return {
+        "cpu_model": model,
+        "nproc": os.cpu_count(),
+        "cpus_available": len(os.sched_getaffinity(0)),
+        "rocm": rocm,
+        "torch": torch.__version__,
+        "python": platform.python_version(),
+        "oracle_threads": 1,
+    }
 
-    return BandwidthGraph()
+
+def roofline(amount: float, ms: float, bound: str = "hbm", traffic=None) -> dict:
+    """Achieved rate of ``amount`` bytes (hbm) or flops (mfma) in ``ms`` against MI355X's peak."""
+    if bound == "hbm":
+        achieved = amount / (ms * 1e-3) / 1e9
+        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic}
+    achieved = amount / (ms * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / BF16_MFMA_PEAK_TFLOPS, 4), "traffic": traffic}
 
 
-def c2_inputs(rows: int = C2_SHAPE[0], cols: int = C2_SHAPE[1]):
-    import torch
+def device_ms(program, runs: int, warmup: int = 3) -> float:
+    """Average time of one execution of ``program``'s plan on what its staging regions hold, from hipEvents
+    on the runtime's stream around ``runs`` back-to-back executions."""
+    native = program.native
+    native.execute(warmup)
+    return native.execute(runs, timed=True) / runs
 
-    generator = torch.Generator().manual_seed(1)
-    x = torch.rand(rows, cols, generator=generator) * 8 - 4
-    y = torch.rand(rows, cols, generator=generator) * 8 - 4
-    return x, y
+
+def interleaved(calls: dict, warmup: int = 10, runs: int = 100, rounds: int = 2, seed: int = 0) -> dict:
+    """The reference's timing method (scripts/benchmark.py:221-230, docs/benchmarks.md:12-16): every call
+    once per round in a seeded shuffled order, ``warmup`` untimed rounds, then ``runs`` timed rounds;
+    repeated ``rounds`` times and pooled; median, p10 and p90 in ms."""
+    samples = {name: [] for name in calls}
+    rng = random.Random(seed)
+    order = list(calls)
+    for _ in range(rounds):
+        for _ in range(warmup):
+            rng.shuffle(order)
+            for name in order:
+                calls[name]()
+        for _ in range(runs):
+            rng.shuffle(order)
+            for name in order:
+                start = time.perf_counter()
+                calls[name]()
+                samples[name].append((time.perf_counter() - start) * 1e3)
+    out = {}
+    for name, values in samples.items():
+        values.sort()
+        out[name] = {"median_ms": round(statistics.median(values), 4), "p10_ms": round(values[len(values) // 10], 4),
+                     "p90_ms": round(values[len(values) * 9 // 10], 4), "samples": len(values)}
+    return out
+
+
+def timed(call, warmup: int, runs: int) -> dict:
+    for _ in range(warmup):
+        call()
+    samples = []
+    for _ in range(runs):
+        start = time.perf_counter()
+        call()
+        samples.append((time.perf_counter() - start) * 1e3)
+    samples.sort()
+    return {"median_ms": round(statistics.median(samples), 4), "p10_ms": round(samples[len(samples) // 10], 4), "runs": runs}
 
 
 def read_traffic():
@@ -73,14 +153,16 @@ def read_traffic():
     return None
 
 
+# ----------------------------------------------------------------------------------------- C2 (headline)
 def bench_c2(args, work: Path) -> dict:
     import numpy as np
     import torch
 
     import chroma_amd
+    from chroma_amd.models.blocks import BandwidthGraph, bandwidth_inputs
 
-    x, y = c2_inputs()
-    exported = torch.export.export(c2_module(), (x, y))
+    x, y = bandwidth_inputs()
+    exported = torch.export.export(BandwidthGraph(), (x, y))
     log("compiling C2 for hip")
     program = chroma_amd.compile(exported, work / "c2")
     native = program.native
@@ -92,40 +174,35 @@ def bench_c2(args, work: Path) -> dict:
     wall = time.perf_counter() - start
     output = np.empty(C2_SHAPE, dtype=np.float32)
     native.download([output])
-    sums = output[:: 1024].sum(axis=1)
+    sums = output[::1024].sum(axis=1)
     if not np.allclose(sums, 1.0, rtol=1e-4):
         raise RuntimeError(f"C2 rows do not sum to 1: {sums[:4]}")
     kernel_ms = event_ms / args.steps
-    achieved = C2_BYTES / (kernel_ms * 1e-3) / 1e9
-    traffic = read_traffic()
+    end_to_end = timed(lambda: program(x.numpy(), y.numpy()), 1, 3)
+    device = native.device
     program.close()
     return {
         "value": C2_BYTES * args.steps / wall / 1e9,
         "ms_per_step": wall / args.steps * 1e3,
         "kernel_ms": kernel_ms,
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-        },
+        "roofline": roofline(C2_BYTES, kernel_ms, traffic=read_traffic()),
         "stats": program.stats,
+        "end_to_end_ms": end_to_end,
+        "device": device,
     }
 
 
 def cpu_c2(work: Path) -> dict:
     """The oracle on a bounded sample of C2 (the first rows), one thread."""
-    import numpy as np
     import torch
 
+    from chroma_amd.models.blocks import BandwidthGraph, bandwidth_inputs
     from oracle import compile_cpu
 
     rows = 2048
-    x, y = c2_inputs()
+    x, y = bandwidth_inputs()
     x, y = x[:rows].contiguous(), y[:rows].contiguous()
-    program = compile_cpu(torch.export.export(c2_module(), (x, y)), work / "c2_cpu")
+    program = compile_cpu(torch.export.export(BandwidthGraph(), (x, y)), work / "c2_cpu")
     arrays = (x.numpy(), y.numpy())
     program(*arrays)
     times = []
@@ -136,6 +213,7 @@ def cpu_c2(work: Path) -> dict:
         times.append(time.perf_counter() - start)
     seconds = statistics.median(times)
     sample_bytes = 3 * rows * C2_SHAPE[1] * 4
+    program.close()
     return {
         "value": round(sample_bytes / seconds / 1e9, 3),
         "unit": "GB/s",
@@ -146,19 +224,102 @@ def cpu_c2(work: Path) -> dict:
     }
 
 
-def timed(call, warmup: int, runs: int) -> dict:
-    for _ in range(warmup):
-        call()
-    samples = []
-    for _ in range(runs):
-        start = time.perf_counter()
-        call()
-        samples.append((time.perf_counter() - start) * 1e3)
-    return {"median_ms": round(statistics.median(samples), 4), "p10_ms": round(sorted(samples)[len(samples) // 10], 4), "runs": runs}
+# ------------------------------------------------------------------------------- HBM ceiling and rows
+def bench_copy(work: Path) -> dict:
+    """A plain copy over [16384, 8192] fp32 (512 MiB read + 512 MiB written per launch)."""
+    import torch
+
+    import chroma_amd
+    from chroma_amd.models.blocks import Copy, bandwidth_inputs
+
+    x = bandwidth_inputs()[0]
+    with chroma_amd.compile(torch.export.export(Copy(), (x,)), work / "copy") as program:
+        program.native.upload([x.numpy()])
+        ms = device_ms(program, 20)
+    moved = 2 * x.numel() * 4
+    return {"workload": "x * 1.0 over [16384, 8192] fp32", "bytes": moved, "ms": round(ms, 4), "gbs": round(moved / (ms * 1e-3) / 1e9, 1),
+            "frac_of_peak": round(moved / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
-def bench_dev(work: Path, runs: int) -> dict:
-    """C3: the dev model's 8-token fp32 forward, host arrays in and out, and the oracle beside it."""
+ROW_CASES = [
+    ("rmsnorm", 2048, 1024), ("rmsnorm", 2048, 2880), ("rmsnorm", 8, VOCAB), ("rmsnorm", 2048, VOCAB),
+    ("softmax", 8, VOCAB), ("softmax", 2048, VOCAB), ("logsumexp", 8, VOCAB), ("logsumexp", 2048, VOCAB),
+]
+
+
+def bench_rows(work: Path, cpu: bool) -> list:
+    """Row reductions in fp32, x ~ N(0, 1) seed 0, inputs resident: device time per execution and GB/s on
+    the algorithmic bytes (read + write of R x D for RMSNorm and softmax, read + R floats for log-sum-exp),
+    checked against the oracle on the first rows; the oracle's time on a sample of at most 64 rows."""
+    import numpy as np
+    import torch
+
+    import chroma_amd
+    from chroma_amd.models.blocks import RowLogSumExp, RowNorm, RowSoftmax
+    from oracle import compile_cpu
+
+    import shutil
+
+    modules = {"rmsnorm": RowNorm, "softmax": RowSoftmax, "logsumexp": RowLogSumExp}
+    results = []
+    for kind, rows, width in ROW_CASES:
+        x = torch.randn(rows, width, generator=torch.Generator().manual_seed(0))
+        module = modules[kind](width) if kind == "rmsnorm" else modules[kind]()
+        moved = rows * width * 4 + (rows * 4 if kind == "logsumexp" else rows * width * 4)
+        with chroma_amd.compile(torch.export.export(module, (x,)), work / f"{kind}_{rows}_{width}") as program:
+            program.native.upload([x.numpy()])
+            ms = device_ms(program, 20 if rows * width < (1 << 26) else 10)
+            got = program(x.numpy())
+            launches = program.stats["launches"]
+        sample = min(rows, 64)
+        head = x[:sample].contiguous()
+        entry = {"kind": kind, "shape": [rows, width], "dtype": "f32", "launches": launches, "ms": round(ms, 4),
+                 "algorithmic_bytes": moved, "roofline": roofline(moved, ms)}
+        if cpu:
+            oracle = compile_cpu(torch.export.export(module, (head,)), work / f"{kind}_{rows}_{width}_cpu")
+            want = oracle(head.numpy())
+            np.testing.assert_allclose(got[:sample], want, rtol=1e-4, atol=1e-5)
+            cpu_ms = timed(lambda: oracle(head.numpy()), 1, 3)["median_ms"]
+            oracle.close()
+            sample_bytes = sample * width * 4 + (sample * 4 if kind == "logsumexp" else sample * width * 4)
+            entry["cpu_oracle"] = {"rows": sample, "ms": cpu_ms, "gbs": round(sample_bytes / (cpu_ms * 1e-3) / 1e9, 3)}
+        results.append(entry)
+        log(f"{kind} [{rows},{width}] {ms * 1e3:.1f} us, {entry['roofline']['achieved']} GB/s")
+        shutil.rmtree(work / f"{kind}_{rows}_{width}", ignore_errors=True)
+    return results
+
+
+# ------------------------------------------------------------------------------------------------- C1
+def bench_c1(work: Path, cpu: bool) -> dict:
+    import numpy as np
+    import torch
+
+    import chroma_amd
+    from chroma_amd.models.blocks import mlp_block, mlp_inputs
+    from oracle import compile_cpu
+
+    module, (x,) = mlp_block(), mlp_inputs()
+    exported = torch.export.export(module, (x,))
+    program = chroma_amd.compile(exported, work / "c1")
+    array = x.numpy()
+    got = program(array)
+    program.native.upload([array])
+    ms = device_ms(program, 50)
+    result = {"workload": "MLP block x[8,1024] fp32 seed 0: RMSNorm, SiLU(gate)*up (1024->4096), down (4096->1024), residual; weights N(0,0.02) seed 0",
+              "device_ms": round(ms, 4), "launches": program.stats["launches"], "algorithmic_bytes": C1_BYTES, "flops": C1_FLOPS,
+              "roofline": roofline(C1_BYTES, ms), "host_to_host": timed(lambda: program(array), 10, 100)}
+    if cpu:
+        oracle = compile_cpu(exported, work / "c1_cpu")
+        np.testing.assert_allclose(got, oracle(array), rtol=1e-4, atol=1e-5)
+        result["cpu_oracle"] = timed(lambda: oracle(array), 2, 20)
+        oracle.close()
+    program.close()
+    return result
+
+
+# ------------------------------------------------------------------------------------------------- C3
+def bench_dev(work: Path, cpu: bool) -> dict:
+    """C3: the dev model's 8-token fp32 forward, host arrays in and out, interleaved with the oracle."""
     import numpy as np
     import torch
 
@@ -167,40 +328,44 @@ def bench_dev(work: Path, runs: int) -> dict:
     from oracle import compile_cpu
 
     model = make_dev_model(0)
-    tokens = torch.randint(0, 201088, (8,), generator=torch.Generator().manual_seed(0))
+    tokens = torch.randint(0, VOCAB, (8,), generator=torch.Generator().manual_seed(0))
     exported = torch.export.export(model, (tokens,))
     log("compiling the dev model for hip and the oracle")
     program = chroma_amd.compile(exported, work / "dev")
-    oracle = compile_cpu(exported, work / "dev_cpu")
+    oracle = compile_cpu(exported, work / "dev_cpu") if cpu else None
     array = tokens.numpy()
-    got, want = program(array), oracle(array)
-    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-5)
-    argmax_equal = bool((got.argmax(-1) == want.argmax(-1)).all())
+    got = program(array)
+    result = {"workload": "dev MoE model (12 layers, 59,079,408 params, vocab 201088), 8-token fp32 forward, batch 1, tokens ~U[0,201088) seed 0",
+              "weights_sha256": weights_digest(model), "launches": program.stats["launches"]}
+    if oracle is not None:
+        want = oracle(array)
+        np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-5)
+        result["argmax_equal"] = bool((got.argmax(-1) == want.argmax(-1)).all())
     out = program(array)  # the reference's out= method reuses an earlier result (scripts/benchmark.py:207-208)
-    pageable = np.empty_like(got)
-    result = {
-        "workload": "dev MoE model (12 layers, 59,079,408 params, vocab 201088), 8-token fp32 forward, batch 1, tokens ~U[0,201088) seed 0",
-        "weights_sha256": weights_digest(model),
-        "hip_fresh": timed(lambda: program(array), 10, runs),
-        "hip_reuse": timed(lambda: program(array, out=out), 10, runs),
-        "hip_reuse_pageable_out": timed(lambda: program(array, out=pageable), 10, runs),
-        "cpu_oracle": timed(lambda: oracle(array), 2, max(5, runs // 10)),
-        "argmax_equal": argmax_equal,
-        "launches": program.stats["launches"],
-    }
-    native = program.native
-    native.upload([array])
-    native.execute(5)
-    result["hip_device_only_ms"] = round(native.execute(runs, timed=True) / runs, 4)
+    calls = {"hip_fresh": lambda: program(array), "hip_reuse": lambda: program(array, out=out)}
+    if oracle is not None:
+        calls["cpu_oracle"] = lambda: oracle(array)
+    timings = interleaved(calls, warmup=10, runs=100, rounds=2)
+    result.update(timings)
+    result["method"] = "2 rounds x (10 warmup + 100 timed) of seeded interleaved calls, pooled (scripts/benchmark.py:221-230)"
+    program.native.upload([array])
+    ms = device_ms(program, 100, warmup=5)
+    result["hip_device_ms"] = round(ms, 4)
+    result["roofline"] = roofline(C3_BYTES, ms)
+    result["algorithmic_bytes"] = C3_BYTES
     program.close()
-    oracle.close()
+    if oracle is not None:
+        oracle.close()
     return result
 
 
-def bench_decode(work: Path, steps: int) -> dict:
-    """C4: dev model KV-cached decode at a 256-position cache through ``Decoder`` (host mask and cache
-    work included), plus the padded uncached 256-token graph, with the oracle's times."""
+# ------------------------------------------------------------------------------------------------- C4
+def bench_decode(work: Path, steps: int, cpu: bool) -> dict:
+    """C4: the dev model's KV-cached decode at a 256-position cache through ``Decoder`` (host mask and cache
+    work included), the padded uncached 256-token graph and a 32-token prefill through the 256-step graph,
+    each beside the oracle; plus the decode step's device-only time and roofline."""
     import numpy as np
+    import torch
 
     import chroma_amd
     from chroma_amd import Decoder
@@ -212,22 +377,36 @@ def bench_decode(work: Path, steps: int) -> dict:
     graphs = {"prefill": export_cached(model, 256, 256), "decode": export_cached(model, 256, 1), "full": export_uncached(model, 256)}
     log("compiling the decode graphs for hip and the oracle")
     hip = {name: chroma_amd.compile(graph, work / f"hip_{name}") for name, graph in graphs.items()}
-    cpu = {name: compile_cpu(graph, work / f"cpu_{name}") for name, graph in graphs.items()}
-    tokens = ((np.arange(8 + steps, dtype=np.int64) * 7919 + 17) % 201088).astype(np.int64)
-    results = {}
-    for name, programs in (("hip", hip), ("cpu_oracle", cpu)):
+    cpu_programs = {name: compile_cpu(graph, work / f"cpu_{name}") for name, graph in graphs.items()} if cpu else {}
+    tokens = torch.randint(0, VOCAB, (32 + steps,), generator=torch.Generator().manual_seed(0)).numpy()
+    results = {"workload": "dev model, Decoder(export_cached(m,256,256), export_cached(m,256,1)); prefill 8 tokens ~U[0,201088) seed 0, "
+               f"then {steps} single-token steps; 32-token prefill through the 256-step graph; padded export_uncached(m,256)"}
+    padded = np.zeros(256, dtype=np.int64)
+    padded[:16] = tokens[:16]
+    last = np.array([15], dtype=np.int64)
+    for name, programs in (("hip", hip), ("cpu_oracle", cpu_programs)):
+        if not programs:
+            continue
         decoder = Decoder(programs["prefill"], programs["decode"])
-        decoder.append(tokens[:8])
-        samples = []
-        count = steps if name == "hip" else min(steps, 8)
-        for i in range(8, 8 + count):
+        count = steps if name == "hip" else min(steps, 32)
+        rounds, samples = (3 if name == "hip" else 1), []
+        for _ in range(rounds):
+            decoder.reset()
+            decoder.append(tokens[:8])
+            for i in range(8, 8 + count):
+                start = time.perf_counter()
+                decoder.append(tokens[i : i + 1])
+                samples.append((time.perf_counter() - start) * 1e3)
+        prefill = []
+        for _ in range(10 if name == "hip" else 3):
+            decoder.reset()
             start = time.perf_counter()
-            decoder.append(tokens[i : i + 1])
-            samples.append((time.perf_counter() - start) * 1e3)
-        greedy = None
+            decoder.append(tokens[:32])
+            prefill.append((time.perf_counter() - start) * 1e3)
+        entry = {"decode_step": {"median_ms": round(statistics.median(samples), 4), "steps": len(samples)},
+                 "prefill_32": {"median_ms": round(statistics.median(prefill), 4), "runs": len(prefill)},
+                 "uncached_256": timed(lambda: programs["full"](padded, last), 2, 10 if name == "hip" else 3)}
         if name == "hip":
-            # the same steps through Decoder.greedy: the logits stay on the device and a selection program
-            # returns the chosen id (8 bytes down instead of the 804 KB row)
             decoder.reset()
             decoder.append(tokens[:8])
             decoder.greedy(tokens[8:9])  # compiles the selection program
@@ -236,66 +415,71 @@ def bench_decode(work: Path, steps: int) -> dict:
                 start = time.perf_counter()
                 decoder.greedy(tokens[i : i + 1])
                 greedy.append((time.perf_counter() - start) * 1e3)
-            decoder.close()
-        padded = np.zeros(256, dtype=np.int64)
-        padded[:16] = tokens[:16]
-        last = np.array([15], dtype=np.int64)
-        full = programs["full"]
-        results[name] = {
-            "decode_step": {"median_ms": round(statistics.median(samples), 4), "steps": count},
-            "uncached_256": timed(lambda: full(padded, last), 2, 10 if name == "hip" else 3),
-            "uncached_logits": full(padded, last),
-        }
-        if greedy:
-            results[name]["decode_step_greedy"] = {"median_ms": round(statistics.median(greedy), 4), "steps": len(greedy)}
-    np.testing.assert_allclose(results["hip"]["uncached_logits"], results["cpu_oracle"]["uncached_logits"], rtol=1e-4, atol=1e-5)
-    for entry in results.values():
-        entry.pop("uncached_logits")
-    for program in (*hip.values(), *cpu.values()):
+            entry["decode_step_greedy"] = {"median_ms": round(statistics.median(greedy), 4), "steps": len(greedy)}
+            # device-only decode step: the decode plan on what its staging holds after the last step
+            ms = device_ms(programs["decode"], 100, warmup=5)
+            entry["decode_step_device_ms"] = round(ms, 4)
+            entry["roofline"] = roofline(C4_BYTES, ms)
+            entry["algorithmic_bytes_per_step"] = C4_BYTES
+        decoder.close()
+        results[name] = entry
+    if cpu:
+        np.testing.assert_allclose(hip["full"](padded, last), cpu_programs["full"](padded, last), rtol=1e-4, atol=1e-5)
+    for program in (*hip.values(), *cpu_programs.values()):
         program.close()
-    results["workload"] = "dev model, Decoder(export_cached(m,256,256), export_cached(m,256,1)), prefill 8 tokens then single-token steps; padded export_uncached(m,256)"
     return results
 
 
+# ------------------------------------------------------------------------------------------------- C5
 C5_CONTEXT, C5_PREFILL = 4096, 2048
 
 
-def c5_flops(config, tokens: int, context: int) -> dict:
-    """Multiply-add work (2 flops each) of one pass of ``export_cached(m, context, tokens)``, per kind of
-    product, as the graph computes it (every score over the whole padded cache; one row unembedded)."""
+def c5_live_flops(config, tokens: int) -> dict:
+    """Multiply-add work (2 flops each) of one fresh ``export_cached(m, context, tokens)`` prefill as it
+    must be performed: the projections, the four selected experts per token, the attention over the query
+    -key pairs the masks leave live (causal on full layers, the last ``sliding_window`` keys on window
+    layers; cached keys are all masked at a fresh prefill) and one unembedded row."""
     d, hd, heads, kv = config.hidden_size, config.head_dim, config.num_attention_heads, config.num_key_value_heads
     inter, top, layers = config.intermediate_size, config.experts_per_token, config.num_hidden_layers
-    keys = context + tokens
-    per_layer = {
-        "qkv": 2 * tokens * d * hd * (heads + 2 * kv),
-        "out": 2 * tokens * hd * heads * d,
-        "router": 2 * tokens * d * config.num_experts,
-        "experts_up": 2 * tokens * top * 2 * inter * d,
-        "experts_down": 2 * tokens * top * d * inter,
-        "scores": 2 * heads * tokens * keys * hd,
-        "attend": 2 * heads * tokens * keys * hd,
+    window = config.sliding_window
+    full_pairs = tokens * (tokens + 1) // 2
+    window_pairs = sum(min(t + 1, window) for t in range(tokens))
+    flops = {
+        "qkv": 2 * tokens * d * hd * (heads + 2 * kv) * layers,
+        "out": 2 * tokens * hd * heads * d * layers,
+        "router": 2 * tokens * d * config.num_experts * layers,
+        "experts_up": 2 * tokens * top * 2 * inter * d * layers,
+        "experts_down": 2 * tokens * top * d * inter * layers,
+        # QK^T and PV: 4 * head_dim flops per live pair and query head; even layers use the window
+        "attention": 4 * hd * heads * (full_pairs * (layers // 2) + window_pairs * (layers - layers // 2)),
+        "unembedding": 2 * d * config.vocab_size,
     }
-    flops = {name: value * layers for name, value in per_layer.items()}
-    flops["unembedding"] = 2 * d * config.vocab_size
     flops["total"] = sum(flops.values())
     return flops
 
 
-def c5_decode_bytes(config, context: int) -> int:
-    """HBM bytes one decode step must read at least: every dense weight, the four selected experts of
-    every layer, the K/V cache, the unembedding, in bfloat16 (norm scales and biases ignored)."""
+def c5_decode_bytes(config, cached: int) -> int:
+    """HBM bytes one decode step must read with ``cached`` valid cache positions: every dense weight, the
+    four selected experts of every layer (bf16 weights and biases), the unembedding, and the live K/V rows
+    (all cached positions on full layers, the window on window layers)."""
     d, hd, heads, kv = config.hidden_size, config.head_dim, config.num_attention_heads, config.num_key_value_heads
-    inter, top = config.intermediate_size, config.experts_per_token
-    per_layer = d * hd * (heads + 2 * kv) + hd * heads * d + d * config.num_experts + top * (2 * inter * d + d * inter)
-    cache = 2 * context * kv * hd
-    return 2 * (config.num_hidden_layers * (per_layer + cache) + d * config.vocab_size)
+    inter, top, layers = config.intermediate_size, config.experts_per_token, config.num_hidden_layers
+    dense = d * hd * (heads + 2 * kv) + hd * (heads + 2 * kv) + hd * heads * d + d + d * config.num_experts + config.num_experts + 2 * d + heads
+    experts = top * (2 * inter * d + 2 * inter + d * inter + d)
+    full_kv = 2 * min(cached + 1, C5_CONTEXT) * kv * hd
+    window_kv = 2 * min(cached + 1, config.sliding_window) * kv * hd
+    kv_bytes = full_kv * (layers // 2) + window_kv * (layers - layers // 2)
+    return 2 * (layers * (dense + experts) + kv_bytes + d * config.vocab_size + d)
 
 
-def bench_c5(work: Path, steps: int) -> dict:
+def bench_c5(work: Path, steps: int, cpu: bool) -> dict:
     """C5: the GPT-OSS-20B-shaped bfloat16 model (24 layers, hidden 2880, 64/8 heads of 64, 32 experts
-    top-4, vocabulary 201,088; weights N(0, 0.02) seed 2 drawn on the GPU), a 2048-token prefill through
-    ``export_cached(m, 4096, 2048)`` and single-token steps through ``export_cached(m, 4096, 1)``. Device
-    times run on device-resident inputs; the ``Decoder`` times are end to end (host cache and masks)."""
+    top-4, vocabulary 201,088; weights N(0, 0.02) seed 2 drawn on the GPU). A 2048-token prefill through
+    ``export_cached(m, 4096, 2048)`` (after one untimed prefill and a reset), a second prefill chunk that
+    fills the 4096-position cache, then single-token steps through ``export_cached(m, 4096, 1)`` with the
+    cache full. Device times run the plans on what their staging holds; ``Decoder`` times are end to end."""
+    import shutil
+
     import numpy as np
     import torch
 
@@ -315,43 +499,91 @@ def bench_c5(work: Path, steps: int) -> dict:
         programs[name] = chroma_amd.compile(export_cached(model, C5_CONTEXT, steps_), work / f"c5_{name}")
         log(f"C5 {name} compiled and loaded in {time.perf_counter() - start:.1f} s ({programs[name].stats['launches']} launches)")
     del model
-    tokens = torch.randint(0, 201088, (C5_PREFILL + steps,), generator=torch.Generator().manual_seed(2)).numpy()
-    result = {"workload": "GPT-OSS-20B-shaped bf16 MoE (24 layers, hidden 2880, 64/8 heads of 64, 32 experts top-4, vocab 201088), "
-              "weights N(0,0.02) seed 2; 2048-token prefill (timed after one untimed prefill and a reset) then decode, cache 4096 positions",
-              "weight_bytes": programs["prefill"].stats["weight_bytes"]}
-    flops = c5_flops(gpt_oss_20b, C5_PREFILL, C5_CONTEXT)
+    tokens = torch.randint(0, VOCAB, (2 * C5_PREFILL + steps,), generator=torch.Generator().manual_seed(2)).numpy()
+    result = {"workload": "GPT-OSS-20B-shaped bf16 MoE (24 layers, hidden 2880, 64/8 heads of 64, 32 experts top-4, vocab 201088, "
+              "128-token windows on even layers), weights N(0,0.02) seed 2; 2048-token prefill from an empty 4096-position cache, "
+              "then decode with all 4096 positions cached", "weight_bytes": programs["prefill"].stats["weight_bytes"],
+              "launches": {name: program.stats["launches"] for name, program in programs.items()}}
     with Decoder(programs["prefill"], programs["decode"], sliding_window=gpt_oss_20b.sliding_window) as decoder:
-        # one untimed prefill first: the host staging's first touch and the decoder's mask-band cache
-        decoder.append(tokens[:C5_PREFILL])
+        decoder.append(tokens[:C5_PREFILL])  # host staging's first touch and the mask-band cache
         decoder.reset()
         start = time.perf_counter()
         logits = decoder.append(tokens[:C5_PREFILL])
         result["prefill_decoder_ms"] = round((time.perf_counter() - start) * 1e3, 3)
         if not np.isfinite((logits.view(np.uint16).astype(np.uint32) << 16).view(np.float32)).all():
             raise RuntimeError("C5 prefill logits are not finite")
+        prefill_ms = device_ms(programs["prefill"], 5, warmup=1)
+        decoder.append(tokens[C5_PREFILL : 2 * C5_PREFILL])  # fills the cache: positions 0..4095
         samples = []
-        for i in range(C5_PREFILL, C5_PREFILL + steps):
+        for i in range(2 * C5_PREFILL, 2 * C5_PREFILL + steps):
             start = time.perf_counter()
             decoder.append(tokens[i : i + 1])
             samples.append((time.perf_counter() - start) * 1e3)
         result["decode_decoder_ms"] = round(statistics.median(samples), 3)
         result["decode_cache_on_device"] = decoder.stats["cache_on_device"]
-        # Device-only times: the plans re-run on what their staging regions hold after the Decoder calls.
-        for name, runs in (("prefill", 5), ("decode", 20)):
-            native = programs[name].native
-            native.execute(2)
-            device_ms = native.execute(runs, timed=True) / runs
-            result[f"{name}_device_ms"] = round(device_ms, 4)
-    result["prefill_flops"] = flops["total"]
-    result["prefill_tflops"] = round(flops["total"] / (result["prefill_device_ms"] * 1e-3) / 1e12, 1)
-    result["prefill_mfma_frac"] = round(result["prefill_tflops"] / BF16_MFMA_PEAK_TFLOPS, 4)
+        decode_ms = device_ms(programs["decode"], 20, warmup=2)
+    flops = c5_live_flops(gpt_oss_20b, C5_PREFILL)
     decode_bytes = c5_decode_bytes(gpt_oss_20b, C5_CONTEXT)
-    result["decode_algorithmic_bytes"] = decode_bytes
-    result["decode_gbs"] = round(decode_bytes / (result["decode_device_ms"] * 1e-3) / 1e9, 1)
-    result["decode_hbm_frac"] = round(result["decode_gbs"] / HBM_PEAK_GBS, 4)
+    result.update({
+        "prefill_device_ms": round(prefill_ms, 3),
+        "prefill_live_flops": flops,
+        "prefill_roofline": roofline(flops["total"], prefill_ms, bound="mfma"),
+        "decode_device_ms": round(decode_ms, 4),
+        "decode_algorithmic_bytes": decode_bytes,
+        "decode_roofline": roofline(decode_bytes, decode_ms),
+    })
+    for name, program in programs.items():
+        program.close()
+        shutil.rmtree(work / f"c5_{name}", ignore_errors=True)
+    if cpu:
+        result["reduced_slice"] = c5_slice(work)
     return result
 
 
+def c5_slice(work: Path) -> dict:
+    """C5 at full width on a reduced slice, hip beside the oracle: 2 layers (one 128-token window layer
+    [window 16 at this context], one full layer), all 32 experts, a 64-position cache, a 32-token prefill
+    chunk and 4 single-token steps; parity of every call's logits and the oracle's time per call."""
+    import numpy as np
+    import torch
+
+    import chroma_amd
+    from chroma_amd import Decoder
+    from chroma_amd.models.cached import export_cached
+    from chroma_amd.models.dev import make_gpt_oss_20b
+    from oracle import compile_cpu
+
+    def widen(a):
+        return (a.view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+    model = make_gpt_oss_20b(2, num_hidden_layers=2, num_experts=32)
+    graphs = [export_cached(model, 64, 32), export_cached(model, 64, 1)]
+    hip = [chroma_amd.compile(g, work / f"c5s_hip{i}") for i, g in enumerate(graphs)]
+    cpu = [compile_cpu(g, work / f"c5s_cpu{i}") for i, g in enumerate(graphs)]
+    tokens = torch.randint(0, VOCAB, (36,), generator=torch.Generator().manual_seed(2)).numpy()
+    times = {"hip": [], "cpu_oracle": []}
+    worst = {"max_abs": 0.0, "rel_norm": 0.0, "argmax_equal": True}
+    with Decoder(*hip, sliding_window=16) as decoder, Decoder(*cpu, sliding_window=16) as reference:
+        for start, end in ((0, 32), *((i, i + 1) for i in range(32, 36))):
+            t0 = time.perf_counter()
+            got = widen(decoder.append(tokens[start:end]))
+            t1 = time.perf_counter()
+            want = widen(reference.append(tokens[start:end]))
+            t2 = time.perf_counter()
+            times["hip"].append((t1 - t0) * 1e3)
+            times["cpu_oracle"].append((t2 - t1) * 1e3)
+            worst["max_abs"] = max(worst["max_abs"], float(np.abs(got - want).max()))
+            worst["rel_norm"] = max(worst["rel_norm"], float(np.linalg.norm(got - want) / np.linalg.norm(want)))
+            worst["argmax_equal"] &= bool(got.argmax() == want.argmax())
+    for program in (*hip, *cpu):
+        program.close()
+    return {"slice": "2 layers (window, full), all 32 experts, hidden 2880, 64/8 heads, vocab 201088, cache 64, 32-token prefill + 4 steps",
+            "hip_prefill_ms": round(times["hip"][0], 3), "cpu_prefill_ms": round(times["cpu_oracle"][0], 3),
+            "hip_step_ms": round(statistics.median(times["hip"][1:]), 3), "cpu_step_ms": round(statistics.median(times["cpu_oracle"][1:]), 3),
+            "parity": {k: (round(v, 5) if isinstance(v, float) else v) for k, v in worst.items()}}
+
+
+# --------------------------------------------------------------------------------------------- counters
 def counters(work: Path) -> None:
     """For rocprofv3 --pmc: three launches of the C2 kernel and of a plain copy kernel of known size
     (``x * 1.0`` over the same [16384, 8192] fp32 input: 512 MiB read, 512 MiB written), which calibrates
@@ -359,11 +591,12 @@ def counters(work: Path) -> None:
     import torch
 
     import chroma_amd
+    from chroma_amd.models.blocks import BandwidthGraph, Copy, bandwidth_inputs
 
-    x, y = c2_inputs()
+    x, y = bandwidth_inputs()
     programs = [
-        (chroma_amd.compile(torch.export.export(c2_module(), (x, y)), work / "c2"), [x.numpy(), y.numpy()]),
-        (chroma_amd.compile(torch.export.export(_copy_module(), (x,)), work / "copy"), [x.numpy()]),
+        (chroma_amd.compile(torch.export.export(BandwidthGraph(), (x, y)), work / "c2"), [x.numpy(), y.numpy()]),
+        (chroma_amd.compile(torch.export.export(Copy(), (x,)), work / "copy"), [x.numpy()]),
     ]
     for program, arrays in programs:
         program.native.upload(arrays)
@@ -372,14 +605,24 @@ def counters(work: Path) -> None:
         program.close()
 
 
-def _copy_module():
-    import torch
+def run_leg(name: str, leg, work: Path):
+    """One secondary measurement in a directory of its own, removed afterwards (the C5 artifacts alone hold
+    42 GB of weights); a failure is recorded in the line instead of losing the headline."""
+    import shutil
+    import traceback
 
-    class Copy(torch.nn.Module):
-        def forward(self, x):
-            return x * 1.0
-
-    return Copy()
+    directory = work / name
+    directory.mkdir()
+    start = time.perf_counter()
+    try:
+        result = leg(directory)
+        log(f"{name} done in {time.perf_counter() - start:.1f} s")
+        return result
+    except Exception as error:  # noqa: BLE001 - reported in the JSON line
+        traceback.print_exc()
+        return {"error": f"{type(error).__name__}: {error}"}
+    finally:
+        shutil.rmtree(directory, ignore_errors=True)
 
 
 def main() -> None:
@@ -387,23 +630,26 @@ def main() -> None:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--no-extras", action="store_true", help="skip the dev-model forward and decode measurements")
-    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    parser.add_argument("--no-extras", action="store_true", help="only the C2 headline (and its CPU baseline)")
+    parser.add_argument("--no-cpu", action="store_true", help="skip every oracle (CPU) measurement")
+    parser.add_argument("--no-c5", action="store_true", help="skip the GPT-OSS-20B-shaped model (about two minutes: 42 GB of weights)")
     parser.add_argument("--counters", action="store_true", help="only run the C2 and copy kernels (for rocprofv3 --pmc)")
-    parser.add_argument("--c5", action="store_true", help="also measure the GPT-OSS-20B-shaped bf16 model (minutes: 42 GB of weights)")
-    parser.add_argument("--c5-only", action="store_true", help="only measure the GPT-OSS-20B-shaped model")
+    parser.add_argument("--only", choices=["c1", "rows", "dev", "decode", "c5"], help="measure one leg and print it")
     args = parser.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the hip backend is single-device (every GPU box here has one GPU)", file=sys.stderr)
         sys.exit(2)
+    cpu = not args.no_cpu
 
     with tempfile.TemporaryDirectory(prefix="chroma-bench-") as directory:
         work = Path(directory)
         if args.counters:
             counters(work)
             return
-        if args.c5_only:
-            print(json.dumps({"c5": bench_c5(work, 16)}), flush=True)
+        if args.only:
+            legs = {"c1": lambda: bench_c1(work, cpu), "rows": lambda: bench_rows(work, cpu), "dev": lambda: bench_dev(work, cpu),
+                    "decode": lambda: bench_decode(work, 32, cpu), "c5": lambda: bench_c5(work, 16, cpu)}
+            print(json.dumps({args.only: legs[args.only]()}), flush=True)
             return
         c2 = bench_c2(args, work)
         log(f"C2 {c2['value']:.1f} GB/s wall, kernel {c2['kernel_ms']:.4f} ms ({c2['roofline']['achieved']:.1f} GB/s)")
@@ -424,17 +670,19 @@ def main() -> None:
                 "workload": "C2 bandwidth graph: softmax(tanh(x*0.5+y)*sigmoid(y)-exp(clamp(x,-8,8))*1e-3, -1), fp32 x,y~U(-4,4) [16384,8192] seed 1, inputs resident in HBM",
                 "algorithmic_bytes_per_step": C2_BYTES,
                 "launches_per_step": c2["stats"]["launches"],
+                "end_to_end_ms_with_pcie": c2["end_to_end_ms"]["median_ms"],
             },
             "roofline": c2["roofline"],
-            "cpu_baseline": None if args.no_cpu else cpu_c2(work),
+            "cpu_baseline": cpu_c2(work) if cpu else None,
         }
+        line["host"] = dict(host_info(), gpu=c2["device"])
         if not args.no_extras:
-            line["dev_forward"] = bench_dev(work, 100)
-            log(f"dev forward {line['dev_forward']['hip_fresh']['median_ms']} ms (oracle {line['dev_forward']['cpu_oracle']['median_ms']} ms)")
-            line["decode"] = bench_decode(work, 32)
-            log(f"decode step {line['decode']['hip']['decode_step']['median_ms']} ms")
-        if args.c5:
-            line["c5"] = bench_c5(work, 16)
+            legs = [("hbm_copy", lambda d: bench_copy(d)), ("rows", lambda d: bench_rows(d, cpu)), ("c1", lambda d: bench_c1(d, cpu)),
+                    ("dev_forward", lambda d: bench_dev(d, cpu)), ("decode", lambda d: bench_decode(d, 32, cpu))]
+            if not args.no_c5:
+                legs.append(("c5", lambda d: bench_c5(d, 16, cpu)))
+            for name, leg in legs:
+                line[name] = run_leg(name, leg, work)
         print(json.dumps(line), flush=True)
 
 

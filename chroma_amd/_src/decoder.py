@@ -37,6 +37,8 @@ from chroma_amd._src import host
 from chroma_amd._src.dtypes import BFLOAT16, numpy_dtype
 from chroma_amd._src.program import NativeModel, Program
 
+SELECT_MAX_K = 1024  # largest k the runtime's row selection takes (chroma_hip_rows_topk)
+
 
 @dataclass(frozen=True)
 class CacheState:
@@ -306,7 +308,7 @@ class Decoder:
 
     def append(self, tokens: Any) -> np.ndarray:
         """Consume new token ids and return the logits [1, vocab] after the last one."""
-        logits, _ = self._consume(tokens, keep_logits=False)
+        logits, _, _ = self._consume(tokens, keep_logits=False)
         return logits
 
     def append_top(self, tokens: Any, k: int = 1, *, allowed: Any = None) -> Tuple[np.ndarray, np.ndarray]:
@@ -314,11 +316,12 @@ class Decoder:
         with their token ids, largest first: NaN outranks every number and ties go to the lower id (the
         reference GPU backend's top-k rule). ``allowed`` (token ids) restricts the choice to those ids.
 
-        With hip programs the logits never leave the device: a small selection program (the top-k kernel,
-        after a gather of the allowed ids) reads the step's logits by a device-to-device copy, and only
-        the ``k`` values and ids are downloaded instead of the vocabulary row. Other programs select on
-        the host by the same rule. (An addition to the reference API: its chat script samples from the
-        downloaded row, scripts/chat.py:82-98.)"""
+        With hip programs the logits never leave the device: the runtime's row selection runs on the step's
+        own stream right after it, under the step's one synchronization, and only the ``k`` values and ids
+        come back instead of the vocabulary row (k up to 1024). With ``allowed``, a small selection
+        program (a gather of the allowed ids, then the top-k kernel) reads the step's logits by a
+        device-to-device copy instead. Other programs select on the host by the same rule. (An addition to
+        the reference API: its chat script samples from the downloaded row, scripts/chat.py:82-98.)"""
         if not isinstance(k, (int, np.integer)) or k < 1:
             raise ValueError(f"k must be a positive integer, got {k!r}")
         ids = None
@@ -333,7 +336,10 @@ class Decoder:
             raise ValueError(f"k = {k} exceeds the number of candidate tokens")
         device = self._on_device and isinstance(self._models[1].native, NativeModel)
         with self._lock:  # the step's device logits stay this step's until the selection has read them
-            logits, which = self._consume(tokens, keep_logits=device)
+            if device and ids is None and k <= SELECT_MAX_K:
+                _, _, (values, picks) = self._consume(tokens, keep_logits=True, top=int(k))
+                return values[0].copy(), picks[0].copy()
+            logits, which, _ = self._consume(tokens, keep_logits=device)
             if not device:
                 return _select_host(logits[0], int(k), ids)
             selector = self._selector(int(k), None if ids is None else len(ids))
@@ -378,9 +384,11 @@ class Decoder:
             self._selectors[key] = program
         return program
 
-    def _consume(self, tokens: Any, *, keep_logits: bool) -> Tuple[Optional[np.ndarray], int]:
+    def _consume(self, tokens: Any, *, keep_logits: bool, top: Optional[int] = None) -> Tuple[Optional[np.ndarray], int, Any]:
         """Run the steps for ``tokens``; return the last step's logits (None when ``keep_logits`` leaves
-        them in the device output of the program that ran it) and that program's index."""
+        them in the device output of the program that ran it), that program's index, and, when ``top`` is
+        given (device mode), the (values, ids) of the last step's ``top`` largest logits selected on the
+        device after it."""
         ids = np.asarray(tokens)
         if ids.ndim != 1 or not len(ids):
             raise ValueError(f"append wants a nonempty 1-D sequence of token IDs, got shape {ids.shape}")
@@ -392,6 +400,7 @@ class Decoder:
                 raise RuntimeError("Decoder is closed")
             offset = 0
             logits = None
+            selection = None
             which = 1
             while offset < len(ids):
                 remaining = len(ids) - offset
@@ -421,7 +430,10 @@ class Decoder:
                 slots[rows] = times[:count]
                 if self._on_device:
                     self._device_cache(which, args)
-                    self._models[which].run_resident(args, [logits, *updates])
+                    if top is not None and offset + count == len(ids):
+                        selection = self._models[which].run_top_resident(args, [logits, *updates], 0, top)
+                    else:
+                        self._models[which].run_resident(args, [logits, *updates])
                     with _interrupts_deferred():
                         self._device_commit(which, state.position, count, steps)
                         self._commit(CacheState(None, None, slots, state.position + count, which))
@@ -432,7 +444,7 @@ class Decoder:
                     values[:, rows] = updates[1][:, :count]
                     self._commit(CacheState(keys, values, slots, state.position + count))
                 offset += count
-            return logits, which
+            return logits, which, selection
 
     def close(self) -> None:
         with self._lock:

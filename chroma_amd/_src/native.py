@@ -11,6 +11,7 @@ import ctypes
 import os
 import shlex
 import subprocess
+import tempfile
 import threading
 from pathlib import Path
 
@@ -18,38 +19,41 @@ PACKAGE = Path(__file__).resolve().parents[1]
 REPO = PACKAGE.parent
 LIBRARY = PACKAGE / "lib" / "libchroma_hip.so"
 RUNTIME_SOURCE = PACKAGE / "csrc" / "runtime.cpp"
+SELECT_SOURCE = PACKAGE / "csrc" / "select.hip"
 DEVICE_INCLUDE = PACKAGE / "csrc" / "include"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 
 OK, INDEX_ERROR, RUNTIME_ERROR = 0, 1, 2
+FLOAT32, BFLOAT16 = 0, 1  # CHROMA_HIP_FLOAT32 / CHROMA_HIP_BFLOAT16
 
 _lock = threading.Lock()
 _library = None
 
 
 def build_runtime(output: Path = LIBRARY) -> Path:
-    """Compile the host runtime (no device code) against the HIP runtime library."""
+    """Build the runtime library: the host runtime (``runtime.cpp``, g++) and the row selection kernels
+    (``select.hip``, hipcc for gfx950 with the same device flags as generated programs), linked by hipcc
+    against the HIP runtime."""
+    from chroma_amd._src.build import DEVICE_FLAGS, architecture
+
     output.parent.mkdir(parents=True, exist_ok=True)
     temporary = output.with_suffix(".so.tmp")
-    command = [
-        *shlex.split(os.environ.get("CXX", "g++")),
-        "-std=c++17",
-        "-O2",
-        "-shared",
-        "-fPIC",
-        "-fvisibility=hidden",
-        "-D__HIP_PLATFORM_AMD__",
-        f"-I{ROCM / 'include'}",
-        str(RUNTIME_SOURCE),
-        "-o",
-        str(temporary),
-        f"-L{ROCM / 'lib'}",
-        f"-Wl,-rpath,{ROCM / 'lib'}",
-        "-lamdhip64",
-    ]
-    result = subprocess.run(command, capture_output=True, text=True, check=False)
-    if result.returncode:
-        raise RuntimeError(f"Building the hip runtime failed:\n{result.stderr[-4000:]}")
+    hipcc = shlex.split(os.environ.get("HIPCC", str(ROCM / "bin" / "hipcc")))
+    device_flags = [flag for flag in DEVICE_FLAGS if flag != "--genco"]
+    with tempfile.TemporaryDirectory(prefix="chroma-runtime-") as work:
+        host_object, device_object = Path(work) / "runtime.o", Path(work) / "select.o"
+        commands = [
+            [*shlex.split(os.environ.get("CXX", "g++")), "-std=c++17", "-O2", "-c", "-fPIC", "-fvisibility=hidden", "-D__HIP_PLATFORM_AMD__",
+             f"-I{ROCM / 'include'}", str(RUNTIME_SOURCE), "-o", str(host_object)],
+            [*hipcc, f"--offload-arch={architecture()}", *device_flags, "-c", "-fPIC", "-fvisibility=hidden", f"-I{DEVICE_INCLUDE}",
+             str(SELECT_SOURCE), "-o", str(device_object)],
+            [*hipcc, f"--offload-arch={architecture()}", "-shared", "-fPIC", str(host_object), str(device_object), "-o", str(temporary),
+             f"-L{ROCM / 'lib'}", f"-Wl,-rpath,{ROCM / 'lib'}", "-lamdhip64"],
+        ]
+        for command in commands:
+            result = subprocess.run(command, capture_output=True, text=True, check=False)
+            if result.returncode:
+                raise RuntimeError(f"Building the hip runtime failed:\n{' '.join(command)}\n{result.stderr[-4000:]}")
     os.replace(temporary, output)
     return output
 
@@ -90,6 +94,12 @@ def library() -> ctypes.CDLL:
         lib.chroma_hip_host_alloc.argtypes = [c.c_size_t, c.POINTER(c.c_void_p), c.c_char_p, c.c_size_t]
         lib.chroma_hip_host_free.argtypes = [c.c_void_p]
         lib.chroma_hip_host_free.restype = None
+        lib.chroma_hip_rows_topk_workspace.argtypes = [c.c_size_t, c.c_size_t, c.c_int]
+        lib.chroma_hip_rows_topk_workspace.restype = c.c_size_t
+        lib.chroma_hip_rows_topk.argtypes = [c.c_void_p, c.c_int, c.c_size_t, c.c_size_t, c.c_int, c.c_int, c.c_void_p, c.c_void_p,
+                                             c.c_void_p, c.c_size_t, c.c_void_p, c.c_char_p, c.c_size_t]
+        lib.chroma_hip_run_top.argtypes = [c.c_void_p, c.c_void_p, c.c_void_p, c.c_int, c.c_int, c.c_size_t, c.c_size_t, c.c_int,
+                                           c.c_void_p, c.c_void_p, c.c_char_p, c.c_size_t]
         _library = lib
         return lib
 
@@ -113,6 +123,9 @@ EXPORTED = (
     "chroma_hip_synchronize",
     "chroma_hip_host_alloc",
     "chroma_hip_host_free",
+    "chroma_hip_rows_topk_workspace",
+    "chroma_hip_rows_topk",
+    "chroma_hip_run_top",
 )
 
 

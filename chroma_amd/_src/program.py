@@ -51,9 +51,8 @@ class NativeModel:
         self.device = self._lib.chroma_hip_device_name(handle).decode()
         self.signature = self._lib.chroma_hip_signature(handle).decode()
 
-    def run(self, inputs: List[np.ndarray], outputs: List[np.ndarray], *, resident: bool = False) -> None:
-        """The extension's ``Model.run``. With ``resident`` an input given as None keeps what its device
-        staging region holds and an output given as None stays on the device."""
+    def _pointers(self, inputs: List[Optional[np.ndarray]], outputs: List[Optional[np.ndarray]], resident: bool) -> Tuple[ctypes.Array, ctypes.Array]:
+        """The host pointer arrays of a call, after the reference's array checks (bindings.h:17-65)."""
         if not isinstance(inputs, list) or not isinstance(outputs, list):
             raise TypeError("run takes two lists of arrays")
         if len(inputs) != len(self._inputs) or len(outputs) != len(self._outputs):
@@ -79,12 +78,36 @@ class NativeModel:
                 raise ValueError("output overlap")
             regions.append((begin, end))
             pointers.append(begin)
-        error = ctypes.create_string_buffer(1024)
         count = len(inputs)
-        status = self._lib.chroma_hip_run(
-            self._handle, native.pointer_array(pointers[:count]), native.pointer_array(pointers[count:]), error, len(error)
-        )
+        return native.pointer_array(pointers[:count]), native.pointer_array(pointers[count:])
+
+    def run(self, inputs: List[np.ndarray], outputs: List[np.ndarray], *, resident: bool = False) -> None:
+        """The extension's ``Model.run``. With ``resident`` an input given as None keeps what its device
+        staging region holds and an output given as None stays on the device."""
+        ins, outs = self._pointers(inputs, outputs, resident)
+        error = ctypes.create_string_buffer(1024)
+        native.check(self._lib.chroma_hip_run(self._handle, ins, outs, error, len(error)), error)
+
+    def run_top(self, inputs: List[Optional[np.ndarray]], outputs: List[Optional[np.ndarray]], index: int, k: int) -> Tuple[np.ndarray, np.ndarray]:
+        """``run`` (resident: None keeps an input's device copy, and leaves an output on the device) that also
+        selects the ``k`` largest values of each row of output ``index`` on the device, after the plan on
+        the same stream and under the same synchronization; returns (values [rows, k], int64 ids [rows, k])
+        in page-locked host arrays."""
+        spec = self._outputs[index]
+        dtype = numpy_dtype(spec["dtype"])
+        if dtype not in (np.dtype(np.float32), BFLOAT16) or not spec["shape"]:
+            raise TypeError("run_top selects over float32 or bfloat16 outputs of rank >= 1")
+        width = int(spec["shape"][-1])
+        rows = int(np.prod(spec["shape"][:-1])) if len(spec["shape"]) > 1 else 1
+        ins, outs = self._pointers(inputs, outputs, True)
+        values = host.empty((rows, k), dtype)
+        ids = host.empty((rows, k), np.int64)
+        code = native.FLOAT32 if dtype == np.dtype(np.float32) else native.BFLOAT16
+        error = ctypes.create_string_buffer(1024)
+        status = self._lib.chroma_hip_run_top(self._handle, ins, outs, index, code, rows, width, k, values.ctypes.data, ids.ctypes.data,
+                                              error, len(error))
         native.check(status, error)
+        return values, ids
 
     def input_pointer(self, index: int) -> int:
         return int(self._lib.chroma_hip_input_pointer(self._handle, index) or 0)
@@ -218,6 +241,15 @@ class Program:
             if self._model is None:
                 raise RuntimeError("Model is closed")
             self._model.run(arrays, list(outputs), resident=True)
+
+    def run_top_resident(self, inputs: Sequence[Optional[Array]], outputs: Sequence[Optional[Array]], index: int, k: int) -> Tuple[Array, Array]:
+        """``run_resident`` that also returns the ``k`` largest values of each row of output ``index`` and
+        their ids, selected on the device (``NativeModel.run_top``)."""
+        arrays = [None if value is None else self._array(value) for value in inputs]
+        with self._lock:
+            if self._model is None:
+                raise RuntimeError("Model is closed")
+            return self._model.run_top(arrays, list(outputs), index, k)
 
     @property
     def native(self) -> NativeModel:

@@ -5,6 +5,7 @@
 // arguments are pre-resolved device pointers. ``run`` uploads inputs, launches every kernel (or replays
 // the captured hipGraph), downloads the error word and the outputs, and synchronizes once.
 #include "../../include/chroma_hip.h"
+#include "select.h"
 
 #include <hip/hip_runtime_api.h>
 
@@ -262,6 +263,9 @@ public:
         if (base_) {
             hipFree(base_);
         }
+        if (select_) {
+            hipFree(select_);
+        }
         if (error_host_) {
             hipHostFree(error_host_);
         }
@@ -288,6 +292,8 @@ public:
         graph_ = nullptr;
         module_ = nullptr;
         base_ = nullptr;
+        select_ = nullptr;
+        select_bytes_ = 0;
         error_host_ = nullptr;
         start_ = stop_ = nullptr;
         stream_ = nullptr;
@@ -320,6 +326,62 @@ public:
             raise_index_error();
         } catch (const HipError&) {
             hipStreamSynchronize(stream_);  // host arrays must outlive every queued copy
+            throw;
+        }
+    }
+
+    // ``run`` with a row selection over output ``index`` queued after the plan: only the k values and ids
+    // of each row come back (and the outputs whose host pointers are non-null), after one synchronization.
+    void run_top(const void* const* inputs, void* const* outputs, int index, int dtype, size_t rows, size_t width, int k, void* values,
+                 int64_t* ids) {
+        DeviceGuard guard(device_);
+        if (index < 0 || size_t(index) >= plan_.outputs.size()) {
+            throw std::runtime_error("run_top: output index out of range");
+        }
+        if (dtype != CHROMA_HIP_FLOAT32 && dtype != CHROMA_HIP_BFLOAT16) {
+            throw std::runtime_error("run_top: dtype must be CHROMA_HIP_FLOAT32 or CHROMA_HIP_BFLOAT16");
+        }
+        const size_t item = dtype == CHROMA_HIP_FLOAT32 ? 4 : 2;
+        if (rows * width * item != plan_.outputs[index].bytes) {
+            throw std::runtime_error("run_top: rows x width elements do not match the output's byte size");
+        }
+        const size_t scratch = chroma_select::workspace_bytes(rows, width, k);
+        if (!scratch) {
+            throw std::runtime_error("run_top: want 1 <= k <= min(width, 1024) and width <= 524288");
+        }
+        auto align = [](size_t n) { return (n + 255) / 256 * 256; };
+        const size_t value_bytes = rows * size_t(k) * item, id_bytes = rows * size_t(k) * sizeof(int64_t);
+        const size_t need = align(scratch) + align(value_bytes) + id_bytes;
+        if (need > select_bytes_) {
+            check(hipStreamSynchronize(stream_), "Selection scratch");
+            if (select_) {
+                check(hipFree(select_), "hipFree selection scratch");
+                select_ = nullptr;
+                select_bytes_ = 0;
+            }
+            check(hipMalloc(&select_, need), "hipMalloc selection scratch");
+            select_bytes_ = need;
+        }
+        char* base = static_cast<char*>(select_);
+        void* device_values = base + align(scratch);
+        int64_t* device_ids = reinterpret_cast<int64_t*>(base + align(scratch) + align(value_bytes));
+        try {
+            upload(inputs);
+            launch_all();
+            char message[256] = {0};
+            if (chroma_select::launch_rows_topk(static_cast<char*>(base_) + plan_.outputs[index].offset, dtype, rows, width, k, 1,
+                                                device_values, device_ids, select_, scratch, stream_, message, sizeof(message))) {
+                throw HipError(message);
+            }
+            check(hipMemcpyAsync(error_host_, static_cast<char*>(base_) + plan_.error, sizeof(unsigned), hipMemcpyDeviceToHost, stream_),
+                  "Read index error");
+            check(hipMemcpyAsync(values, device_values, value_bytes, hipMemcpyDeviceToHost, stream_), "Download selection");
+            check(hipMemcpyAsync(ids, device_ids, id_bytes, hipMemcpyDeviceToHost, stream_), "Download selection");
+            download(outputs);
+            check(hipStreamSynchronize(stream_), "HIP execution");
+            raise_index_error();
+        } catch (const HipError&) {
+            hipStreamSynchronize(stream_);
             throw;
         }
     }
@@ -557,6 +619,8 @@ private:
     hipGraph_t graph_ = nullptr;
     hipGraphExec_t graph_exec_ = nullptr;
     void* staging_[2] = {nullptr, nullptr};  // pinned slots for pageable host transfers (allocated on first use)
+    void* select_ = nullptr;  // run_top's selection scratch and device results (allocated on first use)
+    size_t select_bytes_ = 0;
     hipEvent_t staged_[2] = {nullptr, nullptr};
 };
 
@@ -596,6 +660,12 @@ __attribute__((visibility("default"))) int chroma_hip_create(const char* artifac
 __attribute__((visibility("default"))) int chroma_hip_run(void* handle, const void* const* inputs, void* const* outputs, char* error,
                                                           size_t error_size) {
     return guarded(error, error_size, [&] { program(handle)->run(inputs, outputs); });
+}
+
+__attribute__((visibility("default"))) int chroma_hip_run_top(void* handle, const void* const* inputs, void* const* outputs, int output_index,
+                                                              int dtype, size_t rows, size_t width, int k, void* values, int64_t* ids,
+                                                              char* error, size_t error_size) {
+    return guarded(error, error_size, [&] { program(handle)->run_top(inputs, outputs, output_index, dtype, rows, width, k, values, ids); });
 }
 
 __attribute__((visibility("default"))) const char* chroma_hip_device_name(void* handle) { return program(handle)->name().c_str(); }

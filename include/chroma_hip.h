@@ -12,6 +12,7 @@
 #define CHROMA_HIP_H
 
 #include <stddef.h>
+#include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -20,6 +21,10 @@ extern "C" {
 #define CHROMA_HIP_OK 0
 #define CHROMA_HIP_INDEX_ERROR 1
 #define CHROMA_HIP_RUNTIME_ERROR 2
+
+/* Element types of the selection entry points. */
+#define CHROMA_HIP_FLOAT32 0
+#define CHROMA_HIP_BFLOAT16 1
 
 /* Load the compiled artifact in ``artifact_dir`` (its model.plan, code object and weights file) on the
  * current device. Replaces the reference's generated ``create_model(const char* weights)`` +
@@ -96,6 +101,33 @@ int chroma_hip_synchronize(void* handle, char* error, size_t error_size);
  * fresh outputs in such memory. */
 int chroma_hip_host_alloc(size_t bytes, void** pointer, char* error, size_t error_size);
 void chroma_hip_host_free(void* pointer);
+
+/* --- row selection (top-k over rows of a device matrix) ---
+ * The device counterpart of the reference's GPU top-k family (chroma/_src/codegen/gpu.py:300-337) over
+ * whole vocabulary rows, for callers that pick tokens from logits on the device (the reference's chat
+ * script sorts the downloaded row instead, scripts/chat.py:82-98): the ``k`` largest (``largest`` != 0)
+ * or smallest values of each row of ``x`` [rows, width] (CHROMA_HIP_FLOAT32, or CHROMA_HIP_BFLOAT16
+ * bits) into ``values`` [rows, k] (x's type) and ``ids`` [rows, k] (int64), in order, ties to the lower
+ * id, NaN above every number for largest and below for smallest. 1 <= k <= min(width, 1024) and width <=
+ * 524,288. */
+
+/* Scratch bytes ``chroma_hip_rows_topk`` needs for this shape, or 0 when the shape is not supported. */
+size_t chroma_hip_rows_topk_workspace(size_t rows, size_t width, int k);
+
+/* Queue the selection on ``stream`` (a hipStream_t; null for the null stream) and return: x, values, ids
+ * and ``workspace`` (at least chroma_hip_rows_topk_workspace bytes) are device memory of the current
+ * device, and the caller synchronizes the stream before reading the results or reusing the workspace. */
+int chroma_hip_rows_topk(const void* x, int dtype, size_t rows, size_t width, int k, int largest, void* values, int64_t* ids,
+                         void* workspace, size_t workspace_bytes, void* stream, char* error, size_t error_size);
+
+/* ``chroma_hip_run`` followed, on the program's stream and under the same single synchronization, by the
+ * selection of the ``k`` largest values of each of the ``rows`` rows of output ``output_index`` (``width``
+ * elements of ``dtype`` each, which must be that output's byte size): ``values`` and ``ids`` are host
+ * buffers of rows x k elements. That output itself is downloaded only if ``outputs[output_index]`` is
+ * non-null. The selection's device scratch is allocated by the program on first use and kept. The
+ * KV-cached decoder's ``greedy`` / ``append_top`` use it to return a token instead of a vocabulary row. */
+int chroma_hip_run_top(void* handle, const void* const* inputs, void* const* outputs, int output_index, int dtype, size_t rows,
+                       size_t width, int k, void* values, int64_t* ids, char* error, size_t error_size);
 
 #ifdef __cplusplus
 }

@@ -92,26 +92,10 @@ GRAPHS = _graphs
 
 
 def mlp_module(hidden: int, intermediate: int, seed: int):
-    """BASELINE config C1's block: explicit RMSNorm (eps 1e-5, weight 1), SiLU(gate) * up, down projection,
-    residual; weights N(0, 0.02) drawn with ``seed`` in the order gate, up, down; no biases."""
-    import torch
+    """BASELINE config C1's block (``chroma_amd.models.blocks.mlp_block``) at the given widths."""
+    from chroma_amd.models.blocks import mlp_block
 
-    class MLPBlock(torch.nn.Module):
-        def __init__(self) -> None:
-            super().__init__()
-            generator = torch.Generator().manual_seed(seed)
-            self.norm = torch.nn.Parameter(torch.ones(hidden), requires_grad=False)
-            self.gate = torch.nn.Parameter(torch.randn(intermediate, hidden, generator=generator) * 0.02, requires_grad=False)
-            self.up = torch.nn.Parameter(torch.randn(intermediate, hidden, generator=generator) * 0.02, requires_grad=False)
-            self.down = torch.nn.Parameter(torch.randn(hidden, intermediate, generator=generator) * 0.02, requires_grad=False)
-
-        def forward(self, x):
-            h = x * torch.rsqrt(torch.mean(x**2, dim=-1, keepdim=True) + 1e-5) * self.norm
-            gate = torch.nn.functional.linear(h, self.gate)
-            up = torch.nn.functional.linear(h, self.up)
-            return torch.nn.functional.linear(torch.nn.functional.silu(gate) * up, self.down) + x
-
-    return MLPBlock().eval()
+    return mlp_block(hidden, intermediate, seed)
 
 
 def graph(name: str):
