@@ -1217,6 +1217,11 @@ class HIPCodegen(Codegen):
         rows = math.prod(shape) // columns
         dim = len(shape) - 1
         threads, lanes, chunks, resident = self._row_plan(columns, x.dtype)
+        splits, chunk, split_lanes = self._row_splits(rows, columns, x.dtype)
+        if splits > 1 and not resident:
+            self._split_norm(out, x, weight, epsilon, shape, rows, columns, splits, chunk, split_lanes)
+            self.parallel_reductions += 1
+            return out
         waves = threads // 64
         k = Kernel(lanes)
         slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
@@ -1268,6 +1273,70 @@ class HIPCodegen(Codegen):
         self.launch(k, rows, threads, [x, weight], kind="rmsnorm", prologue=[f"__shared__ float scratch[{waves}];"])
         self.parallel_reductions += 1
         return out
+
+    def _split_norm(self, out: Value, x: Value, weight: Value, epsilon: float, shape, rows: int, columns: int, splits: int, chunk: int,
+                    lanes: int) -> None:
+        """RMSNorm of few wide rows: one workgroup per (row, split) sums the squares of its part of the row
+        into a scratch float; then each (row, split) workgroup adds its row's partial sums, forms the
+        reference's scale 1 / sqrt(sum / D + eps) and writes its part as x * scale * w."""
+        dim = len(shape) - 1
+        step = ROW_THREADS * lanes
+        waves = ROW_THREADS // 64
+        partials = self.allocate((rows * splits,), torch.float32)
+
+        def names_of(k: Kernel, value: Value, coords: List[Aff]) -> List[str]:
+            names = k.emit(self.read(k, value, coords))
+            return names if isinstance(names, list) else [names] * lanes
+
+        def bounds(k: Kernel) -> None:
+            k.line(f"const uint32_t begin = blockIdx.x % {splits}u * {chunk}u;")
+            k.line(f"const uint32_t end = begin + {chunk}u < {columns}u ? begin + {chunk}u : {columns}u;")
+            k.line(f"uint32_t base = begin + threadIdx.x * {lanes}u;")
+
+        k = Kernel(lanes)
+        part_slot = k.slot(partials.name, torch.float32, writable=True, extent=self.extents[partials.name])
+        row = Aff.of(k.atom(f"blockIdx.x / {splits}u", rows - 1, prefix="r"))
+        bounds(k)
+        k.line("float squares = 0.0f;")
+        with k.block(f"for (; base + {(ROW_UNROLL - 1) * step}u < end; base += {ROW_UNROLL * step}u) {{"):
+            loaded = [names_of(k, x, self._row_coords(k, row, shape, dim, Aff.of(k.vector_atom(f"base + {u * step}u", columns - 1))))
+                      for u in range(ROW_UNROLL)]
+            for names in loaded:
+                k.line("squares += " + " + ".join(f"{n} * {n}" for n in names) + ";")
+        with k.block(f"for (; base < end; base += {step}u) {{"):
+            names = names_of(k, x, self._row_coords(k, row, shape, dim, Aff.of(k.vector_atom("base", columns - 1))))
+            k.line("squares += " + " + ".join(f"{n} * {n}" for n in names) + ";")
+        k.line(f"squares = chroma::block_sum<{waves}>(squares, scratch);")
+        k.line(f"if (threadIdx.x == 0) {part_slot}[blockIdx.x] = squares;")
+        self.launch(k, rows * splits, ROW_THREADS, [x], kind="norm_partials", prologue=[f"__shared__ float scratch[{waves}];"])
+
+        k = Kernel(lanes)
+        k.streaming = STREAMING_STORES and math.prod(shape) * ITEMSIZE[out.dtype] >= STREAMING_BYTES
+        part_slot = k.slot(partials.name, torch.float32, extent=self.extents[partials.name])
+        slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        row_atom = k.atom(f"blockIdx.x / {splits}u", rows - 1, prefix="r")
+        row = Aff.of(row_atom)
+        k.line("float squares = 0.0f;")
+        k.line(f"for (uint32_t s = threadIdx.x; s < {splits}u; s += {ROW_THREADS}u) squares += {part_slot}[{row_atom.name} * {splits}u + s];")
+        k.line(f"squares = chroma::block_sum<{waves}>(squares, scratch);")
+        k.line(f"const float scale = 1.0f / sqrtf(squares / {float_literal(columns)} + {float_literal(epsilon)});")
+        bounds(k)
+
+        def write(j: Aff, names: List[str]) -> None:
+            ws = names_of(k, weight, [j])
+            result = self._lane_values(k, [f"{xv} * scale * {wv}" for xv, wv in zip(names, ws)])
+            k.store(slot, out.dtype, Kernel.flatten(self._row_coords(k, row, shape, dim, j), shape), result)
+
+        with k.block(f"for (; base + {(ROW_UNROLL - 1) * step}u < end; base += {ROW_UNROLL * step}u) {{"):
+            js = [Aff.of(k.vector_atom(f"base + {u * step}u", columns - 1)) for u in range(ROW_UNROLL)]
+            loaded = [names_of(k, x, self._row_coords(k, row, shape, dim, j)) for j in js]
+            for j, names in zip(js, loaded):
+                write(j, names)
+        with k.block(f"for (; base < end; base += {step}u) {{"):
+            j = Aff.of(k.vector_atom("base", columns - 1))
+            write(j, names_of(k, x, self._row_coords(k, row, shape, dim, j)))
+        self.launch(k, rows * splits, ROW_THREADS, [x, weight, partials], kind="rmsnorm_split",
+                    prologue=[f"__shared__ float scratch[{waves}];"])
 
     # ------------------------------------------------------------------------------ reduction
     def reduction(self, meta, x: Value, axes: Sequence[int], keepdim: bool, mean: bool) -> Value:
