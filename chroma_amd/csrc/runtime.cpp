@@ -266,6 +266,9 @@ public:
         if (select_) {
             hipFree(select_);
         }
+        if (select_host_) {
+            hipHostFree(select_host_);
+        }
         if (error_host_) {
             hipHostFree(error_host_);
         }
@@ -294,6 +297,8 @@ public:
         base_ = nullptr;
         select_ = nullptr;
         select_bytes_ = 0;
+        select_host_ = nullptr;
+        select_host_bytes_ = 0;
         error_host_ = nullptr;
         start_ = stop_ = nullptr;
         stream_ = nullptr;
@@ -351,20 +356,29 @@ public:
         }
         auto align = [](size_t n) { return (n + 255) / 256 * 256; };
         const size_t value_bytes = rows * size_t(k) * item, id_bytes = rows * size_t(k) * sizeof(int64_t);
-        const size_t need = align(scratch) + align(value_bytes) + id_bytes;
-        if (need > select_bytes_) {
+        // ids then values, adjacent, so one copy brings both back
+        const size_t result_bytes = id_bytes + value_bytes;
+        const size_t need = align(scratch) + result_bytes;
+        if (need > select_bytes_ || result_bytes > select_host_bytes_) {
             check(hipStreamSynchronize(stream_), "Selection scratch");
             if (select_) {
                 check(hipFree(select_), "hipFree selection scratch");
                 select_ = nullptr;
                 select_bytes_ = 0;
             }
+            if (select_host_) {
+                check(hipHostFree(select_host_), "hipHostFree selection results");
+                select_host_ = nullptr;
+                select_host_bytes_ = 0;
+            }
             check(hipMalloc(&select_, need), "hipMalloc selection scratch");
             select_bytes_ = need;
+            check(hipHostMalloc(&select_host_, result_bytes, hipHostMallocDefault), "hipHostMalloc selection results");
+            select_host_bytes_ = result_bytes;
         }
         char* base = static_cast<char*>(select_);
-        void* device_values = base + align(scratch);
-        int64_t* device_ids = reinterpret_cast<int64_t*>(base + align(scratch) + align(value_bytes));
+        int64_t* device_ids = reinterpret_cast<int64_t*>(base + align(scratch));
+        void* device_values = base + align(scratch) + id_bytes;
         try {
             upload(inputs);
             launch_all();
@@ -375,10 +389,11 @@ public:
             }
             check(hipMemcpyAsync(error_host_, static_cast<char*>(base_) + plan_.error, sizeof(unsigned), hipMemcpyDeviceToHost, stream_),
                   "Read index error");
-            check(hipMemcpyAsync(values, device_values, value_bytes, hipMemcpyDeviceToHost, stream_), "Download selection");
-            check(hipMemcpyAsync(ids, device_ids, id_bytes, hipMemcpyDeviceToHost, stream_), "Download selection");
+            check(hipMemcpyAsync(select_host_, device_ids, result_bytes, hipMemcpyDeviceToHost, stream_), "Download selection");
             download(outputs);
             check(hipStreamSynchronize(stream_), "HIP execution");
+            std::memcpy(ids, select_host_, id_bytes);
+            std::memcpy(values, static_cast<char*>(select_host_) + id_bytes, value_bytes);
             raise_index_error();
         } catch (const HipError&) {
             hipStreamSynchronize(stream_);
@@ -621,6 +636,8 @@ private:
     void* staging_[2] = {nullptr, nullptr};  // pinned slots for pageable host transfers (allocated on first use)
     void* select_ = nullptr;  // run_top's selection scratch and device results (allocated on first use)
     size_t select_bytes_ = 0;
+    void* select_host_ = nullptr;  // pinned landing area of run_top's ids and values
+    size_t select_host_bytes_ = 0;
     hipEvent_t staged_[2] = {nullptr, nullptr};
 };
 
