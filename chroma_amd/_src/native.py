@@ -98,6 +98,8 @@ def library() -> ctypes.CDLL:
         lib.chroma_hip_rows_topk_workspace.restype = c.c_size_t
         lib.chroma_hip_rows_topk.argtypes = [c.c_void_p, c.c_int, c.c_size_t, c.c_size_t, c.c_int, c.c_int, c.c_void_p, c.c_void_p,
                                              c.c_void_p, c.c_size_t, c.c_void_p, c.c_char_p, c.c_size_t]
+        lib.chroma_hip_rows_topk_static.argtypes = [c.c_void_p, c.c_int, c.c_size_t, c.c_size_t, c.c_int, c.c_int, c.c_void_p, c.c_void_p,
+                                                    c.c_void_p, c.c_char_p, c.c_size_t]
         lib.chroma_hip_run_top.argtypes = [c.c_void_p, c.c_void_p, c.c_void_p, c.c_int, c.c_int, c.c_size_t, c.c_size_t, c.c_int,
                                            c.c_void_p, c.c_void_p, c.c_char_p, c.c_size_t]
         _library = lib
@@ -125,6 +127,7 @@ EXPORTED = (
     "chroma_hip_host_free",
     "chroma_hip_rows_topk_workspace",
     "chroma_hip_rows_topk",
+    "chroma_hip_rows_topk_static",
     "chroma_hip_run_top",
 )
 

@@ -202,6 +202,40 @@ int launch_rows_topk(const void* x, int dtype, size_t rows, size_t width, int k,
 
 }  // namespace chroma_select
 
+namespace {
+
+// Scratch of chroma_hip_rows_topk_static: one copy of this array per GPU, at that GPU's own address, kept
+// until the process ends. Its address on a device comes from hipGetSymbolAddress on the first call there;
+// the array's name itself is a host-side stand-in that must never reach a kernel or a copy.
+constexpr size_t kStaticScratchBytes = CHROMA_HIP_STATIC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mutex;
+void* scratch_address[kMaxDevices] = {};  // per device, null until looked up
+
+int static_scratch(void** address, char* error, size_t error_size) {
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) {
+        return fail("rows_topk_static: no usable current device", error, error_size);
+    }
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    if (!scratch_address[device]) {
+        void* found = nullptr;
+        const hipError_t status = hipGetSymbolAddress(&found, HIP_SYMBOL(scratch));
+        if (status != hipSuccess || !found) {
+            char message[160];
+            std::snprintf(message, sizeof(message), "rows_topk_static: hipGetSymbolAddress: %s", hipGetErrorString(status));
+            return fail(message, error, error_size);
+        }
+        scratch_address[device] = found;
+    }
+    *address = scratch_address[device];
+    return CHROMA_HIP_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 __attribute__((visibility("default"))) size_t chroma_hip_rows_topk_workspace(size_t rows, size_t width, int k) {
@@ -212,6 +246,25 @@ __attribute__((visibility("default"))) int chroma_hip_rows_topk(const void* x, i
                                                                 void* values, int64_t* ids, void* workspace, size_t workspace_bytes,
                                                                 void* stream, char* error, size_t error_size) {
     return chroma_select::launch_rows_topk(x, dtype, rows, width, k, largest, values, ids, workspace, workspace_bytes,
+                                           static_cast<hipStream_t>(stream), error, error_size);
+}
+
+__attribute__((visibility("default"))) int chroma_hip_rows_topk_static(const void* x, int dtype, size_t rows, size_t width, int k,
+                                                                       int largest, void* values, int64_t* ids, void* stream, char* error,
+                                                                       size_t error_size) {
+    const size_t need = chroma_select::workspace_bytes(rows, width, k);
+    if (need > kStaticScratchBytes) {
+        char message[200];
+        std::snprintf(message, sizeof(message), "rows_topk_static: this selection needs %zu bytes of scratch; the static scratch holds %zu",
+                      need, kStaticScratchBytes);
+        return fail(message, error, error_size);
+    }
+    void* address = nullptr;
+    const int status = static_scratch(&address, error, error_size);
+    if (status != CHROMA_HIP_OK) {
+        return status;
+    }
+    return chroma_select::launch_rows_topk(x, dtype, rows, width, k, largest, values, ids, address, kStaticScratchBytes,
                                            static_cast<hipStream_t>(stream), error, error_size);
 }
 

@@ -120,6 +120,17 @@ size_t chroma_hip_rows_topk_workspace(size_t rows, size_t width, int k);
 int chroma_hip_rows_topk(const void* x, int dtype, size_t rows, size_t width, int k, int largest, void* values, int64_t* ids,
                          void* workspace, size_t workspace_bytes, void* stream, char* error, size_t error_size);
 
+/* ``chroma_hip_rows_topk`` without a workspace: the scratch is a static device array of
+ * CHROMA_HIP_STATIC_SCRATCH_BYTES per GPU (looked up on the first call on each device and kept until the
+ * process ends), so the call allocates nothing. No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). A selection needing more scratch than the array holds (chroma_hip_rows_topk_workspace) is
+ * rejected with a message. Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (two streams, or two threads) race and must be serialized by the caller. */
+#define CHROMA_HIP_STATIC_SCRATCH_BYTES ((size_t)4 << 20)
+int chroma_hip_rows_topk_static(const void* x, int dtype, size_t rows, size_t width, int k, int largest, void* values, int64_t* ids,
+                                void* stream, char* error, size_t error_size);
+
 /* ``chroma_hip_run`` followed, on the program's stream and under the same single synchronization, by the
  * selection of the ``k`` largest values of each of the ``rows`` rows of output ``output_index`` (``width``
  * elements of ``dtype`` each, which must be that output's byte size): ``values`` and ``ids`` are host
