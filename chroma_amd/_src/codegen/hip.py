@@ -63,6 +63,8 @@ WIDE_TOPK_LANE_VALUES = 32  # rows needing more values per lane take the two-sta
 TRANSCENDENTAL_OPS = frozenset({"sin", "cos", "exp", "tanh", "sigmoid", "silu", "pow", "log"})
 STORED_TABLE_ELEMENTS = 4096  # multi-consumer expressions with such ops and at least this many elements are stored
 MFMA_CUS = 256  # compute units of the target (MI355X), for the tile-round choice of the matrix-core products
+DIRECT_GEMM_THREADS = 512  # chroma::kDirectThreads: the direct-to-LDS matrix-core body's 8 waves
+DIRECT_GEMM_WAVES = 4  # waves per SIMD it is compiled for (two 64 KiB-LDS workgroups per compute unit)
 REUSED_EVALUATIONS = 1 << 18  # a contraction operand is stored when (elements x reuse) reaches this
 SMALL_REDUCTION = 8  # contractions summing at most this many products are fused expressions...
 SMALL_OPERAND_COST = 8  # ...over operands that cost at most this much per element (others are stored)
@@ -1606,8 +1608,18 @@ class HIPCodegen(Codegen):
         # the 64-deep body (two workgroups per CU) when every tile fits in one round of the chip, else the
         # 32-deep body (three per CU), whose rounds quantize less
         path = 0 if tiles <= 2 * MFMA_CUS else 1
+        threads = 256
+        if self._direct_gemm(out.dtype, inner):
+            path, threads = 2, DIRECT_GEMM_THREADS
+            k.min_waves = DIRECT_GEMM_WAVES
         k.line(f"chroma::mfma_linear<{ctype_of(out.dtype)}, {path}>({args[0]}, {args[1]}, {args[2]}, {out_slot}, {rows}u, {columns}u, {inner}u);")
-        self.launch(k, 8 * -(-tiles // 8), 256, [x, weight] + ([bias] if bias is not None else []), kind="linear_mfma")
+        self.launch(k, 8 * -(-tiles // 8), threads, [x, weight] + ([bias] if bias is not None else []), kind="linear_mfma")
+
+    @staticmethod
+    def _direct_gemm(dtype: torch.dtype, inner: int) -> bool:
+        """The direct-to-LDS matrix-core body (``mfma_gemm_direct``) applies: bfloat16 operands whose
+        contiguous rows of ``inner`` elements split into 64-deep slices of 16-byte chunks."""
+        return dtype == torch.bfloat16 and inner % 64 == 0
 
     def _tiled_linear(self, out, x, weight, bias, rows, columns, inner) -> None:
         k = Kernel(1)
@@ -1995,35 +2007,48 @@ class HIPCodegen(Codegen):
         k.line(f"a.sinks = {pointer('sinks')}; a.sh = {sink_strides[0]}u; a.sg = {sink_strides[1]}u;")
         k.line(f"a.out = {slot}; a.tokens = {tokens}u; a.past = {past}u; a.keys = {keys}u; a.kv_heads = {kv_heads}u; a.group = {group}u;")
         k.line(f"a.scale = {float_literal(scale)};")
-        live = self._live_blocks(plan["mask"], tokens, keys) if mask_strides[0] == mask_strides[1] == 0 else None
-        if live is not None:
+        shared_mask = mask_strides[0] == mask_strides[1] == 0
+        if shared_mask and group <= 8:
+            # one workgroup per (16-query tile, KV head), one wave per query head: K/V/mask tiles staged once
+            live = self._live_blocks(plan["mask"], tokens, keys, tile=(16, 64))
             k.line(f"a.live_blocks = reinterpret_cast<const uint8_t*>({k.slot(live.name, torch.int64, extent=self.extents[live.name])});")
+            k.line(f"chroma::attention_heads_mfma_bf16<{dim}, {group}>(a);")
+            operands = [entry[0] for entry in plan.values() if entry is not None] + [live]
+            self.launch(k, (-(-tokens // 16), kv_heads, 1), 64 * group, operands, kind="attention_heads")
         else:
-            k.line("a.live_blocks = nullptr;")
-        k.line(f"chroma::attention_mfma_bf16<{dim}>(a);")
-        # every key block's loads are a round trip and more resident workgroups hide them; five waves per
-        # SIMD fit without spills up to D = 64 (D = 128 would spill)
-        k.min_waves = 5 if dim <= 64 else 0
-        operands = [entry[0] for entry in plan.values() if entry is not None] + ([live] if live is not None else [])
-        self.launch(k, (-(-tokens // 64), kv_heads * group, 1), 256, operands, kind="attention_mfma")
+            live = self._live_blocks(plan["mask"], tokens, keys) if shared_mask else None
+            if live is not None:
+                k.line(f"a.live_blocks = reinterpret_cast<const uint8_t*>({k.slot(live.name, torch.int64, extent=self.extents[live.name])});")
+            else:
+                k.line("a.live_blocks = nullptr;")
+            k.line(f"chroma::attention_mfma_bf16<{dim}>(a);")
+            # every key block's loads are a round trip and more resident workgroups hide them; five waves per
+            # SIMD fit without spills up to D = 64 (D = 128 would spill)
+            k.min_waves = 5 if dim <= 64 else 0
+            operands = [entry[0] for entry in plan.values() if entry is not None] + ([live] if live is not None else [])
+            self.launch(k, (-(-tokens // 64), kv_heads * group, 1), 256, operands, kind="attention_mfma")
         self.fused_attentions += 1
         self.mfma_matmuls += 1
         return True
 
-    def _live_blocks(self, mask_plan, tokens: int, keys: int) -> Value:
-        """Per (64-query, 32-key) block of a head-independent bfloat16 mask, whether any entry is not -inf:
-        computed once per mask and shared by every attention that reads it."""
+    def _live_blocks(self, mask_plan, tokens: int, keys: int, tile: Tuple[int, int] = (64, 32)) -> Value:
+        """Per (queries x keys) block of a head-independent bfloat16 mask, whether any entry is not -inf:
+        computed once per mask and block shape and shared by every attention that reads it. (64, 32)
+        blocks also mark the all-+0.0 blocks (``attention_live_blocks``); (16, 64) blocks serve the
+        group-shared kernel (``attention_live_tiles``)."""
         value, strides, offset = mask_plan
-        key = (value.root.name, offset, strides[2], tokens, keys)
+        key = (value.root.name, offset, strides[2], tokens, keys, tile)
         if key not in self.live_block_tables:
-            query_blocks, key_blocks = -(-tokens // 64), -(-keys // 32)
+            query_blocks, key_blocks = -(-tokens // tile[0]), -(-keys // tile[1])
             table = self.allocate((-(-query_blocks * key_blocks // 8),), torch.int64)
             k = Kernel(1)
             root = value.root
             base = k.slot(root.name, root.dtype, extent=self.extents[root.name])
             flags = k.slot(table.name, torch.int64, writable=True, extent=self.extents[table.name])
             pointer = f"{base} + {offset}u" if offset else base
-            k.line(f"chroma::attention_live_blocks({pointer}, {strides[2]}u, {tokens}u, {keys}u, reinterpret_cast<uint8_t*>({flags}));")
+            function = "attention_live_blocks" if tile == (64, 32) else "attention_live_tiles"
+            assert tile in ((64, 32), (16, 64))
+            k.line(f"chroma::{function}({pointer}, {strides[2]}u, {tokens}u, {keys}u, reinterpret_cast<uint8_t*>({flags}));")
             self.launch(k, (query_blocks, key_blocks, 1), 256, [value], kind="attention_blocks")
             self.live_block_tables[key] = table
         return self.live_block_tables[key]
@@ -2258,11 +2283,15 @@ class HIPCodegen(Codegen):
         w, xs = self._matrix_slot(k, weight), self._matrix_slot(k, x)
         table = k.slot(scratch.name, torch.int64, extent=self.extents[scratch.name])
         out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        path, threads = 1, 256
+        if self._direct_gemm(out.dtype, inner):
+            path, threads = 2, DIRECT_GEMM_THREADS
+            k.min_waves = DIRECT_GEMM_WAVES
         k.line(
-            f"chroma::grouped_expert_linear<{ctype_of(out.dtype)}, {str(per_slot).lower()}, 1>({w}, {xs}, {out_slot}, "
+            f"chroma::grouped_expert_linear<{ctype_of(out.dtype)}, {str(per_slot).lower()}, {path}>({w}, {xs}, {out_slot}, "
             f"reinterpret_cast<const int32_t*>({table}), {tokens * selected}u, {selected}u, {experts}u, {channels}u, {inner}u);"
         )
-        self.launch(k, 8 * -(-(-(-channels // 128) * tiles) // 8), 256, [weight, x, scratch], kind="experts_mfma")
+        self.launch(k, 8 * -(-(-(-channels // 128) * tiles) // 8), threads, [weight, x, scratch], kind="experts_mfma")
         self.mfma_matmuls += 1
 
     def _loop_einsum(self, meta, labels, output, sizes, reduction, values) -> Value:

@@ -887,4 +887,259 @@ template <int D> __device__ __forceinline__ void attention_mfma_bf16(const Atten
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Matrix-core attention for long bfloat16 prefills, one workgroup per (16-query tile, key/value head) and
+// one wave per query head of the group: the K tile, the V^T tile and the mask tile of each 64-key block are
+// staged into LDS once and serve all G heads (the head-parallel form stages them once per head). Mask
+// shared by every head (mh = mg = 0). Same computation as attention_mfma_bf16 and the reference chain:
+// S^T = K . Q^T on v_mfma_f32_16x16x32_bf16, each score rounded to bfloat16, scaled and rounded, masked
+// and rounded (gfx950's v_cvt_pk_bf16_f32 rounds, to nearest even like f32_to_bf16); pass 1 accumulates
+// (max, sum of exp) per query in float, pass 2 forms p = exp(s - max) * (1 / sum) rounded to bfloat16
+// (within one ulp of the quotient) and O^T += V^T . P^T; the output is rounded once. The 64-key blocks a
+// query tile visits come from ``attention_live_tiles`` (blocks whose mask is -inf throughout are never
+// read); a visited block's next block is staged into the other LDS buffer while it is computed, so each
+// block costs one barrier. Key rows past ``keys`` are zeros with a -inf mask, queries past ``tokens`` see
+// only -inf and are not stored.
+
+constexpr uint32_t kLiveTilesMax = 1024;  // 64-key blocks a workgroup lists in LDS (64K keys)
+
+// live_tiles[qt * key_blocks + kb] for queries [16 qt, 16 qt + 16) and keys [64 kb, 64 kb + 64) of a mask
+// shared by every head: 0 when every entry there is -inf, 1 otherwise (grid: query tiles x key blocks).
+__device__ __forceinline__ void attention_live_tiles(const uint16_t* __restrict__ mask, uint32_t mt, uint32_t tokens, uint32_t keys,
+                                                     uint8_t* __restrict__ live_tiles) {
+    const uint32_t qt = blockIdx.x, kb = blockIdx.y;
+    bool any = false;
+    for (uint32_t i = threadIdx.x; i < 16u * 64u; i += blockDim.x) {
+        const uint32_t t = qt * 16u + i / 64u, j = kb * 64u + i % 64u;
+        if (t < tokens && j < keys) {
+            any |= mask[size_t(t) * mt + j] != 0xff80u;
+        }
+    }
+    any = __syncthreads_or(any);
+    if (threadIdx.x == 0) {
+        live_tiles[qt * gridDim.y + kb] = any ? 1 : 0;
+    }
+}
+
+template <int D, int G> __device__ __forceinline__ void attention_heads_mfma_bf16(const AttentionOperands& a) {
+    static_assert(D % 32 == 0 && D <= 128 && G >= 1 && G <= 8, "head dimension and group");
+    constexpr int QT = 16, KB = 64, THREADS = 64 * G;
+    constexpr int KPAD = D + 8, VPAD = KB + 8, MPAD = KB + 4;
+    constexpr int CHUNKS = (KB * D / 8 + THREADS - 1) / THREADS;  // 16-byte K (and V) chunks per thread per block
+    constexpr int MASKS = (QT * KB + THREADS - 1) / THREADS;      // mask entries per thread per block
+    __shared__ __attribute__((aligned(16))) uint16_t k_s[2][KB * KPAD];
+    __shared__ __attribute__((aligned(16))) uint16_t v_s[2][D * VPAD];
+    __shared__ __attribute__((aligned(16))) uint16_t m_s[2][QT * MPAD];
+    __shared__ uint16_t live_list[kLiveTilesMax];
+    __shared__ uint32_t live_total;
+    const uint32_t tid = threadIdx.x, lane = tid % 64u, g = tid / 64u, quad = lane / 16u, col = lane % 16u;
+    const uint32_t kv = blockIdx.y;
+    const uint32_t tile = gridDim.x - 1u - blockIdx.x;  // later query tiles see more keys: dispatched first
+    const uint32_t q0 = tile * QT, query = q0 + col;
+    const bool live = query < a.tokens;
+    const uint32_t qrow = live ? query : a.tokens - 1u;
+    const float neg_inf = -__builtin_inff();
+
+    bf16x8_t qf[D / 32];
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) {
+        qf[ks] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(a.q + size_t(qrow) * a.qt + kv * a.qh + g * a.qg + ks * 32u + quad * 8u));
+    }
+
+    // The 64-key blocks this tile visits, in key order: wave 0 compacts its row of the live table with a
+    // ballot per 64 blocks; without a table (or past the list's capacity) every block.
+    const uint32_t blocks = (a.keys + KB - 1) / KB;
+    const bool listed = a.live_blocks != nullptr && blocks <= kLiveTilesMax;
+    if (listed) {
+        if (g == 0) {
+            const uint8_t* row = a.live_blocks + size_t(tile) * blocks;
+            uint32_t n = 0;
+            for (uint32_t base = 0; base < blocks; base += 64u) {
+                const uint32_t kb = base + lane;
+                const bool on = kb < blocks && row[kb] != 0;
+                const unsigned long long bits = __ballot(on);
+                if (on) {
+                    live_list[n + uint32_t(__popcll(bits & ((1ull << lane) - 1ull)))] = uint16_t(kb);
+                }
+                n += uint32_t(__popcll(bits));
+            }
+            if (lane == 0) {
+                live_total = n;
+            }
+        }
+        __syncthreads();
+    }
+    const uint32_t visits = listed ? live_total : blocks;
+    auto block_of = [&](uint32_t i) -> uint32_t { return listed ? uint32_t(live_list[i]) : i; };
+
+    // Global -> registers (every load unconditional, its index clamped; what lies out of range is replaced
+    // when stored to LDS), then registers -> LDS buffer: K row-major, V transposed, mask [query][key].
+    uint4 rk[CHUNKS], rv[CHUNKS];
+    uint16_t rm[MASKS];
+    auto fetch = [&](uint32_t kb, bool values) {
+#pragma unroll
+        for (int i = 0; i < CHUNKS; ++i) {
+            const uint32_t c = tid + i * THREADS;
+            const uint32_t cc = c < uint32_t(KB * D / 8) ? c : 0u;
+            const uint32_t r = cc / (D / 8), dc = (cc % (D / 8)) * 8u, j = kb * KB + r;
+            const uint32_t jj = j < a.keys ? j : a.keys - 1u;
+            const bool old = jj < a.past;
+            const size_t kr = old ? size_t(jj) * a.kpj + kv * a.kph : size_t(jj - a.past) * a.knj + kv * a.knh;
+            rk[i] = *reinterpret_cast<const uint4*>((old ? a.k_past : a.k_new) + kr + dc);
+            if (values) {
+                const size_t vr = old ? size_t(jj) * a.vpj + kv * a.vph : size_t(jj - a.past) * a.vnj + kv * a.vnh;
+                rv[i] = *reinterpret_cast<const uint4*>((old ? a.v_past : a.v_new) + vr + dc);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < MASKS; ++i) {
+            const uint32_t e = tid + i * THREADS;
+            const uint32_t t = q0 + (e / KB) % QT, j = kb * KB + e % KB;
+            rm[i] = a.mask[size_t(t < a.tokens ? t : a.tokens - 1u) * a.mt + (j < a.keys ? j : a.keys - 1u)];
+        }
+    };
+    auto put = [&](int buffer, uint32_t kb, bool values) {
+#pragma unroll
+        for (int i = 0; i < CHUNKS; ++i) {
+            const uint32_t c = tid + i * THREADS;
+            if (c < uint32_t(KB * D / 8)) {
+                const uint32_t r = c / (D / 8), dc = (c % (D / 8)) * 8u;
+                const bool ok = kb * KB + r < a.keys;
+                *reinterpret_cast<uint4*>(&k_s[buffer][r * KPAD + dc]) = ok ? rk[i] : uint4{0, 0, 0, 0};
+                if (values) {
+                    const uint4 v = ok ? rv[i] : uint4{0, 0, 0, 0};
+                    const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
+#pragma unroll
+                    for (int x = 0; x < 8; ++x) {
+                        v_s[buffer][(dc + x) * VPAD + r] = e[x];
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < MASKS; ++i) {
+            const uint32_t e = tid + i * THREADS;
+            if (e < uint32_t(QT * KB)) {
+                const uint32_t qr = e / KB, kc = e % KB;
+                const bool ok = q0 + qr < a.tokens && kb * KB + kc < a.keys;
+                m_s[buffer][qr * MPAD + kc] = ok ? rm[i] : uint16_t(0xff80u);
+            }
+        }
+    };
+    // Masked scores of this lane: key 16 t + 4 quad + r of the block, query ``col`` of the tile.
+    auto scores = [&](int buffer, float (&s2)[4][4]) {
+        f32x4_t acc[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) {
+                const bf16x8_t kf = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(&k_s[buffer][(t * 16u + col) * KPAD + ks * 32u + quad * 8u]));
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ks], acc[t], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint2 m = *reinterpret_cast<const uint2*>(&m_s[buffer][col * MPAD + t * 16u + quad * 4u]);
+            const float mv[4] = {__uint_as_float(m.x << 16), __uint_as_float(m.x & 0xffff0000u), __uint_as_float(m.y << 16),
+                                 __uint_as_float(m.y & 0xffff0000u)};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float s1 = round_bf16_fast(round_bf16_fast(acc[t][r]) * a.scale);
+                s2[t][r] = round_bf16_fast(s1 + mv[r]);
+            }
+        }
+    };
+    // One pass over the visited blocks, the next block staged while the current one is computed.
+    auto sweep = [&](bool values, auto&& body) {
+        if (visits == 0) {
+            return;
+        }
+        fetch(block_of(0), values);
+        put(0, block_of(0), values);
+        fetch(block_of(visits > 1 ? 1u : 0u), values);
+        __syncthreads();
+        for (uint32_t i = 0; i < visits; ++i) {
+            body(int(i & 1u));
+            // registers hold block i + 1 (or re-read block i when it is the last, never stored)
+            if (i + 1 < visits) {
+                put(int((i + 1) & 1u), block_of(i + 1), values);
+            }
+            const uint32_t ahead = i + 2 < visits ? i + 2 : visits - 1u;
+            fetch(block_of(ahead), values);
+            __syncthreads();
+        }
+    };
+
+    float peak = neg_inf, total = 0.0f;
+    sweep(false, [&](int buffer) {
+        float s2[4][4];
+        scores(buffer, s2);
+        float top = peak;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                top = __builtin_fmaxf(top, s2[t][r]);
+            }
+        }
+        if (top != neg_inf) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    sum += fast_exp(s2[t][r] - top);
+                }
+            }
+            total = total * fast_exp(peak - top) + sum;
+            peak = top;
+        }
+    });
+    // Combine the four lane groups that share a query, then fold in the sink.
+#pragma unroll
+    for (int offset = 16; offset < 64; offset <<= 1) {
+        softmax_stats_merge(peak, total, __shfl_xor(peak, offset, kWave), __shfl_xor(total, offset, kWave));
+    }
+    softmax_stats_add(peak, total, bf16_to_f32(a.sinks[kv * a.sh + g * a.sg]));
+    const float inverse = 1.0f / total;
+
+    f32x4_t o[D / 16];
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) {
+        o[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    sweep(true, [&](int buffer) {
+        float s2[4][4];
+        scores(buffer, s2);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            // keys 32 h + (4 quad + r) and 32 h + 16 + (4 quad + r): this lane's B operand slots 0-3 and 4-7
+            bf16x8_t pf;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                pf[i] = __bf16(fast_exp(s2[2 * h + i / 4][i % 4] - peak) * inverse);
+            }
+#pragma unroll
+            for (int dt = 0; dt < D / 16; ++dt) {
+                const uint16_t* row = &v_s[buffer][(dt * 16u + col) * VPAD + h * 32u];
+                const uint2 lo = *reinterpret_cast<const uint2*>(row + quad * 4u);
+                const uint2 hi = *reinterpret_cast<const uint2*>(row + 16u + quad * 4u);
+                const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, uint4{lo.x, lo.y, hi.x, hi.y});
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[dt], 0, 0, 0);
+            }
+        }
+    });
+    if (live) {
+        uint16_t* dst = a.out + ((size_t(query) * a.kv_heads + kv) * a.group + g) * D;
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt) {
+            const uint32_t d = dt * 16u + quad * 4u;
+            const uint32_t w0 = uint32_t(f32_to_bf16(o[dt][0])) | (uint32_t(f32_to_bf16(o[dt][1])) << 16);
+            const uint32_t w1 = uint32_t(f32_to_bf16(o[dt][2])) | (uint32_t(f32_to_bf16(o[dt][3])) << 16);
+            *reinterpret_cast<uint2*>(dst + d) = uint2{w0, w1};
+        }
+    }
+}
+
 }  // namespace chroma

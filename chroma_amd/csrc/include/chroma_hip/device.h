@@ -25,6 +25,11 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float value) {
 
 __device__ __forceinline__ float round_bf16(float value) { return bf16_to_f32(f32_to_bf16(value)); }
 
+// The same rounding for intermediate values on gfx950's v_cvt_pk_bf16_f32 (round to nearest even, like
+// f32_to_bf16 for every value but NaN, which stays a NaN with another payload): one conversion and one
+// shift instead of five integer operations. Stored results keep f32_to_bf16, whose NaN is always 0x7fc0.
+__device__ __forceinline__ float round_bf16_fast(float value) { return float(__bf16(value)); }
+
 // ---------------------------------------------------------------------------------------------
 // Gather row index with the reference's bounds rule (chroma/_src/codegen/cuda/runtime.h:18-32):
 // an index outside [0, count) - or outside [-count, count) when negative indices are allowed - raises

@@ -714,6 +714,131 @@ __device__ __forceinline__ void mfma_gemm_deep(const uint16_t* __restrict__ a, u
     mfma_store<uint16_t>(acc, bias, c, ldc, m_total, n_total, c_rows, m0, n0);
 }
 
+// bfloat16 with a k-contiguous B, K a multiple of 64 and 16-byte aligned rows, on kDirectThreads threads
+// (8 waves as 4 x 2, each a 32 x 64 part of the 128 x 128 tile). Each 64-deep slice goes from global memory
+// straight into LDS (global_load_lds_dwordx4: no staging registers and no LDS store instructions, which
+// took a third of the time of the register-staged bodies), double-buffered: the next slice's copies are
+// issued at the start of a step and waited for only at its end, and the second half's fragments are read
+// while the first half's MFMAs issue. LDS layout as ``deep_lds``: the lane that fills LDS position p of
+// a tile row fetches the global chunk p ^ (row & 7). Rows past the tile's edge repeat the last valid row
+// (never stored). The MFMA sequence per accumulator is the 64-deep path's.
+constexpr uint32_t kDirectThreads = 512;
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void global_void;
+
+template <class T>
+__device__ __forceinline__ void mfma_gemm_direct(const uint16_t* __restrict__ a, uint32_t lda, const uint16_t* __restrict__ b,
+                                                 uint32_t ldb, const T* __restrict__ bias, T* __restrict__ c, uint32_t ldc,
+                                                 uint32_t m_total, uint32_t n_total, uint32_t k_total, const int32_t* __restrict__ a_rows,
+                                                 const int32_t* __restrict__ c_rows, uint32_t m0, uint32_t n0) {
+    constexpr int WM = 4, WN = 2, WAVES = WM * WN, BM = 128, BN = 128;
+    constexpr int TM = BM / WM / 16, TN = BN / WN / 16;  // 16 x 16 tiles per wave: 2 x 4
+    constexpr int BLOCKS = BM / 8 / WAVES;                // 8-row (1 KB) blocks each wave copies per operand per slice
+    __shared__ __attribute__((aligned(16))) uint16_t as[2][BM * 64];
+    __shared__ __attribute__((aligned(16))) uint16_t bs[2][BN * 64];
+    const uint32_t tid = threadIdx.x, lane = tid % 64u, wave = tid / 64u;
+    const uint32_t wm = wave / WN, wn = wave % WN;
+    if (m0 >= m_total) {
+        return;
+    }
+    const uint16_t* ga[BLOCKS];
+    const uint16_t* gb[BLOCKS];
+#pragma unroll
+    for (int i = 0; i < BLOCKS; ++i) {
+        const uint32_t row = (i * WAVES + wave) * 8u + lane / 8u;
+        const uint32_t chunk = (lane % 8u) ^ (row & 7u);
+        const uint32_t gm = m0 + row < m_total ? m0 + row : m_total - 1u;
+        const uint32_t gn = n0 + row < n_total ? n0 + row : n_total - 1u;
+        ga[i] = a + (a_rows ? size_t(a_rows[gm]) : size_t(gm)) * lda + chunk * 8u;
+        gb[i] = b + size_t(gn) * ldb + chunk * 8u;
+    }
+    auto copy = [&](int buffer, uint32_t k0) {
+#pragma unroll
+        for (int i = 0; i < BLOCKS; ++i) {
+            __builtin_amdgcn_global_load_lds((global_void*)(ga[i] + k0), (lds_void*)&as[buffer][(i * WAVES + wave) * 512u], 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((global_void*)(gb[i] + k0), (lds_void*)&bs[buffer][(i * WAVES + wave) * 512u], 16, 0, 0);
+        }
+    };
+    auto fragments = [&](int buffer, int half, bf16x8_t (&fa)[TM], bf16x8_t (&fb)[TN]) {
+        const uint32_t chunk = half * 4u + lane / 16u;
+#pragma unroll
+        for (int t = 0; t < TM; ++t) {
+            fa[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(&as[buffer][deep_lds(wm * (BM / WM) + t * 16u + lane % 16u, chunk)]));
+        }
+#pragma unroll
+        for (int t = 0; t < TN; ++t) {
+            fb[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(&bs[buffer][deep_lds(wn * (BN / WN) + t * 16u + lane % 16u, chunk)]));
+        }
+    };
+    f32x4_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
+    const uint32_t steps = k_total / 64u;
+    copy(0, 0);
+    __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): the first slice is in LDS
+    __syncthreads();
+    bf16x8_t fa0[TM], fb0[TN], fa1[TM], fb1[TN];
+    fragments(0, 0, fa0, fb0);
+    for (uint32_t step = 0; step < steps; ++step) {
+        const int buffer = step & 1;
+        const bool more = step + 1 < steps;
+        if (more) {
+            copy(buffer ^ 1, (step + 1) * 64u);  // the other buffer was last read before the previous barrier
+        }
+        fragments(buffer, 1, fa1, fb1);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa0[i], fb0[j], acc[i][j], 0, 0, 0);
+            }
+        }
+        // one fragment read of the second half between pairs of the first half's MFMAs
+#pragma unroll
+        for (int g = 0; g < TM + TN; ++g) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa1[i], fb1[j], acc[i][j], 0, 0, 0);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): the next slice has landed
+        __syncthreads();
+        if (more) {
+            fragments(buffer ^ 1, 0, fa0, fb0);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const uint32_t gn = n0 + wn * (BN / WN) + j * 16u + lane % 16u;
+        if (gn >= n_total) {
+            continue;
+        }
+        const float offset = bias ? load1<T>(bias + gn) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t gm = m0 + wm * (BM / WM) + i * 16u + (lane / 16u) * 4u + r;
+                if (gm < m_total) {
+                    const size_t crow = c_rows ? size_t(c_rows[gm]) : size_t(gm);
+                    store1<T>(c + crow * ldc + gn, acc[i][j][r] + offset);
+                }
+            }
+        }
+    }
+}
+
 template <class T, bool B_K_CONTIGUOUS>
 __device__ __forceinline__ void mfma_gemm_sliced(const T* __restrict__ a, uint32_t lda, const T* __restrict__ b, uint32_t ldb,
                                                  const T* __restrict__ bias, T* __restrict__ c, uint32_t ldc, uint32_t m_total,
@@ -828,19 +953,28 @@ __device__ __forceinline__ void mfma_gemm_sliced(const T* __restrict__ a, uint32
     mfma_store<T>(acc, bias, c, ldc, m_total, n_total, c_rows, m0, n0);
 }
 
-// PATH 0 takes the 64-deep bfloat16 path whenever its conditions hold; PATH 1 always takes the sliced one.
+// PATH 0 takes the 64-deep bfloat16 path whenever its conditions hold; PATH 1 always takes the sliced one;
+// PATH 2 is the direct-to-LDS body (kDirectThreads threads), for bfloat16 with a k-contiguous B, K % 64 = 0
+// and lda, ldb multiples of 8, which the code generator guarantees before it selects it.
 template <class T, bool B_K_CONTIGUOUS, int PATH = 0>
 __device__ __forceinline__ void mfma_gemm(const T* __restrict__ a, uint32_t lda, const T* __restrict__ b, uint32_t ldb,
                                           const T* __restrict__ bias, T* __restrict__ c, uint32_t ldc, uint32_t m_total,
                                           uint32_t n_total, uint32_t k_total, const int32_t* __restrict__ a_rows,
                                           const int32_t* __restrict__ c_rows, uint32_t m_base, uint32_t n_base) {
+    if constexpr (PATH == 2) {
+        static_assert(sizeof(T) == 2 && B_K_CONTIGUOUS, "the direct-to-LDS body takes bfloat16 with a k-contiguous B");
+        mfma_gemm_direct<T>(a, lda, b, ldb, bias, c, ldc, m_total, n_total, k_total, a_rows, c_rows, m_base, n_base);
+        return;
+    }
     if constexpr (sizeof(T) == 2 && B_K_CONTIGUOUS && PATH == 0) {
         if (k_total % 64u == 0 && lda % 8u == 0 && ldb % 8u == 0) {
             mfma_gemm_deep(a, lda, b, ldb, bias, c, ldc, m_total, n_total, k_total, a_rows, c_rows, m_base, n_base);
             return;
         }
     }
-    mfma_gemm_sliced<T, B_K_CONTIGUOUS>(a, lda, b, ldb, bias, c, ldc, m_total, n_total, k_total, a_rows, c_rows, m_base, n_base);
+    if constexpr (PATH != 2) {
+        mfma_gemm_sliced<T, B_K_CONTIGUOUS>(a, lda, b, ldb, bias, c, ldc, m_total, n_total, k_total, a_rows, c_rows, m_base, n_base);
+    }
 }
 
 // XCD-aware tile order. Workgroups are handed to the 8 XCDs (each with its own L2) round-robin by

@@ -99,7 +99,10 @@ def test_linear_kernel_selection():
     assert "linear_tiled" in lower(torch.nn.Linear(17, 7).eval(), torch.ones(40, 17)).files["model.hip"]
     # rows that are not a whole number of 16-byte chunks keep the 4-element skinny kernel
     assert "linear_skinny" in lower(torch.nn.Linear(12, 7).bfloat16().eval(), torch.ones(3, 12, dtype=torch.bfloat16)).files["model.hip"]
-    assert "mfma_linear<uint16_t, 0>" in lower(torch.nn.Linear(64, 7).bfloat16().eval(), torch.ones(40, 64, dtype=torch.bfloat16)).files["model.hip"]
+    # bfloat16 with K a multiple of 64 takes the direct-to-LDS body on 512 threads; other K the register-staged ones
+    direct = lower(torch.nn.Linear(64, 7).bfloat16().eval(), torch.ones(40, 64, dtype=torch.bfloat16)).files["model.hip"]
+    assert "mfma_linear<uint16_t, 2>" in direct and "__launch_bounds__(512, 4)" in direct
+    assert "mfma_linear<uint16_t, 0>" in lower(torch.nn.Linear(40, 7).bfloat16().eval(), torch.ones(40, 40, dtype=torch.bfloat16)).files["model.hip"]
     # bfloat16 keeps float accumulation in both paths
     generated = lower(torch.nn.Linear(17, 7).bfloat16().eval(), torch.ones(3, 5, 17, dtype=torch.bfloat16))
     assert generated.inputs[0]["dtype"] == "bfloat16" and generated.outputs[0]["dtype"] == "bfloat16"

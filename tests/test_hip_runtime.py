@@ -9,6 +9,7 @@ returns the given arrays, that a later call leaves earlier results untouched, an
 from __future__ import annotations
 
 import math
+import shutil
 import subprocess
 import sys
 from pathlib import Path
@@ -744,7 +745,7 @@ def test_jit(tmp_path):
 
 
 # ------------------------------------------------------------------------- C5 (20B-shaped, bf16) slice
-def test_gpt_oss_20b_slice_decoder(tmp_path):
+def test_gpt_oss_20b_slice_decoder(tmp_path, request):
     """C5 at full width on a reduced slice, in bfloat16 against the oracle's decoder: hidden 2880, 64 query
     / 8 KV heads of 64, SwiGLU experts of 2880 with top-4 routing, vocabulary 201,088, a sliding-window
     layer and a full-attention layer. Left out: 22 of 24 layers and 24 of 32 experts, and the 4096-position
@@ -754,6 +755,7 @@ def test_gpt_oss_20b_slice_decoder(tmp_path):
     from chroma_amd.models.dev import make_gpt_oss_20b
 
     model = make_gpt_oss_20b(2, num_hidden_layers=2, num_experts=8)
+    request.addfinalizer(lambda: shutil.rmtree(tmp_path, ignore_errors=True))  # several GB of weights
     context, chunk = 64, 32
     graphs = [export_cached(model, context, chunk), export_cached(model, context, 1)]
     hip = [chroma_amd.compile(g, tmp_path / f"hip{i}") for i, g in enumerate(graphs)]
@@ -810,7 +812,7 @@ def router_near_ties(model, tokens: torch.Tensor, ulps: float = 4.0) -> Tuple[se
 
 
 @pytest.mark.parametrize("layer", ["window", "full"])
-def test_gpt_oss_20b_block_matches_oracle(tmp_path, layer):
+def test_gpt_oss_20b_block_matches_oracle(tmp_path, layer, request):
     """One C5 block at full width - hidden 2880, 64/8 heads of 64, all 32 experts with top-4 routing - on a
     128-token prefill (matrix-core attention, expert-grouped matrix-core products), a sliding-window
     (window 16) or a full-attention layer: the hidden state of every token against the oracle element-wise
@@ -829,6 +831,7 @@ def test_gpt_oss_20b_block_matches_oracle(tmp_path, layer):
     tokens = torch.randint(0, 201088, (128,), generator=torch.Generator().manual_seed(2))
     exported = torch.export.export(HiddenStates(model).eval(), (tokens,))
     exempt, eager = router_near_ties(model, tokens)
+    request.addfinalizer(lambda: shutil.rmtree(tmp_path, ignore_errors=True))  # several GB of weights
     with chroma_amd.compile(exported, tmp_path / "hip") as program:
         assert program.stats["mfma_matmuls"] >= 5 and program.stats["expert_contractions"] == 2
         got = as_float(program(tokens))
@@ -842,7 +845,7 @@ def test_gpt_oss_20b_block_matches_oracle(tmp_path, layer):
     np.testing.assert_allclose(got[checked], want[checked], rtol=2e-2, atol=max(1e-2, 2 * noise))
 
 
-def test_gpt_oss_20b_full_shape_decoder(tmp_path):
+def test_gpt_oss_20b_full_shape_decoder(tmp_path, request):
     """C5 at its full shape (24 layers, 32 experts, 4096-position cache, 201,088-entry vocabulary, weights
     N(0, 0.02) seed 2 drawn on the GPU) through ``Decoder``: A prefills 2048 tokens; B prefills the first
     2047 (a padded chunk) and decodes the last one.
@@ -861,8 +864,11 @@ def test_gpt_oss_20b_full_shape_decoder(tmp_path):
 
     model = make_gpt_oss_20b(2, generator_device="cuda")
     torch.cuda.empty_cache()
+    # the artifacts hold 42 GB of weights: removed at the end, pass or fail (pytest keeps tmp_path)
+    request.addfinalizer(lambda: shutil.rmtree(tmp_path, ignore_errors=True))
     programs = [chroma_amd.compile(export_cached(model, 4096, 2048), tmp_path / "prefill"),
                 chroma_amd.compile(export_cached(model, 4096, 1), tmp_path / "decode")]
+    request.addfinalizer(lambda: [program.close() for program in programs])
     del model
     tokens = torch.randint(0, 201088, (2048,), generator=torch.Generator().manual_seed(2)).numpy()
     prefill, decode = programs
@@ -887,8 +893,6 @@ def test_gpt_oss_20b_full_shape_decoder(tmp_path):
     np.testing.assert_allclose(step_values[0, 0], a_values[0, 2047], rtol=2e-2, atol=1e-2)
     assert np.isfinite(a_logits).all() and np.isfinite(b_logits).all()
     assert np.corrcoef(a_logits.ravel(), b_logits.ravel())[0, 1] >= 0.9
-    for program in programs:
-        program.close()
 
 
 # ----------------------------------------------------------------------------------- fused attention
