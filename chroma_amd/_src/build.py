@@ -30,7 +30,10 @@ from chroma_amd._src.native import DEVICE_INCLUDE
 from chroma_amd._src.spec import MANIFEST_VERSION, signature
 
 # -ffp-contract=off keeps every fused chain's multiply and add separately rounded, as the reference
-# backends do; packed fp32 ALU forms are disabled (they are avoided on this hardware pool).
+# backends do; packed fp32 ALU forms are disabled (they are avoided on this hardware pool). MFMA
+# accumulators are allocated in VGPRs: with the AGPR form the register allocator rotates the wide GEMM
+# body's 192 loop-carried accumulators through copies every stage (the other kernels allocate the same
+# either way).
 DEVICE_FLAGS = [
     "--genco",
     "-O3",
@@ -40,6 +43,8 @@ DEVICE_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form=1",
 ]
 
 

@@ -64,7 +64,14 @@ TRANSCENDENTAL_OPS = frozenset({"sin", "cos", "exp", "tanh", "sigmoid", "silu", 
 STORED_TABLE_ELEMENTS = 4096  # multi-consumer expressions with such ops and at least this many elements are stored
 MFMA_CUS = 256  # compute units of the target (MI355X), for the tile-round choice of the matrix-core products
 DIRECT_GEMM_THREADS = 512  # chroma::kDirectThreads: the direct-to-LDS matrix-core body's 8 waves
-DIRECT_GEMM_WAVES = 4  # waves per SIMD it is compiled for (two 64 KiB-LDS workgroups per compute unit)
+# minimum resident workgroups per compute unit it is compiled for (__launch_bounds__'s second argument):
+# two 64 KiB-LDS workgroups of 8 waves, i.e. 4 waves per SIMD and up to 128 VGPRs each
+DIRECT_GEMM_BLOCKS = 2
+WIDE_GEMM_THREADS = 256  # chroma::kWideThreads: the wide matrix-core body's 4 waves, one 140 KiB-LDS workgroup per CU
+WIDE_GEMM_TILE = (256, 192)  # chroma::kWideM, kWideN
+# the wide body takes dense products with at least this many of its tiles: below that its larger tiles
+# leave too much of the chip idle and the 128 x 128 body is faster
+WIDE_GEMM_MIN_TILES = 200
 REUSED_EVALUATIONS = 1 << 18  # a contraction operand is stored when (elements x reuse) reaches this
 SMALL_REDUCTION = 8  # contractions summing at most this many products are fused expressions...
 SMALL_OPERAND_COST = 8  # ...over operands that cost at most this much per element (others are stored)
@@ -1609,11 +1616,25 @@ class HIPCodegen(Codegen):
         # 32-deep body (three per CU), whose rounds quantize less
         path = 0 if tiles <= 2 * MFMA_CUS else 1
         threads = 256
+        if self._wide_gemm(out.dtype, inner, rows, columns):
+            wide_tiles = -(-rows // WIDE_GEMM_TILE[0]) * -(-columns // WIDE_GEMM_TILE[1])
+            k.min_waves = 1
+            k.line(f"chroma::mfma_linear_wide<{ctype_of(out.dtype)}>({args[0]}, {args[1]}, {args[2]}, {out_slot}, {rows}u, {columns}u, {inner}u);")
+            self.launch(k, 8 * -(-wide_tiles // 8), WIDE_GEMM_THREADS, [x, weight] + ([bias] if bias is not None else []), kind="linear_wide")
+            return
         if self._direct_gemm(out.dtype, inner):
             path, threads = 2, DIRECT_GEMM_THREADS
-            k.min_waves = DIRECT_GEMM_WAVES
+            k.min_waves = DIRECT_GEMM_BLOCKS
         k.line(f"chroma::mfma_linear<{ctype_of(out.dtype)}, {path}>({args[0]}, {args[1]}, {args[2]}, {out_slot}, {rows}u, {columns}u, {inner}u);")
         self.launch(k, 8 * -(-tiles // 8), threads, [x, weight] + ([bias] if bias is not None else []), kind="linear_mfma")
+
+    @staticmethod
+    def _wide_gemm(dtype: torch.dtype, inner: int, rows: int, columns: int) -> bool:
+        """The wide matrix-core body (``mfma_gemm_wide``) applies: bfloat16 operands whose contiguous rows
+        of ``inner`` elements split into 32-deep slices of 16-byte chunks, in a product large enough to give
+        it ``WIDE_GEMM_MIN_TILES`` tiles."""
+        tiles = -(-rows // WIDE_GEMM_TILE[0]) * -(-columns // WIDE_GEMM_TILE[1])
+        return dtype == torch.bfloat16 and inner % 32 == 0 and tiles >= WIDE_GEMM_MIN_TILES
 
     @staticmethod
     def _direct_gemm(dtype: torch.dtype, inner: int) -> bool:
@@ -2286,7 +2307,7 @@ class HIPCodegen(Codegen):
         path, threads = 1, 256
         if self._direct_gemm(out.dtype, inner):
             path, threads = 2, DIRECT_GEMM_THREADS
-            k.min_waves = DIRECT_GEMM_WAVES
+            k.min_waves = DIRECT_GEMM_BLOCKS
         k.line(
             f"chroma::grouped_expert_linear<{ctype_of(out.dtype)}, {str(per_slot).lower()}, {path}>({w}, {xs}, {out_slot}, "
             f"reinterpret_cast<const int32_t*>({table}), {tokens * selected}u, {selected}u, {experts}u, {channels}u, {inner}u);"

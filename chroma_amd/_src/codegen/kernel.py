@@ -182,7 +182,8 @@ class Kernel:
         self.indent = 1
         self.definitions: Dict[str, Tuple[str, "Aff", int]] = {}  # opaque atom -> (op, operand, constant)
         self.uses_error = False
-        # Waves per SIMD the register allocation must leave room for (0: the compiler's choice); a
+        # Workgroups per compute unit the register allocation must leave room for (__launch_bounds__'s
+        # second argument; 0: the compiler's choice): with 256 threads, n workgroups are n waves per SIMD. A
         # latency-bound kernel trades a few registers for more resident workgroups.
         self.min_waves = 0
         self.streaming = False  # vector float stores bypass the caches (results read by later kernels only)

@@ -4,6 +4,7 @@
 #pragma once
 
 #include <type_traits>
+#include <utility>
 
 #include "device.h"
 
@@ -783,6 +784,19 @@ __device__ __forceinline__ void mfma_gemm_direct(const uint16_t* __restrict__ a,
     copy(0, 0);
     __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): the first slice is in LDS
     __syncthreads();
+    if (m0 + wm * (BM / WM) >= m_total) {
+        // every row of this wave's part lies past the tile's edge (a ragged expert tile): it only copies
+        // its share of each slice and keeps the workgroup's barriers; the MFMA pipe and LDS reads it leaves
+        // free go to the other resident workgroup
+        for (uint32_t step = 0; step < steps; ++step) {
+            if (step + 1 < steps) {
+                copy((step & 1) ^ 1, (step + 1) * 64u);
+            }
+            __builtin_amdgcn_s_waitcnt(0xF70);
+            __syncthreads();
+        }
+        return;
+    }
     bf16x8_t fa0[TM], fb0[TN], fa1[TM], fb1[TN];
     fragments(0, 0, fa0, fb0);
     for (uint32_t step = 0; step < steps; ++step) {
@@ -837,6 +851,171 @@ __device__ __forceinline__ void mfma_gemm_direct(const uint16_t* __restrict__ a,
             }
         }
     }
+}
+
+// Compile-time index loops: ``unroll<N>(fn)`` calls fn(integral_constant<int, 0>) ... fn(<N - 1>), so every
+// register array below is indexed by constants before any optimisation runs (a runtime-indexed private
+// array is placed in memory instead of registers).
+template <class Fn, int... I>
+__device__ __forceinline__ void unroll_impl(Fn&& fn, std::integer_sequence<int, I...>) {
+    (fn(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class Fn>
+__device__ __forceinline__ void unroll(Fn&& fn) {
+    unroll_impl(fn, std::make_integer_sequence<int, N>{});
+}
+
+// Wide bfloat16 body for large products: a kWideM x kWideN (256 x 192) tile on kWideThreads threads, 4
+// waves as 2 x 2, each wave a 128 x 96 part (8 x 6 MFMA tiles, 192 accumulator registers). K advances in
+// 32-deep stages copied global -> LDS directly (global_load_lds_dwordx4) into a 5-slot ring (3 stages in
+// flight, 140 KiB, one workgroup per CU). A stage's 7 copies per wave are spread one per MFMA row, the
+// next stage's fragments are read right after their last use (A fragment i after MFMA row i, B fragments
+// during the last row), and stage s refills the slot stage s-1 used: every wave consumed those fragments
+// in its stage s-1 MFMAs before the barrier that opens stage s. The larger tile reads 0.29 KB of LDS and
+// copies 0.15 KB per MFMA (the 128 x 128 body: 0.75 and 0.25), which the measured LDS and copy throughput
+// of a compute unit favour. LDS rows are 64 B; the 16-byte chunk c of row r sits at position
+// c ^ wide_swizzle(r), so a fragment read (16 rows x 64 B) touches distinct banks both when 16 lanes share
+// a 256-byte bank cycle and when 8 lanes share 128 bytes. MFMA operands are swapped (W fragment first) so a
+// lane holds 4 consecutive output columns of one row and stores them as one 8-byte write. Each output
+// element accumulates the same 32-deep MFMA sequence as the 64-deep bodies. Requires bfloat16, a
+// k-contiguous B, K % 32 = 0 and lda, ldb multiples of 8.
+constexpr uint32_t kWideThreads = 256, kWideM = 256, kWideN = 192;
+
+__device__ __forceinline__ uint32_t wide_swizzle(uint32_t row) { return ((row >> 2) ^ (row >> 1)) & 3u; }
+
+// s_waitcnt immediate waiting for at most n outstanding vector-memory operations (lgkm and exp counts free)
+constexpr int16_t vmcnt_wait(uint32_t n) { return int16_t((n & 15u) | ((n >> 4) << 14) | 0x70u | 0xF00u); }
+
+template <class T>
+__device__ __forceinline__ void mfma_gemm_wide(const uint16_t* __restrict__ a, uint32_t lda, const uint16_t* __restrict__ b,
+                                               uint32_t ldb, const T* __restrict__ bias, T* __restrict__ c, uint32_t ldc,
+                                               uint32_t m_total, uint32_t n_total, uint32_t k_total,
+                                               const int32_t* __restrict__ a_rows, const int32_t* __restrict__ c_rows, uint32_t m0,
+                                               uint32_t n0) {
+    static_assert(sizeof(T) == 2, "the wide body takes bfloat16");
+    constexpr int BM = kWideM, BN = kWideN, WM = 2, WN = 2, WAVES = WM * WN, S = 5;
+    constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
+    constexpr int CA = BM / 16 / WAVES, CB = BN / 16 / WAVES, PER = CA + CB;  // 1 KB copies per wave per stage
+    constexpr int SLOT = (BM + BN) * 32;                                       // bf16 elements per ring slot
+    static_assert(CA * 16 * WAVES == BM && CB * 16 * WAVES == BN && PER <= TM, "one copy per MFMA row");
+    __shared__ __attribute__((aligned(1024))) uint16_t ring[S * SLOT];
+    const uint32_t lane = threadIdx.x % 64u, wave = threadIdx.x / 64u;
+    const uint32_t wm = wave / WN, wn = wave % WN;
+    // copy i moves 16 rows x 64 B: lane -> row block * 16 + lane / 4, LDS position lane % 4
+    const uint16_t* src[PER];
+    uint32_t dst[PER];
+    unroll<PER>([&](auto ic) {
+        constexpr int i = ic;
+        const uint32_t block = (i < CA ? i : i - CA) * WAVES + wave;
+        const uint32_t row = block * 16u + lane / 4u;
+        const uint32_t chunk = (lane % 4u) ^ wide_swizzle(row);
+        if constexpr (i < CA) {
+            const uint32_t g = m0 + row < m_total ? m0 + row : m_total - 1u;
+            src[i] = a + (a_rows ? size_t(a_rows[g]) : size_t(g)) * lda + chunk * 8u;
+            dst[i] = block * 512u;
+        } else {
+            const uint32_t g = n0 + row < n_total ? n0 + row : n_total - 1u;
+            src[i] = b + size_t(g) * ldb + chunk * 8u;
+            dst[i] = BM * 32u + block * 512u;
+        }
+    });
+    uint32_t oa[TM], ob[TN];
+    unroll<TM>([&](auto t) {
+        const uint32_t row = wm * (BM / WM) + t * 16u + lane % 16u;
+        oa[t] = row * 32u + (((lane / 16u) ^ wide_swizzle(row)) * 8u);
+    });
+    unroll<TN>([&](auto t) {
+        const uint32_t row = wn * (BN / WN) + t * 16u + lane % 16u;
+        ob[t] = BM * 32u + row * 32u + (((lane / 16u) ^ wide_swizzle(row)) * 8u);
+    });
+    const uint32_t steps = k_total / 32u;
+    // stages past the end re-copy the last stage into a slot that is never read again
+    auto k_of = [&](uint32_t stage) { return (stage < steps ? stage : steps - 1u) * 32u; };
+    auto copy = [&](auto ic, uint32_t slot, uint32_t k0) {
+        constexpr int i = ic;
+        __builtin_amdgcn_global_load_lds((global_void*)(src[i] + k0), (lds_void*)(ring + slot * SLOT + dst[i]), 16, 0, 0);
+    };
+    unroll<S - 1>([&](auto st) { unroll<PER>([&](auto i) { copy(i, uint32_t(st), k_of(st)); }); });
+    __builtin_amdgcn_s_waitcnt(vmcnt_wait(3 * PER));  // stage 0 landed
+    __builtin_amdgcn_s_barrier();
+    bf16x8_t fa[TM], fb[TN];
+    unroll<TM>([&](auto t) { fa[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(ring + oa[t])); });
+    unroll<TN>([&](auto t) { fb[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(ring + ob[t])); });
+    f32x4_t acc[TM][TN];
+    unroll<TM>([&](auto i) { unroll<TN>([&](auto j) { acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}; }); });
+    for (uint32_t s = 0; s + 1u < steps; ++s) {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(vmcnt_wait(2 * PER));  // stage s+1 landed (s+2, s+3 may be in flight)
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        const uint16_t* next = ring + ((s + 1u) % S) * SLOT;
+        const uint32_t fill = (s + S - 1u) % S, k_fill = k_of(s + S - 1u);
+        unroll<TM - 1>([&](auto ic) {
+            constexpr int i = ic;
+            unroll<TN>([&](auto jc) {
+                constexpr int j = jc;
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
+                if constexpr (j == TN / 2 && i < PER) copy(ic, fill, k_fill);
+            });
+            fa[i] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(next + oa[i]));
+        });
+        unroll<TN>([&](auto jc) {
+            constexpr int j = jc;
+            acc[TM - 1][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[TM - 1], acc[TM - 1][j], 0, 0, 0);
+            if constexpr (j == TN / 2 && TM - 1 < PER) copy(std::integral_constant<int, TM - 1>{}, fill, k_fill);
+            fb[j] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(next + ob[j]));
+        });
+        fa[TM - 1] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(next + oa[TM - 1]));
+        // issue order: per row, half its MFMAs, its copy, the rest, one fragment read
+        unroll<TM - 1>([&](auto ic) {
+            __builtin_amdgcn_sched_group_barrier(0x008, TN / 2 + 1, 0);
+            if constexpr (int(ic) < PER) {
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, TN - TN / 2 - 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        });
+        unroll<TN>([&](auto jc) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if constexpr (int(jc) == TN / 2 && TM - 1 < PER) {
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        });
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    unroll<TM>([&](auto i) {
+        unroll<TN>([&](auto j) { acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0); });
+    });
+    __builtin_amdgcn_s_waitcnt(vmcnt_wait(0));  // re-copies of the last stage land before the workgroup ends
+    // lane holds row lane % 16 and columns 4 (lane / 16) .. + 3 of each 16 x 16 tile
+    const bool vector_rows = (ldc & 3u) == 0;
+    unroll<TM>([&](auto i) {
+        const uint32_t gm = m0 + wm * (BM / WM) + i * 16u + lane % 16u;
+        if (gm < m_total) {
+            T* row = c + (c_rows ? size_t(c_rows[gm]) : size_t(gm)) * ldc;
+            unroll<TN>([&](auto j) {
+                const uint32_t gn = n0 + wn * (BN / WN) + j * 16u + (lane / 16u) * 4u;
+                float v[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    v[r] = acc[i][j][r] + (bias && gn + r < n_total ? load1<T>(bias + gn + r) : 0.0f);
+                }
+                if (vector_rows && gn + 3u < n_total) {
+                    const uint32_t lo = uint32_t(f32_to_bf16(v[0])) | (uint32_t(f32_to_bf16(v[1])) << 16);
+                    const uint32_t hi = uint32_t(f32_to_bf16(v[2])) | (uint32_t(f32_to_bf16(v[3])) << 16);
+                    *reinterpret_cast<uint2*>(row + gn) = uint2{lo, hi};
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        if (gn + r < n_total) {
+                            store1<T>(row + gn + r, v[r]);
+                        }
+                    }
+                }
+            });
+        }
+    });
 }
 
 template <class T, bool B_K_CONTIGUOUS>
@@ -1008,6 +1187,26 @@ __device__ __forceinline__ void mfma_linear(const T* __restrict__ x, const T* __
     const uint32_t ty = first + within % height, tx = within / height;
     mfma_gemm<T, true, PATH>(x, k_total, w, k_total, bias, out, n_total, m_total, n_total, k_total, nullptr, nullptr, ty * 128u,
                              tx * 128u);
+}
+
+// A linear layer on the wide body: Y[M, N] = X[M, K] . W[N, K]^T (+ bias) in kWideM x kWideN tiles, launched
+// as 8 * ceil(tiles / 8) workgroups of kWideThreads; logical tiles run down groups of 4 row tiles before
+// the next column tile, so an XCD's concurrent tiles share X and W rows in its L2.
+template <class T>
+__device__ __forceinline__ void mfma_linear_wide(const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias,
+                                                 T* __restrict__ out, uint32_t m_total, uint32_t n_total, uint32_t k_total) {
+    const uint32_t gx = (n_total + kWideN - 1u) / kWideN, gy = (m_total + kWideM - 1u) / kWideM;
+    uint32_t logical;
+    if (!xcd_logical_tile(gx * gy, logical)) {
+        return;
+    }
+    constexpr uint32_t G = 4;
+    const uint32_t group = logical / (G * gx), first = group * G;
+    const uint32_t height = gy - first < G ? gy - first : G;
+    const uint32_t within = logical - group * G * gx;
+    const uint32_t ty = first + within % height, tx = within / height;
+    mfma_gemm_wide<T>(x, k_total, w, k_total, bias, out, n_total, m_total, n_total, k_total, nullptr, nullptr, ty * kWideM,
+                      tx * kWideN);
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -205,6 +205,26 @@ def test_matrix_core_linear(tmp_path, dtype, rows, inner, columns):
     assert_close(got, want, **tolerance(want))
 
 
+@pytest.mark.parametrize("rows, inner, columns", [(2048, 320, 4800), (2000, 96, 4803), (1800, 32, 5000), (2600, 512, 3901)])
+def test_wide_matrix_core_linear(tmp_path, rows, inner, columns):
+    """bfloat16 products on the wide 256 x 192 body against the oracle: whole tiles; ragged rows and columns
+    with an odd column count (element stores); K of 96 and 32 (fewer 32-deep stages than the copy ring holds,
+    so stages past the end are re-copied into slots never read); and a deeper ragged case."""
+    generator = torch.Generator().manual_seed(rows + inner + columns)
+    layer = torch.nn.Linear(inner, columns).eval()
+    with torch.no_grad():
+        layer.weight.copy_(torch.randn(columns, inner, generator=generator) * 0.05)
+        layer.bias.copy_(torch.randn(columns, generator=generator))
+    layer = layer.to(torch.bfloat16)
+    x = torch.randn(rows, inner, generator=generator).to(torch.bfloat16)
+    exported = torch.export.export(layer, (x,))
+    with chroma_amd.compile(exported, tmp_path / "hip") as model:
+        assert "chroma::mfma_linear_wide<uint16_t>" in (tmp_path / "hip" / "model.hip").read_text()
+        got = model(x)
+    want = compile_cpu(exported, tmp_path / "cpu")(numpy_of(x))
+    assert_close(got, want, **tolerance(want))
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_matrix_core_contractions(tmp_path, dtype):
     """Attention-shaped einsums on the batched MFMA path: k-contiguous and n-contiguous right operands,
