@@ -1113,7 +1113,8 @@ class HIPCodegen(Codegen):
         """Emit the prologue that fills ``__shared__ float array[rows * inner]`` with ``x`` row by row:
         element (r, c) is ``x`` at ``coords_of(r) + [c]``, evaluated through generated code (so views and
         fused expressions are read in place). Deferred norms that ``x`` depends on get their row scales
-        computed first. Ends with a workgroup barrier."""
+        computed first. Ends with a workgroup barrier. The prologue's threads exchange data through LDS only,
+        so its barriers publish LDS alone and leave a weight stream requested before it in flight."""
         waves = threads // 64
         resolved = []
         for buffer in sorted((self.sources[x.name] & self.pending_stores) - set(k.slots)):
@@ -1146,7 +1147,7 @@ class HIPCodegen(Codegen):
         # A buffer computed in place is evaluated once into LDS (every later read in this kernel, and
         # the first workgroup's store of it, come from there) ...
         if any([stage_rows(k.unstored[buffer], buffer) for buffer in resolved]):
-            k.line("__syncthreads();")
+            k.line("chroma::lds_barrier();")
         for buffer in resolved:
             expression = k.unstored[buffer]
             shape = _shape(expression.shape)
@@ -1171,7 +1172,7 @@ class HIPCodegen(Codegen):
             if loads and stage_rows(source, source.name):
                 staged_sources = True
         if staged_sources:
-            k.line("__syncthreads();")
+            k.line("chroma::lds_barrier();")
         k.norm_scales = {}
         for name in sorted(self.pending_of.get(x.name, frozenset())):
             if name in self.materialized:
@@ -1204,19 +1205,19 @@ class HIPCodegen(Codegen):
                     per_row = lanes // 64
                     k.line(f"__shared__ float {scales}_waves[{threads // 64}];")
                     k.line(f"if (threadIdx.x % 64u == 0u) {scales}_waves[threadIdx.x / 64u] = squares;")
-                    k.line("__syncthreads();")
+                    k.line("chroma::lds_barrier();")
                     k.line(f"if (nl == 0u && nr < {norm_rows}u) {{ float total = 0.0f; "
                            f"for (uint32_t w = 0; w < {per_row}u; ++w) total += {scales}_waves[nr * {per_row}u + w]; {scales}[nr] = {formula}; }}")
             k.norm_scales[name] = scales
         if k.norm_scales:
-            k.line("__syncthreads();")
+            k.line("chroma::lds_barrier();")
         k.line(f"__shared__ float {array}[{rows * inner}];")
         k.line("#pragma unroll 4")
         with k.block(f"for (uint32_t i = threadIdx.x; i < {rows * inner}u; i += {threads}u) {{"):
             i = Aff.of(Atom("i", rows * inner - 1))
             row, column = k.div(i, inner), k.mod(i, inner)
             k.line(f"{array}[i] = {k.emit(self.read(k, x, [*coords_of(row), column]))};")
-        k.line("__syncthreads();")
+        k.line("chroma::lds_barrier();")
         k.norm_scales = {}
 
     def _norm_kernel(self, meta, x: Value, weight: Value, epsilon: float) -> Value:
@@ -1479,11 +1480,12 @@ class HIPCodegen(Codegen):
         per_chunk = 16 // ITEMSIZE[x.dtype]
         chunks = inner // per_chunk if inner % per_chunk == 0 else 0
         lanes = next((l for l in (64, 32, 16, 8, 4, 2) if chunks and chunks % l == 0 and chunks // l >= 4), 1 if chunks else 0)
+        self._stage(k, source, 1, inner, lambda _r: k.unflatten(row, lead) if lead else [], 256)
         if lanes:
-            # the gate weights are requested before the prologue that stages the row
+            # the gate weights are requested after the prologue: vector loads complete in order, so a
+            # stream requested first would hold back every dependent load of the prologue behind it
             k.line(f"chroma::StreamStep<{inner}, {lanes}, 1, {ctype}> prefetched;")
             k.line(f"chroma::router_fetch<{columns}>(prefetched, {w_arg});")
-        self._stage(k, source, 1, inner, lambda _r: k.unflatten(row, lead) if lead else [], 256)
         b_arg = self._matrix_slot(k, bias) if bias is not None else "nullptr"
         logits = k.slot(x.name, x.dtype, writable=True, extent=self.extents[x.name])
         value_slot = k.slot(values.name, values.dtype, writable=True, extent=self.extents[values.name])
@@ -1580,10 +1582,12 @@ class HIPCodegen(Codegen):
         b_arg = self._matrix_slot(k, bias) if bias is not None else "nullptr"
         out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
         lead = tuple(x.shape[:-1])
-        # The first step of W is requested before the prologue, so the weight read overlaps it.
+        # W is requested after the prologue that stages X: vector loads complete in order, so a stream
+        # requested first makes every dependent load of the prologue wait for it (and queue behind it);
+        # measured on the GPT-OSS-20B decode products, the prologue then costs several times its own latency.
+        self._stage(k, x, rows, inner, lambda row: k.unflatten(row, lead) if lead else [], 256)
         k.line(f"chroma::StreamStep<{inner}, {lanes}, {steps}, {ctype_of(out.dtype)}> prefetched;")
         k.line(f"chroma::stream_linear_fetch(prefetched, {w_arg}, {columns}u);")
-        self._stage(k, x, rows, inner, lambda row: k.unflatten(row, lead) if lead else [], 256)
         k.line(
             f"chroma::stream_linear<{rows}, {inner}, {lanes}, {steps}, true, {ctype_of(out.dtype)}>("
             f"nullptr, xs, {w_arg}, {b_arg}, {out_slot}, {columns}u, prefetched);"
@@ -1725,7 +1729,7 @@ class HIPCodegen(Codegen):
     def _waves_attention(self, out, q, k_past, k_new, v_past, v_new, mask, sinks, scale, epilogue=None) -> Kernel:
         """The one-wave-per-query-head attention kernel. ``epilogue`` = (weight, bias, linear output, lanes,
         steps): the workgroup also multiplies its finished row (all heads, rounded as stored) by W^T from
-        LDS, with W's first step requested before the attention starts."""
+        LDS, with W requested once the attention is done."""
         tokens, kv_heads, group, dim = q.shape
         keys = (k_past.shape[0] if k_past is not None else 0) + k_new.shape[0]
         bf16 = out.dtype == torch.bfloat16
@@ -1734,9 +1738,7 @@ class HIPCodegen(Codegen):
         if epilogue is not None:
             weight, bias, linear_out, lanes, steps = epilogue
             ctype, inner, columns = ctype_of(out.dtype), group * dim, weight.shape[0]
-            prelude = [lambda k: f"chroma::StreamStep<{inner}, {lanes}, {steps}, {ctype}> prefetched;",
-                       lambda k: f"chroma::stream_block_fetch(prefetched, {self._matrix_slot(k, weight)}, {columns}u);",
-                       lambda k: f"__shared__ float attention_row[{inner}];"]
+            prelude = [lambda k: f"__shared__ float attention_row[{inner}];"]
             store_extra = [f"attention_row[g * {dim}u + d] = chroma::storage_round<{str(bf16).lower()}>(value);"]
         k, _, _ = self._attention_kernel(out, q, k_past, k_new, v_past, v_new, mask, sinks, None, prelude=prelude, store_extra=store_extra)
         k.line(f"chroma::attention_waves<{dim}, {group}, {str(bf16).lower()}>({keys}u, {float_literal(scale)}, "
@@ -1745,6 +1747,9 @@ class HIPCodegen(Codegen):
             b_arg = self._matrix_slot(k, bias) if bias is not None else "nullptr"
             out_slot = k.slot(linear_out.name, linear_out.dtype, writable=True, extent=self.extents[linear_out.name])
             k.line("__syncthreads();")
+            # W is requested once the attention is done (see _stream_linear)
+            k.line(f"chroma::StreamStep<{inner}, {lanes}, {steps}, {ctype}> prefetched;")
+            k.line(f"chroma::stream_block_fetch(prefetched, {self._matrix_slot(k, weight)}, {columns}u);")
             k.line(f"chroma::stream_block_linear<1, {inner}, {lanes}, {steps}, true, {ctype}>(nullptr, attention_row, "
                    f"{self._matrix_slot(k, weight)}, {b_arg}, {out_slot} + size_t(blockIdx.x) * {columns}u, {columns}u, prefetched);")
         return k
@@ -1854,6 +1859,8 @@ class HIPCodegen(Codegen):
                    f"load_q, {sources[0]}, {sources[1]}, load_mask, load_sink, {split}, "
                    f"{scores_slot} + (size_t(blockIdx.x) * {kv_heads}u + blockIdx.y) * {keys * group}u);")
             self.launch(k, (tokens, kv_heads, splits), 256, inputs + [stats, scores] + ([partial] if phase == 2 else []), kind=f"attention_decode{phase}")
+        # the splits are added in a launch of their own: a last-split combine needs a device-scope release
+        # in every split (an L2 write-back on this chip), which costs more than the launch
         k, _, row = self._attention_kernel(out, q, k_past, k_new, v_past, v_new, mask, sinks, (stats, partial, splits), loaders=False)
         table = k.slot(partial.name, torch.float32, extent=self.extents[partial.name])
         k.line(f"chroma::attention_combine<{dim}, {group}>({table} + {row} * {group * dim}u, {splits}u, store);")
@@ -2173,9 +2180,10 @@ class HIPCodegen(Codegen):
                 coords_of = lambda _row: [k.div(slot, selected), k.mod(slot, selected)]
             else:
                 coords_of = lambda _row: [k.div(slot, selected)]
+            # the slab is requested after the prologue (see _stream_linear)
+            self._stage(k, x, 1, inner, coords_of, 256)
             k.line(f"chroma::StreamStep<{inner}, {lanes}, {steps}, {ctype_of(out.dtype)}> prefetched;")
             k.line(f"chroma::stream_expert_fetch(prefetched, {w}, {idx}, {experts}u, {channels}u, error);")
-            self._stage(k, x, 1, inner, coords_of, 256)
             k.line(
                 f"chroma::stream_expert_linear<{inner}, {lanes}, {steps}, true, {ctype_of(out.dtype)}, {per_expert}>("
                 f"{w}, {idx}, nullptr, xs, {out_slot}, {selected}u, {experts}u, {channels}u, {blocks_per_slot}u, error, prefetched);"

@@ -355,12 +355,14 @@ template <class T> struct KeyRows {
 
 // Workgroup: 4 waves over keys [begin, end) of one (query row, key/value head). A key's D elements are
 // LPK lanes x one 16-byte chunk each (N elements), so a wave takes 64 / LPK consecutive keys per load and
-// every load instruction reads whole rows. Query heads' dot products meet through a butterfly over the
-// LPK lanes. PHASE 1 writes the masked scores of the keys ([keys][G] at ``scores``) and the split's
-// statistics; PHASE 2 merges every split's statistics with the sink, then writes the split's partial
-// p . v sums (``attention_combine`` adds the splits in order). A split whose mask is -inf for every key
-// and head reads no rows and writes no scores (its statistics are (-inf, 0) and its partial sums 0:
-// exactly what its keys contribute as long as their rows are finite).
+// every load instruction reads whole rows; the mask values of those keys are requested with them.
+// Query heads' dot products meet through a butterfly over the LPK lanes. PHASE 1 writes the masked
+// scores of the keys ([keys][G] at ``scores``) and the split's statistics; PHASE 2 merges every split's
+// statistics with the sink (32 lanes per head, each merging every 32nd split, then a butterfly: the loads
+// go out together instead of one dependent round trip per split), then writes the split's partial p . v
+// sums (``attention_combine`` adds the splits in order). A split whose mask is -inf for every key and head
+// reads no rows and writes no scores (its statistics are (-inf, 0) and its partial sums 0: exactly what
+// its keys contribute as long as their rows are finite).
 template <int PHASE, int D, int G, bool BF16, class T, class LoadQ, class LoadMask, class LoadSink>
 __device__ __forceinline__ void attention_decode(uint32_t begin, uint32_t end, uint32_t keys, float scale, LoadQ load_q, KeyRows<T> k_rows,
                                                  KeyRows<T> v_rows, LoadMask load_mask, LoadSink load_sink, AttentionSplit split,
@@ -427,11 +429,16 @@ __device__ __forceinline__ void attention_decode(uint32_t begin, uint32_t end, u
         }
         constexpr int U = 4;  // key steps whose rows are requested together
         for (uint32_t j0 = begin + wave * KPW + kq; j0 < end; j0 += U * WAVES * KPW) {
-            float kv[U][N];
+            float kv[U][N], mk[U][G];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const uint32_t j = j0 + u * WAVES * KPW;
-                chunk(k_rows, j < end ? j : end - 1, kv[u]);
+                const uint32_t jj = j < end ? j : end - 1;
+                chunk(k_rows, jj, kv[u]);
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    mk[u][g] = load_mask(jj, g);
+                }
             }
 #pragma unroll
             for (int u = 0; u < U; ++u) {
@@ -450,7 +457,7 @@ __device__ __forceinline__ void attention_decode(uint32_t begin, uint32_t end, u
                     }
                     const float s = storage_round<BF16>(dot);
                     const float s1 = storage_round<BF16>(s * scale);
-                    s2[g] = storage_round<BF16>(s1 + load_mask(j < end ? j : end - 1, g));
+                    s2[g] = storage_round<BF16>(s1 + mk[u][g]);
                 }
                 if (j < end) {
 #pragma unroll
@@ -487,16 +494,26 @@ __device__ __forceinline__ void attention_decode(uint32_t begin, uint32_t end, u
     } else {
         // The row's statistics: every split's, then the sink; the split is live if any head's own
         // statistics are.
+        static_assert(G * 32 <= WAVES * kWave, "one 32-lane group per query head");
         bool live = false;
-        if (tid < uint32_t(G)) {
+        {
+            const uint32_t g = tid / 32u, l = tid % 32u;
             float top = neg_inf, sum = 0.0f;
-            for (uint32_t w = 0; w < split.splits; ++w) {
-                softmax_stats_merge(top, sum, split.stats[(w * G + tid) * 2], split.stats[(w * G + tid) * 2 + 1]);
+            if (g < uint32_t(G)) {
+                for (uint32_t w = l; w < split.splits; w += 32u) {
+                    softmax_stats_merge(top, sum, split.stats[(w * G + g) * 2], split.stats[(w * G + g) * 2 + 1]);
+                }
             }
-            softmax_stats_add(top, sum, load_sink(tid));
-            peak_s[tid] = top;
-            total_s[tid] = sum;
-            live = split.stats[(split.split * G + tid) * 2] != neg_inf;
+#pragma unroll
+            for (int offset = 16; offset > 0; offset >>= 1) {
+                softmax_stats_merge(top, sum, __shfl_xor(top, offset, kWave), __shfl_xor(sum, offset, kWave));
+            }
+            if (g < uint32_t(G) && l == 0) {
+                softmax_stats_add(top, sum, load_sink(g));
+                peak_s[g] = top;
+                total_s[g] = sum;
+                live = split.stats[(split.split * G + g) * 2] != neg_inf;
+            }
         }
         float* partial = split.partial + size_t(split.split) * G * D;
         if (!__syncthreads_or(live)) {

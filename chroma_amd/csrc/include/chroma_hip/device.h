@@ -136,6 +136,15 @@ template <class Op> __device__ __forceinline__ float wave_reduce(float v, Op op)
     return op(__uint_as_float(halves[0]), __uint_as_float(halves[1]));  // lanes 0-31 + 32-63
 }
 
+// Workgroup barrier that publishes LDS only: the fences are restricted to the local address space, so
+// the wait before the barrier is lgkmcnt(0) and global loads still in flight (a weight stream requested
+// ahead of a staging prologue) are not waited for. For code whose threads exchange data through LDS only.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
     return wave_reduce(v, [](float a, float b) { return a + b; });
 }
