@@ -1128,6 +1128,16 @@ class HIPCodegen(Codegen):
             self.write_through_stores += 1
         budget = [LDS_STAGED_FLOATS - rows * inner]
 
+        def staging_loop(count: int, element: Callable[[List[Aff]], object], shape: Sequence[int]) -> None:
+            """Before a loop over ``count`` staged elements: element 0 is evaluated at the enclosing scope,
+            so row indices gathered through values that do not depend on the element (a token's id, the
+            selected experts) are loaded and checked once instead of once per unrolled batch (the unused
+            element-0 loads are dropped by the compiler); loops of up to 16 iterations are unrolled whole,
+            so every element's loads are in flight together."""
+            k.emit(element(k.unflatten(ZERO, shape) if shape else []))
+            iterations = -(-count // threads)
+            k.line(f"#pragma unroll {iterations if iterations <= 16 else 8}")
+
         def stage_rows(value: Value, key: str) -> bool:
             """Evaluate ``value`` once into a __shared__ float array (row-major) read in its place."""
             shape = _shape(value.shape)
@@ -1137,7 +1147,7 @@ class HIPCodegen(Codegen):
             budget[0] -= count
             array = k.fresh("hs")
             k.line(f"__shared__ float {array}[{count}];")
-            k.line(f"#pragma unroll {max(1, min(8, -(-count // threads)))}")
+            staging_loop(count, lambda coords: self.read(k, value, coords), shape if value.shape else [])
             with k.block(f"for (uint32_t i = threadIdx.x; i < {count}u; i += {threads}u) {{"):
                 i = Aff.of(Atom("i", count - 1))
                 k.line(f"{array}[i] = {k.emit(self.read(k, value, k.unflatten(i, shape) if value.shape else []))};")
@@ -1212,7 +1222,7 @@ class HIPCodegen(Codegen):
         if k.norm_scales:
             k.line("chroma::lds_barrier();")
         k.line(f"__shared__ float {array}[{rows * inner}];")
-        k.line("#pragma unroll 4")
+        staging_loop(rows * inner, lambda coords: self.read(k, x, [*coords_of(coords[0]), coords[1]]), (rows, inner))
         with k.block(f"for (uint32_t i = threadIdx.x; i < {rows * inner}u; i += {threads}u) {{"):
             i = Aff.of(Atom("i", rows * inner - 1))
             row, column = k.div(i, inner), k.mod(i, inner)
