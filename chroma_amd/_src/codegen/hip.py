@@ -2050,7 +2050,10 @@ class HIPCodegen(Codegen):
             # one workgroup per (16-query tile, KV head), one wave per query head: K/V/mask tiles staged once
             live = self._live_blocks(plan["mask"], tokens, keys, tile=(16, 64))
             k.line(f"a.live_blocks = reinterpret_cast<const uint8_t*>({k.slot(live.name, torch.int64, extent=self.extents[live.name])});")
-            k.line(f"chroma::attention_heads_mfma_bf16<{dim}, {group}>(a);")
+            # a power-of-two scale <= 1 makes the scaled score a bfloat16 value: its rounding is left out
+            mantissa, exponent = math.frexp(scale)
+            pow2 = mantissa == 0.5 and -64 <= exponent <= 1
+            k.line(f"chroma::attention_heads_mfma_bf16<{dim}, {group}, {'true' if pow2 else 'false'}>(a);")
             operands = [entry[0] for entry in plan.values() if entry is not None] + [live]
             self.launch(k, (-(-tokens // 16), kv_heads, 1), 64 * group, operands, kind="attention_heads")
         else:

@@ -10,8 +10,10 @@
 // scaled scores and the masked scores are rounded to the storage type, the softmax statistics are float,
 // each probability is exp(x - max) / sum rounded to the storage type before it meets V, and the output
 // sum is float. Two things differ from the reference: the order of the float sums, and, in the
-// matrix-core kernel only, the quotient, which is exp(x - max) times the float reciprocal of the sum
-// (within one ulp of the correctly rounded quotient before the rounding to the storage type).
+// matrix-core kernels only, the quotient, which is exp(x - max) times the float reciprocal of the sum
+// (attention_mfma_bf16: within one ulp of the correctly rounded quotient) or one exp2 whose exponent
+// carries log2 of the sum (attention_heads_mfma_bf16: within a few ulps), before the rounding to the
+// storage type.
 #pragma once
 
 #include "device.h"
@@ -910,40 +912,71 @@ template <int D> __device__ __forceinline__ void attention_mfma_bf16(const Atten
 // staged into LDS once and serve all G heads (the head-parallel form stages them once per head). Mask
 // shared by every head (mh = mg = 0). Same computation as attention_mfma_bf16 and the reference chain:
 // S^T = K . Q^T on v_mfma_f32_16x16x32_bf16, each score rounded to bfloat16, scaled and rounded, masked
-// and rounded (gfx950's v_cvt_pk_bf16_f32 rounds, to nearest even like f32_to_bf16); pass 1 accumulates
-// (max, sum of exp) per query in float, pass 2 forms p = exp(s - max) * (1 / sum) rounded to bfloat16
-// (within one ulp of the quotient) and O^T += V^T . P^T; the output is rounded once. The 64-key blocks a
-// query tile visits come from ``attention_live_tiles`` (blocks whose mask is -inf throughout are never
-// read); a visited block's next block is staged into the other LDS buffer while it is computed, so each
-// block costs one barrier. Key rows past ``keys`` are zeros with a -inf mask, queries past ``tokens`` see
-// only -inf and are not stored.
+// and rounded (gfx950's v_cvt_pk_bf16_f32 rounds two values at once, to nearest even like f32_to_bf16);
+// pass 1 accumulates (max, sum of exp) per query in float, pass 2 forms p = exp(s - max) / sum as
+// 2^(s log2(e) - max log2(e) - log2(sum)) - one multiply-add and one v_exp_f32, within a few float ulps
+// of the quotient, far below the bfloat16 rounding p then gets - and O^T += V^T . P^T; the output is
+// rounded once.
+// The 64-key blocks a query tile visits come from ``attention_live_tiles`` (blocks whose mask is -inf
+// throughout are never read); a visited block's next block is staged into the other LDS buffer while it
+// is computed, so each block costs one barrier. Key rows past ``keys`` are zeros with a -inf mask, queries
+// past ``tokens`` see only -inf and are not stored.
+//
+// Two steps of the chain are the identity where their operands allow it, and are then left out:
+//  * a block whose mask entries are all +0.0 or -0.0 (every causal block below the diagonal): adding a
+//    zero and rounding changes no bfloat16 value (only -0 may become +0, and every later use - a max, a
+//    difference with the max, exp - gives the same result for either zero), so the block reads no mask;
+//  * a power-of-two scale <= 1 (POW2; 1/8 at head dimension 64): the product of a bfloat16 value and the
+//    scale is a bfloat16 value whenever it is a normal float, so its rounding is left out and the scale
+//    is applied inside the one fused multiply-add that forms s - max. Below the normal range (|s| <
+//    2^-126) the unrounded product may differ from the rounded one in its last bits; every exp it feeds
+//    is then exp of a difference below 2^-25 in magnitude or of a difference the tiny term does not change,
+//    so the probabilities and the output are the same.
+// Scores are kept in "u" units: s = u * cs, with cs the scale when its rounding is left out, else 1
+// (u is then the masked score itself); u - max/cs never forms: s - max is fma(u, cs, -max), exact in u*cs.
 
 constexpr uint32_t kLiveTilesMax = 1024;  // 64-key blocks a workgroup lists in LDS (64K keys)
 
 // live_tiles[qt * key_blocks + kb] for queries [16 qt, 16 qt + 16) and keys [64 kb, 64 kb + 64) of a mask
-// shared by every head: 0 when every entry there is -inf, 1 otherwise (grid: query tiles x key blocks).
+// shared by every head: 0 when every entry there is -inf, 2 when every key of the block is below ``keys``
+// and every entry is a zero (+0.0 or -0.0), else 1 (grid: query tiles x key blocks).
 __device__ __forceinline__ void attention_live_tiles(const uint16_t* __restrict__ mask, uint32_t mt, uint32_t tokens, uint32_t keys,
                                                      uint8_t* __restrict__ live_tiles) {
     const uint32_t qt = blockIdx.x, kb = blockIdx.y;
-    bool any = false;
+    bool any = false, zero = kb * 64u + 64u <= keys;
     for (uint32_t i = threadIdx.x; i < 16u * 64u; i += blockDim.x) {
         const uint32_t t = qt * 16u + i / 64u, j = kb * 64u + i % 64u;
         if (t < tokens && j < keys) {
-            any |= mask[size_t(t) * mt + j] != 0xff80u;
+            const uint16_t bits = mask[size_t(t) * mt + j];
+            any |= bits != 0xff80u;
+            zero &= (bits & 0x7fffu) == 0u;
         }
     }
     any = __syncthreads_or(any);
+    zero = __syncthreads_and(zero);
     if (threadIdx.x == 0) {
-        live_tiles[qt * gridDim.y + kb] = any ? 1 : 0;
+        live_tiles[qt * gridDim.y + kb] = any ? (zero ? 2 : 1) : 0;
     }
 }
 
-template <int D, int G> __device__ __forceinline__ void attention_heads_mfma_bf16(const AttentionOperands& a) {
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Round two floats to bfloat16 with one v_cvt_pk_bf16_f32 and widen them back.
+__device__ __forceinline__ void round_bf16_pair(float& x, float& y) {
+    const uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{x, y}, bf16x2_t));
+    x = __uint_as_float(w << 16);
+    y = __uint_as_float(w & 0xffff0000u);
+}
+
+template <int D, int G, bool POW2> __device__ __forceinline__ void attention_heads_mfma_bf16(const AttentionOperands& a) {
     static_assert(D % 32 == 0 && D <= 128 && G >= 1 && G <= 8, "head dimension and group");
     constexpr int QT = 16, KB = 64, THREADS = 64 * G;
     constexpr int KPAD = D + 8, VPAD = KB + 8, MPAD = KB + 4;
     constexpr int CHUNKS = (KB * D / 8 + THREADS - 1) / THREADS;  // 16-byte K (and V) chunks per thread per block
     constexpr int MASKS = (QT * KB + THREADS - 1) / THREADS;      // mask entries per thread per block
+    constexpr uint32_t MASKED = 0x8000u;                           // list entry flag: the block reads its mask
+    constexpr float kLog2e = 1.44269504088896341f;
     __shared__ __attribute__((aligned(16))) uint16_t k_s[2][KB * KPAD];
     __shared__ __attribute__((aligned(16))) uint16_t v_s[2][D * VPAD];
     __shared__ __attribute__((aligned(16))) uint16_t m_s[2][QT * MPAD];
@@ -963,8 +996,9 @@ template <int D, int G> __device__ __forceinline__ void attention_heads_mfma_bf1
         qf[ks] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(a.q + size_t(qrow) * a.qt + kv * a.qh + g * a.qg + ks * 32u + quad * 8u));
     }
 
-    // The 64-key blocks this tile visits, in key order: wave 0 compacts its row of the live table with a
-    // ballot per 64 blocks; without a table (or past the list's capacity) every block.
+    // The 64-key blocks this tile visits, in key order, each with the MASKED flag unless its mask is all
+    // zeros: wave 0 compacts its row of the live table with a ballot per 64 blocks; without a table (or
+    // past the list's capacity) every block, each reading its mask.
     const uint32_t blocks = (a.keys + KB - 1) / KB;
     const bool listed = a.live_blocks != nullptr && blocks <= kLiveTilesMax;
     if (listed) {
@@ -973,10 +1007,11 @@ template <int D, int G> __device__ __forceinline__ void attention_heads_mfma_bf1
             uint32_t n = 0;
             for (uint32_t base = 0; base < blocks; base += 64u) {
                 const uint32_t kb = base + lane;
-                const bool on = kb < blocks && row[kb] != 0;
+                const uint32_t state = kb < blocks ? row[kb] : 0u;
+                const bool on = state != 0;
                 const unsigned long long bits = __ballot(on);
                 if (on) {
-                    live_list[n + uint32_t(__popcll(bits & ((1ull << lane) - 1ull)))] = uint16_t(kb);
+                    live_list[n + uint32_t(__popcll(bits & ((1ull << lane) - 1ull)))] = uint16_t(kb | (state == 1 ? MASKED : 0u));
                 }
                 n += uint32_t(__popcll(bits));
             }
@@ -987,35 +1022,45 @@ template <int D, int G> __device__ __forceinline__ void attention_heads_mfma_bf1
         __syncthreads();
     }
     const uint32_t visits = listed ? live_total : blocks;
-    auto block_of = [&](uint32_t i) -> uint32_t { return listed ? uint32_t(live_list[i]) : i; };
+    // (block index | MASKED) of visit i; uniform over the workgroup, so every branch on it is scalar
+    auto entry_of = [&](uint32_t i) -> uint32_t { return listed ? uint32_t(live_list[i]) : (i | MASKED); };
 
     // Global -> registers (every load unconditional, its index clamped; what lies out of range is replaced
     // when stored to LDS), then registers -> LDS buffer: K row-major, V transposed, mask [query][key].
     uint4 rk[CHUNKS], rv[CHUNKS];
     uint16_t rm[MASKS];
-    auto fetch = [&](uint32_t kb, bool values) {
+    auto fetch = [&](uint32_t entry, bool values) {
+        const uint32_t kb = entry & ~MASKED;
 #pragma unroll
         for (int i = 0; i < CHUNKS; ++i) {
             const uint32_t c = tid + i * THREADS;
             const uint32_t cc = c < uint32_t(KB * D / 8) ? c : 0u;
+            // K: 8 lanes per key row (a row's 16-byte chunks side by side); V: the 64 keys of one 8-column
+            // chunk side by side, so the transposed LDS writes of a wave are contiguous (see ``put``)
             const uint32_t r = cc / (D / 8), dc = (cc % (D / 8)) * 8u, j = kb * KB + r;
             const uint32_t jj = j < a.keys ? j : a.keys - 1u;
             const bool old = jj < a.past;
             const size_t kr = old ? size_t(jj) * a.kpj + kv * a.kph : size_t(jj - a.past) * a.knj + kv * a.knh;
             rk[i] = *reinterpret_cast<const uint4*>((old ? a.k_past : a.k_new) + kr + dc);
             if (values) {
-                const size_t vr = old ? size_t(jj) * a.vpj + kv * a.vph : size_t(jj - a.past) * a.vnj + kv * a.vnh;
-                rv[i] = *reinterpret_cast<const uint4*>((old ? a.v_past : a.v_new) + vr + dc);
+                const uint32_t vj = kb * KB + cc % KB, vdc = (cc / KB) * 8u;
+                const uint32_t vjj = vj < a.keys ? vj : a.keys - 1u;
+                const bool vold = vjj < a.past;
+                const size_t vr = vold ? size_t(vjj) * a.vpj + kv * a.vph : size_t(vjj - a.past) * a.vnj + kv * a.vnh;
+                rv[i] = *reinterpret_cast<const uint4*>((vold ? a.v_past : a.v_new) + vr + vdc);
             }
         }
+        if (entry & MASKED) {
 #pragma unroll
-        for (int i = 0; i < MASKS; ++i) {
-            const uint32_t e = tid + i * THREADS;
-            const uint32_t t = q0 + (e / KB) % QT, j = kb * KB + e % KB;
-            rm[i] = a.mask[size_t(t < a.tokens ? t : a.tokens - 1u) * a.mt + (j < a.keys ? j : a.keys - 1u)];
+            for (int i = 0; i < MASKS; ++i) {
+                const uint32_t e = tid + i * THREADS;
+                const uint32_t t = q0 + (e / KB) % QT, j = kb * KB + e % KB;
+                rm[i] = a.mask[size_t(t < a.tokens ? t : a.tokens - 1u) * a.mt + (j < a.keys ? j : a.keys - 1u)];
+            }
         }
     };
-    auto put = [&](int buffer, uint32_t kb, bool values) {
+    auto put = [&](int buffer, uint32_t entry, bool values) {
+        const uint32_t kb = entry & ~MASKED;
 #pragma unroll
         for (int i = 0; i < CHUNKS; ++i) {
             const uint32_t c = tid + i * THREADS;
@@ -1024,27 +1069,33 @@ template <int D, int G> __device__ __forceinline__ void attention_heads_mfma_bf1
                 const bool ok = kb * KB + r < a.keys;
                 *reinterpret_cast<uint4*>(&k_s[buffer][r * KPAD + dc]) = ok ? rk[i] : uint4{0, 0, 0, 0};
                 if (values) {
-                    const uint4 v = ok ? rv[i] : uint4{0, 0, 0, 0};
+                    // lanes hold consecutive keys vr of one chunk: each 2-byte store of a wave covers 128
+                    // contiguous bytes of a V^T row (no two lanes in one bank at different addresses)
+                    const uint32_t vr = c % KB, vdc = (c / KB) * 8u;
+                    const uint4 v = kb * KB + vr < a.keys ? rv[i] : uint4{0, 0, 0, 0};
                     const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
 #pragma unroll
                     for (int x = 0; x < 8; ++x) {
-                        v_s[buffer][(dc + x) * VPAD + r] = e[x];
+                        v_s[buffer][(vdc + x) * VPAD + vr] = e[x];
                     }
                 }
             }
         }
+        if (entry & MASKED) {
 #pragma unroll
-        for (int i = 0; i < MASKS; ++i) {
-            const uint32_t e = tid + i * THREADS;
-            if (e < uint32_t(QT * KB)) {
-                const uint32_t qr = e / KB, kc = e % KB;
-                const bool ok = q0 + qr < a.tokens && kb * KB + kc < a.keys;
-                m_s[buffer][qr * MPAD + kc] = ok ? rm[i] : uint16_t(0xff80u);
+            for (int i = 0; i < MASKS; ++i) {
+                const uint32_t e = tid + i * THREADS;
+                if (e < uint32_t(QT * KB)) {
+                    const uint32_t qr = e / KB, kc = e % KB;
+                    const bool ok = q0 + qr < a.tokens && kb * KB + kc < a.keys;
+                    m_s[buffer][qr * MPAD + kc] = ok ? rm[i] : uint16_t(0xff80u);
+                }
             }
         }
     };
-    // Masked scores of this lane: key 16 t + 4 quad + r of the block, query ``col`` of the tile.
-    auto scores = [&](int buffer, float (&s2)[4][4]) {
+    // Scores of this lane (key 16 t + 4 quad + r of the block, query ``col`` of the tile) in u units;
+    // returns cs (s = u * cs).
+    auto scores = [&](int buffer, uint32_t entry, float (&u)[4][4]) -> float {
         f32x4_t acc[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -1057,56 +1108,88 @@ template <int D, int G> __device__ __forceinline__ void attention_heads_mfma_bf1
         }
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            const uint2 m = *reinterpret_cast<const uint2*>(&m_s[buffer][col * MPAD + t * 16u + quad * 4u]);
-            const float mv[4] = {__uint_as_float(m.x << 16), __uint_as_float(m.x & 0xffff0000u), __uint_as_float(m.y << 16),
-                                 __uint_as_float(m.y & 0xffff0000u)};
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float s1 = round_bf16_fast(round_bf16_fast(acc[t][r]) * a.scale);
-                s2[t][r] = round_bf16_fast(s1 + mv[r]);
+            for (int r = 0; r < 4; r += 2) {
+                u[t][r] = acc[t][r];
+                u[t][r + 1] = acc[t][r + 1];
+                round_bf16_pair(u[t][r], u[t][r + 1]);
             }
         }
+        if (POW2 && !(entry & MASKED)) {
+            return a.scale;
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+#pragma unroll
+            for (int r = 0; r < 4; r += 2) {
+                if constexpr (!POW2) {
+                    u[t][r] *= a.scale;
+                    u[t][r + 1] *= a.scale;
+                    round_bf16_pair(u[t][r], u[t][r + 1]);
+                } else {
+                    u[t][r] *= a.scale;  // exact: a power-of-two scale, no rounding (see above)
+                    u[t][r + 1] *= a.scale;
+                }
+            }
+        }
+        if (entry & MASKED) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint2 m = *reinterpret_cast<const uint2*>(&m_s[buffer][col * MPAD + t * 16u + quad * 4u]);
+                u[t][0] += __uint_as_float(m.x << 16);
+                u[t][1] += __uint_as_float(m.x & 0xffff0000u);
+                u[t][2] += __uint_as_float(m.y << 16);
+                u[t][3] += __uint_as_float(m.y & 0xffff0000u);
+                round_bf16_pair(u[t][0], u[t][1]);
+                round_bf16_pair(u[t][2], u[t][3]);
+            }
+        }
+        return 1.0f;
     };
     // One pass over the visited blocks, the next block staged while the current one is computed.
     auto sweep = [&](bool values, auto&& body) {
         if (visits == 0) {
             return;
         }
-        fetch(block_of(0), values);
-        put(0, block_of(0), values);
-        fetch(block_of(visits > 1 ? 1u : 0u), values);
+        const uint32_t first = entry_of(0);
+        uint32_t next = entry_of(visits > 1 ? 1u : 0u);
+        fetch(first, values);
+        put(0, first, values);
+        fetch(next, values);
         __syncthreads();
+        uint32_t current = first;
         for (uint32_t i = 0; i < visits; ++i) {
-            body(int(i & 1u));
+            body(int(i & 1u), current);
             // registers hold block i + 1 (or re-read block i when it is the last, never stored)
             if (i + 1 < visits) {
-                put(int((i + 1) & 1u), block_of(i + 1), values);
+                put(int((i + 1) & 1u), next, values);
             }
-            const uint32_t ahead = i + 2 < visits ? i + 2 : visits - 1u;
-            fetch(block_of(ahead), values);
+            current = next;
+            next = entry_of(i + 2 < visits ? i + 2 : visits - 1u);
+            fetch(next, values);
             __syncthreads();
         }
     };
 
     float peak = neg_inf, total = 0.0f;
-    sweep(false, [&](int buffer) {
-        float s2[4][4];
-        scores(buffer, s2);
-        float top = peak;
+    sweep(false, [&](int buffer, uint32_t entry) {
+        float u[4][4];
+        const float cs = scores(buffer, entry, u);
+        float top = neg_inf;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                top = __builtin_fmaxf(top, s2[t][r]);
-            }
+            top = __builtin_fmaxf(top, __builtin_fmaxf(__builtin_fmaxf(u[t][0], u[t][1]), __builtin_fmaxf(u[t][2], u[t][3])));
         }
+        top = __builtin_fmaxf(peak, top * cs);  // exact: cs is 1 or a power of two
         if (top != neg_inf) {
+            // exp(s - top) = 2^(u * cs * log2(e) - top * log2(e)): one multiply-add per score
+            const float scale2 = cs * kLog2e, shift = -top * kLog2e;
             float sum = 0.0f;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    sum += fast_exp(s2[t][r] - top);
+                    sum += __builtin_amdgcn_exp2f(__builtin_fmaf(u[t][r], scale2, shift));
                 }
             }
             total = total * fast_exp(peak - top) + sum;
@@ -1119,23 +1202,33 @@ template <int D, int G> __device__ __forceinline__ void attention_heads_mfma_bf1
         softmax_stats_merge(peak, total, __shfl_xor(peak, offset, kWave), __shfl_xor(total, offset, kWave));
     }
     softmax_stats_add(peak, total, bf16_to_f32(a.sinks[kv * a.sh + g * a.sg]));
-    const float inverse = 1.0f / total;
+    // p = exp(s - peak) / total = 2^(s * log2(e) - (peak * log2(e) + log2(total))): the normalisation
+    // rides in the exponent's one multiply-add (v_log_f32 is log2). Only a row whose scores and sink are
+    // all -inf has total 0; its probabilities are NaN, as the reference's 0 / 0 is.
+    const float norm = -(peak * kLog2e + __builtin_amdgcn_logf(total));
 
     f32x4_t o[D / 16];
 #pragma unroll
     for (int dt = 0; dt < D / 16; ++dt) {
         o[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    sweep(true, [&](int buffer) {
-        float s2[4][4];
-        scores(buffer, s2);
+    sweep(true, [&](int buffer, uint32_t entry) {
+        float u[4][4];
+        const float scale2 = scores(buffer, entry, u) * kLog2e;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             // keys 32 h + (4 quad + r) and 32 h + 16 + (4 quad + r): this lane's B operand slots 0-3 and 4-7
-            bf16x8_t pf;
+            float e[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                pf[i] = __bf16(fast_exp(s2[2 * h + i / 4][i % 4] - peak) * inverse);
+                e[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(u[2 * h + i / 4][i % 4], scale2, norm));
+            }
+            bf16x8_t pf;
+#pragma unroll
+            for (int i = 0; i < 8; i += 2) {
+                const bf16x2_t pair = __builtin_convertvector(f32x2_t{e[i], e[i + 1]}, bf16x2_t);
+                pf[i] = pair[0];
+                pf[i + 1] = pair[1];
             }
 #pragma unroll
             for (int dt = 0; dt < D / 16; ++dt) {

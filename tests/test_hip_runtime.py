@@ -982,6 +982,39 @@ def test_fused_attention_matches_oracle(tmp_path, dtype, tokens, past, kv_heads,
     compare(got, want)
 
 
+@pytest.mark.parametrize("tokens, past, dim", [(200, 0, 64), (150, 70, 128)])
+def test_fused_attention_additive_mask(tmp_path, tokens, past, dim):
+    """A shared mask that is not only 0 / -inf: causal, with an additive bias on a band of keys (so some key
+    blocks need every step of the chain - the mask add and its rounding - while the blocks outside the band
+    are all zeros and leave both out), at a power-of-two scale (head dimension 64) and another (128);
+    bfloat16 against the oracle's unfused chain."""
+    generator = torch.Generator().manual_seed(tokens + past)
+    dtype = torch.bfloat16
+
+    def rand(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=generator) * scale).to(dtype)
+
+    keys = past + tokens
+    mask = torch.zeros(tokens, keys)
+    band = slice(max(0, keys // 2 - 40), keys // 2 + 24)
+    mask[:, band] = torch.randn(tokens, band.stop - band.start, generator=generator) * 0.7
+    for t in range(tokens):
+        mask[t, past + t + 1 :] = -math.inf
+    kv_heads, group = 2, 4
+    inputs = (rand(tokens, kv_heads, group, dim), rand(past or 1, kv_heads, dim), rand(tokens, kv_heads, dim),
+              rand(past or 1, kv_heads, dim), rand(tokens, kv_heads, dim), mask.to(dtype), rand(kv_heads * group, scale=2.0))
+    if not past:
+        module, inputs = FreshAttention(), (inputs[0], inputs[2], inputs[4], inputs[5], inputs[6])
+    else:
+        module = SinkAttention()
+    exported = torch.export.export(module, inputs)
+    with chroma_amd.compile(exported, tmp_path / "hip") as model:
+        assert model.stats["fused_attentions"] == 1 and model.stats["mfma_matmuls"] == 1
+        got = model(*inputs)
+    want = compile_cpu(exported, tmp_path / "cpu")(*[numpy_of(v) for v in inputs])
+    compare(got, want)
+
+
 class PerHeadAttention(torch.nn.Module):
     """Attention whose mask differs per query head ([kv, group, queries, keys])."""
 
