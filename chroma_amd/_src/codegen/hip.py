@@ -77,6 +77,7 @@ SMALL_REDUCTION = 8  # contractions summing at most this many products are fused
 SMALL_OPERAND_COST = 8  # ...over operands that cost at most this much per element (others are stored)
 MATRIX_MIN_WORK = 1 << 18  # smaller batched products stay on the generic contraction kernel
 GROUPED_SLOTS = 64  # from this many (token, expert) slots on, expert products are grouped by expert
+FUSED_ROUTER_BYTES = 32 << 10  # a router with gate weights up to this size is recomputed inside its first expert product
 MATRIX_ATTENTION_TOKENS = 64  # bfloat16 attention over at least this many queries runs on the matrix cores
 SPLIT_KEYS = 256  # keys per workgroup when an attention row's keys are split over workgroups
 DECODE_SPLIT_KEYS = 128  # the same for stored key/value rows read with 16-byte loads (decode steps)
@@ -162,6 +163,8 @@ class HIPCodegen(Codegen):
         self.pending_of: Dict[str, frozenset] = {}  # value -> deferred norms its expression reads
         self.retractable: Dict[str, tuple] = {}  # small linear output -> (launch index, x, weight, bias)
         self.router_weights: Dict[str, Value] = {}  # top-k values -> their softmax, written by the router
+        self.router_launches: Dict[str, dict] = {}  # router indices -> the router launch (for fusion into its expert product)
+        self.routed_experts = 0  # routers fused into their first expert product
         # Write-through stores: a small expression the front end asks to store gets its arena buffer at
         # once, but the buffer is written by the first kernel that reads it. A staging kernel computes the
         # expression itself and also stores it; any other reader has a copy kernel launched before it.
@@ -1509,6 +1512,9 @@ class HIPCodegen(Codegen):
         )
         self.launch(k, rows, 256, [source, weight] + ([bias] if bias is not None else []), kind="router")
         self.router_weights[values.name] = weights
+        self.router_launches[indices.name] = dict(index=len(self.launches) - 1, source=source, weight=weight, bias=bias, logits=x, values=values,
+                                                  indices=indices, weights=weights, rows=rows, columns=columns, inner=inner, lanes=lanes,
+                                                  largest=bool(largest), count=count)
         self.fused_routers += 1
         return True
 
@@ -2183,6 +2189,13 @@ class HIPCodegen(Codegen):
             # evaluated into LDS, then the selected expert's slab is streamed.
             lanes, steps = plan
             blocks_per_slot = max(1, min(-(-(-(-channels // (64 // lanes * steps))) // 4), STREAM_BLOCKS))
+            router = None
+            if not per_slot and (blocks_per_slot * tokens * selected <= FOLDED_STAGING_BLOCKS or x.stored or (x.view is not None and x.view.base is not None)):
+                router = self._fusible_router(indices, x, tokens, selected, weight.dtype)  # (x is staged as it is: see _stageable)
+            if router is not None:
+                self._routed_expert_stream(router, out, weight, x, tokens, selected, experts, channels, inner, lanes, steps, blocks_per_slot)
+                self.expert_contractions += 1
+                return out
             x = self._stageable(x, blocks_per_slot * tokens * selected)
             k = Kernel(1)
             w, idx = self._matrix_slot(k, weight), self._matrix_slot(k, indices)
@@ -2225,6 +2238,44 @@ class HIPCodegen(Codegen):
         self.launch(k, (blocks_per_slot, tokens * selected, 1), 256, [weight, indices, x], kind="expert_linear")
         self.expert_contractions += 1
         return out
+
+    def _fusible_router(self, indices: Value, x: Value, tokens: int, selected: int, dtype) -> Optional[dict]:
+        """The router launch that selected ``indices`` when it can be recomputed inside the first expert
+        product: it is the last launch, it stages the same row ``x`` the product stages, it routes one row
+        per token to ``selected`` experts, and its gate weights are small."""
+        router = self.router_launches.get(indices.name)
+        if (router is None or router["index"] != len(self.launches) - 1 or router["source"].name != x.name or router["rows"] != tokens
+                or router["count"] != selected or router["weight"].dtype != dtype or router["columns"] > 64 or not router["lanes"]
+                or router["columns"] * router["inner"] * ITEMSIZE[dtype] > FUSED_ROUTER_BYTES):
+            return None
+        return router
+
+    def _routed_expert_stream(self, router: dict, out: Value, weight: Value, x: Value, tokens: int, selected: int, experts: int,
+                              channels: int, inner: int, lanes: int, steps: int, blocks_per_slot: int) -> None:
+        """The router and the first expert product in one kernel (``routed_expert_stream``): the router's
+        launch is retracted; every workgroup stages its token's row, selects the token's experts itself and
+        streams the slab of its slot's expert; one workgroup per token writes the router's outputs."""
+        self._retract_last_launch()
+        del self.router_launches[router["indices"].name]
+        k = Kernel(1)
+        ctype = ctype_of(out.dtype)
+        slot = Aff.of(k.atom("blockIdx.y", tokens * selected - 1, prefix="s"))
+        self._stage(k, x, 1, inner, lambda _row: [k.div(slot, selected)], 256)
+        gate = self._matrix_slot(k, router["weight"])
+        gate_bias = self._matrix_slot(k, router["bias"]) if router["bias"] is not None else "nullptr"
+        outputs = [k.slot(router[name].name, router[name].dtype, writable=True, extent=self.extents[router[name].name])
+                   for name in ("logits", "values", "indices", "weights")]
+        w = self._matrix_slot(k, weight)
+        out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        k.uses_error = True
+        k.line(
+            f"chroma::routed_expert_stream<{router['columns']}, {router['inner']}, {router['lanes']}, {str(router['largest']).lower()}, "
+            f"{inner}, {lanes}, {steps}, {ctype}>(xs, {gate}, {gate_bias}, {outputs[0]}, {outputs[1]}, {outputs[2]}, {outputs[3]}, "
+            f"{selected}u, {w}, {out_slot}, {experts}u, {channels}u, {blocks_per_slot}u, error);"
+        )
+        inputs = [x, router["weight"], weight] + ([router["bias"]] if router["bias"] is not None else [])
+        self.launch(k, (blocks_per_slot, tokens * selected, 1), 256, inputs, kind="routed_experts")
+        self.routed_experts += 1
 
     def _matrix_einsum(self, meta, labels, output, sizes, reduction, values) -> Optional[Value]:
         """A batched matrix product on the matrix cores (the reference's ``matrix`` hook, gpu.py:426-435,
@@ -2441,6 +2492,7 @@ class HIPCodegen(Codegen):
             mfma_matmuls=self.mfma_matmuls,
             fused_attentions=self.fused_attentions,
             fused_routers=self.fused_routers,
+            routed_experts=self.routed_experts,
             small_contractions=self.small_contractions,
             attention_epilogues=self.attention_epilogues,
             write_through_stores=self.write_through_stores,

@@ -26,6 +26,14 @@ template <class T> __device__ __forceinline__ float load1(const T* p);
 template <> __device__ __forceinline__ float load1<float>(const float* p) { return *p; }
 template <> __device__ __forceinline__ float load1<uint16_t>(const uint16_t* p) { return bf16_to_f32(*p); }
 
+// The storage value of v (rounded to bfloat16 for uint16_t storage) and its widening back to float.
+template <class T> __device__ __forceinline__ T storage_of(float v);
+template <> __device__ __forceinline__ float storage_of<float>(float v) { return v; }
+template <> __device__ __forceinline__ uint16_t storage_of<uint16_t>(float v) { return f32_to_bf16(v); }
+template <class T> __device__ __forceinline__ float widen_of(T v);
+template <> __device__ __forceinline__ float widen_of<float>(float v) { return v; }
+template <> __device__ __forceinline__ float widen_of<uint16_t>(uint16_t v) { return bf16_to_f32(v); }
+
 template <class T> __device__ __forceinline__ void store1(T* p, float v);
 template <> __device__ __forceinline__ void store1<float>(float* p, float v) { *p = v; }
 template <> __device__ __forceinline__ void store1<uint16_t>(uint16_t* p, float v) { *p = f32_to_bf16(v); }
@@ -348,6 +356,19 @@ __device__ __forceinline__ void stream_expert_rows(const T* __restrict__ w, cons
                                                         blocks_per_slot * waves_per_block, first);
 }
 
+// The same product for a slot whose expert index the kernel has just selected itself (``routed_expert_stream``):
+// ``chosen`` is that index, checked like a stored one.
+template <int K, int LPR, int ROWS, class T>
+__device__ __forceinline__ void stream_expert_chosen(const T* __restrict__ w, int64_t chosen, const float* xs, T* __restrict__ out,
+                                                     uint32_t experts, uint32_t channels, uint32_t blocks_per_slot, unsigned int* error) {
+    const uint32_t slot = blockIdx.y;
+    const uint64_t expert = checked_index(chosen, experts, true, error);
+    const uint32_t waves_per_block = blockDim.x / kWave;
+    const uint32_t wave = blockIdx.x * waves_per_block + threadIdx.x / kWave;
+    stream_rows<1, K, LPR, ROWS, true, false, T>(nullptr, xs, w + expert * uint64_t(channels) * K, nullptr, out + uint64_t(slot) * channels, channels,
+                                                 channels, wave, blocks_per_slot * waves_per_block, nullptr);
+}
+
 template <int K, int LPR, int ROWS, bool STAGED, class T, bool PER_SLOT_INPUT>
 __device__ __forceinline__ void stream_expert_linear(const T* __restrict__ w, const int64_t* __restrict__ indices, const T* __restrict__ x,
                                                      const float* xs, T* __restrict__ out, uint32_t selected, uint32_t experts, uint32_t channels,
@@ -383,10 +404,14 @@ __device__ __forceinline__ void router_fetch(StreamStep<K, LPR, 1, T>& first, co
 
 // With PREFETCHED (LPR > 0 only), this wave's first step of W was requested into ``first`` by
 // ``router_fetch`` before the prologue that stages the row; the step is then used and refilled in place.
-template <int E, int K, int LPR, bool LARGEST, class T, bool PREFETCHED = false>
+//
+// With CHOSEN (``routed_expert_stream``), every workgroup of the kernel selects for its row: the chosen
+// indices go to ``chosen`` (LDS, k entries, visible to every wave when this returns), and the global
+// outputs are written only where ``write`` holds (one workgroup per row).
+template <int E, int K, int LPR, bool LARGEST, class T, bool PREFETCHED = false, bool CHOSEN = false>
 __device__ __forceinline__ void router_rows(const float* xs, const T* __restrict__ w, const T* __restrict__ bias, T* __restrict__ logits,
                                             T* __restrict__ values, int64_t* __restrict__ indices, T* __restrict__ weights, uint32_t k,
-                                            StreamStep<K, (LPR > 0 ? LPR : 1), 1, T>* first) {
+                                            StreamStep<K, (LPR > 0 ? LPR : 1), 1, T>* first, int32_t* chosen_s = nullptr, bool write = true) {
     static_assert(E <= kWave, "one expert per lane");
     __shared__ float logit_s[E];
     const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
@@ -445,15 +470,21 @@ __device__ __forceinline__ void router_rows(const float* xs, const T* __restrict
     }
     __syncthreads();
     if (wave != 0) {
-        return;  // the first wave selects; no barrier follows
+        if constexpr (CHOSEN) {
+            __syncthreads();  // the first wave's selection
+        }
+        return;  // the first wave selects; without CHOSEN no barrier follows
     }
     const float mine = lane < uint32_t(E) ? logit_s[lane] : 0.0f;
     float logit = 0.0f;
     uint64_t key = 0;
     if (lane < uint32_t(E)) {
         const float b = bias ? load1<T>(bias + lane) : 0.0f;
-        store1<T>(logits + lane, mine + b);
-        logit = load1<T>(logits + lane);  // the rounded logit, as stored
+        const T stored = storage_of<T>(mine + b);
+        if (write) {
+            logits[lane] = stored;
+        }
+        logit = widen_of<T>(stored);  // the rounded logit, as stored
         key = topk_key(logit, lane, LARGEST);
     }
     float chosen[E];
@@ -465,8 +496,19 @@ __device__ __forceinline__ void router_rows(const float* xs, const T* __restrict
             key = 0;
         }
         if (lane == 0) {
-            store1<T>(values + s, chosen[s]);
-            indices[s] = int64_t(winner);
+            if constexpr (CHOSEN) {
+                chosen_s[s] = int32_t(winner);
+            }
+            if (write) {
+                store1<T>(values + s, chosen[s]);
+                indices[s] = int64_t(winner);
+            }
+        }
+    }
+    if constexpr (CHOSEN) {
+        __syncthreads();  // publishes chosen_s to the other waves
+        if (!write) {
+            return;
         }
     }
     if (lane == 0) {
@@ -488,6 +530,25 @@ template <int E, int K, int LPR, bool LARGEST, class T>
 __device__ __forceinline__ void router_row(const float* xs, const T* __restrict__ w, const T* __restrict__ bias, T* __restrict__ logits,
                                            T* __restrict__ values, int64_t* __restrict__ indices, T* __restrict__ weights, uint32_t k) {
     router_rows<E, K, LPR, LARGEST, T, false>(xs, w, bias, logits, values, indices, weights, k, nullptr);
+}
+
+// A router fused into its first expert product (one kernel instead of two): each workgroup of the expert
+// stream (grid.y: slot = token * selected + s) recomputes its token's router from the staged row ``xs``
+// (the gate weights are small: E x K), takes expert s of the selection and streams that expert's slab.
+// The workgroup at blockIdx.x == 0 of slot s == 0 also writes the router's outputs (logits, values,
+// indices, softmax weights) for later readers. Selection, rounding and tie rules are router_rows'.
+template <int E, int K, int RLPR, bool LARGEST, int SK, int LPR, int ROWS, class T>
+__device__ __forceinline__ void routed_expert_stream(const float* xs, const T* __restrict__ gate, const T* __restrict__ gate_bias,
+                                                     T* __restrict__ logits, T* __restrict__ values, int64_t* __restrict__ indices,
+                                                     T* __restrict__ weights, uint32_t selected, const T* __restrict__ w, T* __restrict__ out,
+                                                     uint32_t experts, uint32_t channels, uint32_t blocks_per_slot, unsigned int* error) {
+    __shared__ int32_t chosen_s[E];
+    const uint32_t token = blockIdx.y / selected, s = blockIdx.y % selected;
+    const bool write = blockIdx.x == 0 && s == 0;
+    router_rows<E, K, RLPR, LARGEST, T, false, true>(xs, gate, gate_bias, logits + size_t(token) * E, values + size_t(token) * selected,
+                                                     indices + size_t(token) * selected, weights + size_t(token) * selected, selected, nullptr,
+                                                     chosen_s, write);
+    stream_expert_chosen<SK, LPR, ROWS, T>(w, int64_t(chosen_s[s]), xs, out, experts, channels, blocks_per_slot, error);
 }
 
 template <int E, int K, int LPR, bool LARGEST, class T>
