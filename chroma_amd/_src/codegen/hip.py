@@ -78,6 +78,7 @@ SMALL_OPERAND_COST = 8  # ...over operands that cost at most this much per eleme
 MATRIX_MIN_WORK = 1 << 18  # smaller batched products stay on the generic contraction kernel
 GROUPED_SLOTS = 64  # from this many (token, expert) slots on, expert products are grouped by expert
 FUSED_ROUTER_BYTES = 32 << 10  # a router with gate weights up to this size is recomputed inside its first expert product
+ROUTER_TICKETS = 48  # rows a split router can serve (chroma::kRouterTickets words of the error region)
 MATRIX_ATTENTION_TOKENS = 64  # bfloat16 attention over at least this many queries runs on the matrix cores
 SPLIT_KEYS = 256  # keys per workgroup when an attention row's keys are split over workgroups
 DECODE_SPLIT_KEYS = 128  # the same for stored key/value rows read with 16-byte loads (decode steps)
@@ -1486,13 +1487,16 @@ class HIPCodegen(Codegen):
         self._retract_last_launch()  # the replacement kernel stages the same operand (and writes its pending stores)
         weights = self.allocate(tuple(values.shape), values.dtype)
         k = Kernel(1)
+        per_chunk = 16 // ITEMSIZE[x.dtype]
+        chunks = inner // per_chunk if inner % per_chunk == 0 else 0
+        lanes = next((l for l in (64, 32, 16, 8, 4, 2) if chunks and chunks % l == 0 and chunks // l >= 4), 1 if chunks else 0)
+        if lanes and columns <= 64 and columns * inner * ITEMSIZE[x.dtype] > FUSED_ROUTER_BYTES and chunks // lanes <= 64 and rows <= ROUTER_TICKETS:
+            self._split_router(k, source, x, weight, bias, values, indices, weights, rows, columns, inner, lanes, bool(largest), count)
+            return True
         row = Aff.of(k.atom("blockIdx.x", rows - 1, prefix="r"))
         lead = tuple(source.shape[:-1])
         ctype = ctype_of(x.dtype)
         w_arg = self._matrix_slot(k, weight)
-        per_chunk = 16 // ITEMSIZE[x.dtype]
-        chunks = inner // per_chunk if inner % per_chunk == 0 else 0
-        lanes = next((l for l in (64, 32, 16, 8, 4, 2) if chunks and chunks % l == 0 and chunks // l >= 4), 1 if chunks else 0)
         self._stage(k, source, 1, inner, lambda _r: k.unflatten(row, lead) if lead else [], 256)
         if lanes:
             # the gate weights are requested after the prologue: vector loads complete in order, so a
@@ -1517,6 +1521,29 @@ class HIPCodegen(Codegen):
                                                   largest=bool(largest), count=count)
         self.fused_routers += 1
         return True
+
+    def _split_router(self, k: Kernel, source: Value, x: Value, weight: Value, bias: Optional[Value], values: Value, indices: Value,
+                      weights: Value, rows: int, columns: int, inner: int, lanes: int, largest: bool, count: int) -> None:
+        """A router over gate weights too large for one workgroup (``router_split``): parts of 64 / lanes
+        experts each per row (4-wave workgroups: all stage the row, the first wave streams the part's gate
+        rows), the last part to finish selecting; its per-row ticket counters are
+        words of the program's error region (zero at load, returned to zero by every launch)."""
+        parts = -(-columns // (64 // lanes))
+        row = Aff.of(k.atom("blockIdx.y", rows - 1, prefix="r"))
+        lead = tuple(source.shape[:-1])
+        ctype = ctype_of(x.dtype)
+        w_arg = self._matrix_slot(k, weight)
+        b_arg = self._matrix_slot(k, bias) if bias is not None else "nullptr"
+        self._stage(k, source, 1, inner, lambda _r: k.unflatten(row, lead) if lead else [], 256)
+        outputs = [k.slot(v.name, v.dtype, writable=True, extent=self.extents[v.name]) for v in (x, values, indices, weights)]
+        k.uses_error = True
+        k.line(
+            f"chroma::router_split<{columns}, {inner}, {lanes}, {str(largest).lower()}, {ctype}>(xs, {w_arg}, {b_arg}, {outputs[0]}, "
+            f"{outputs[1]}, {outputs[2]}, {outputs[3]}, {count}u, error + chroma::kRouterTicketWord);"
+        )
+        self.launch(k, (parts, rows, 1), 256, [source, weight] + ([bias] if bias is not None else []), kind="router_split")
+        self.router_weights[values.name] = weights
+        self.fused_routers += 1
 
     # =================================================================================== linear
     def linear(self, meta, x: Value, weight: Value, bias: Optional[Value]) -> Value:
@@ -1566,22 +1593,45 @@ class HIPCodegen(Codegen):
 
     @staticmethod
     def _stream_plan(rows: int, inner: int, dtype: torch.dtype, weight_bytes: int) -> Optional[Tuple[int, int]]:
-        """(lanes per row, rows per step) for ``stream_rows``: the widest power-of-two lane group that still
-        gives each lane 4 or more 16-byte chunks of a row (or a whole short row), and enough row steps
-        that about 32 chunks per lane are in flight; None when a row is not a whole number of chunks.
-        Products streaming at most ``SPREAD_BYTES`` of weights take one row step per wave instead: a
-        workgroup's stream is bounded by its compute unit's outstanding requests, so small matrices go
-        fastest spread over as many compute units as they have rows for."""
+        """(lanes per row, rows per step) for ``stream_rows``: 64 lanes per row when a row has at least 64
+        16-byte chunks, wastes at most 1/8 of its lanes' chunks on a ragged end and the launch stays within
+        ``FOLDED_STAGING_BLOCKS`` workgroups; otherwise the widest power-of-two lane group that gives each lane
+        4 or more whole chunks (or a whole short row). Products streaming at most ``SPREAD_BYTES`` of
+        weights take one row step per wave; larger ones take more only as far as needed to stay within
+        ``FOLDED_STAGING_BLOCKS`` workgroups (up to ~32 chunks per lane in flight). A workgroup's stream is
+        bounded by its compute unit's outstanding requests, so products go fastest spread over as many
+        compute units as they have rows for. None when a row is not a whole number of chunks."""
         per_chunk = 16 // ITEMSIZE[dtype]
         if inner % per_chunk:
             return None
         chunks = inner // per_chunk
+        rows_of_w = weight_bytes // (inner * ITEMSIZE[dtype])
+
+        def plan(lanes: int) -> Optional[Tuple[int, int, int]]:
+            per_lane = -(-chunks // lanes)
+            if per_lane > 64:
+                return None
+            if weight_bytes <= SPREAD_BYTES:
+                return lanes, 1, 0
+            # Up to ~32 chunks per lane in flight, but more row steps per wave only while the launch would
+            # otherwise exceed FOLDED_STAGING_BLOCKS workgroups: more workgroups stream faster than more rows
+            # per wave (a workgroup's stream is bounded by its compute unit's outstanding requests).
+            most = max(1, min(8, 32 // per_lane, max(1, 32 // rows)))
+            steps = 1
+            while steps < most and -(-rows_of_w // (64 // lanes * steps * 4)) > FOLDED_STAGING_BLOCKS:
+                steps += 1
+            return lanes, steps, -(-rows_of_w // (64 // lanes * steps * 4))
+
+        wide = -(-chunks // 64)
+        if chunks >= 64 and (wide * 64 - chunks) * 8 <= wide * 64:
+            # 64 lanes per row (a ragged last chunk costs at most 1/8 of a lane's chunks): a wave covers one
+            # row per step, so the product spreads over as many workgroups as its rows allow
+            chosen = plan(64)
+            if chosen is not None and chosen[2] <= FOLDED_STAGING_BLOCKS:
+                return chosen[0], chosen[1]
         lanes = next((l for l in (64, 32, 16, 8, 4, 2) if chunks % l == 0 and chunks // l >= 4), 1)
-        per_lane = chunks // lanes
-        if per_lane > 64:
-            return None
-        steps = 1 if weight_bytes <= SPREAD_BYTES else max(1, min(8, 32 // per_lane, max(1, 32 // rows)))
-        return lanes, steps
+        chosen = plan(lanes)
+        return None if chosen is None else (chosen[0], chosen[1])
 
     def _stream_blocks(self, columns: int, lanes: int, steps: int) -> int:
         waves = -(-columns // (64 // lanes * steps))
@@ -1591,7 +1641,7 @@ class HIPCodegen(Codegen):
         """A few-row linear on the weight-streaming kernel; X (any view or fused expression, including a
         deferred norm) is evaluated into LDS by the generated prologue."""
         lanes, steps = plan
-        blocks = self._stream_blocks(columns, lanes, steps)
+        blocks, threads = self._stream_blocks(columns, lanes, steps), 256
         x = self._stageable(x, blocks)
         k = Kernel(1)
         w_arg = self._matrix_slot(k, weight)
@@ -1601,14 +1651,14 @@ class HIPCodegen(Codegen):
         # W is requested after the prologue that stages X: vector loads complete in order, so a stream
         # requested first makes every dependent load of the prologue wait for it (and queue behind it);
         # measured on the GPT-OSS-20B decode products, the prologue then costs several times its own latency.
-        self._stage(k, x, rows, inner, lambda row: k.unflatten(row, lead) if lead else [], 256)
+        self._stage(k, x, rows, inner, lambda row: k.unflatten(row, lead) if lead else [], threads)
         k.line(f"chroma::StreamStep<{inner}, {lanes}, {steps}, {ctype_of(out.dtype)}> prefetched;")
         k.line(f"chroma::stream_linear_fetch(prefetched, {w_arg}, {columns}u);")
         k.line(
             f"chroma::stream_linear<{rows}, {inner}, {lanes}, {steps}, true, {ctype_of(out.dtype)}>("
             f"nullptr, xs, {w_arg}, {b_arg}, {out_slot}, {columns}u, prefetched);"
         )
-        self.launch(k, blocks, 256, [x, weight] + ([bias] if bias is not None else []), kind="linear_stream")
+        self.launch(k, blocks, threads, [x, weight] + ([bias] if bias is not None else []), kind="linear_stream")
 
     def _skinny_linear(self, out, x, weight, bias, rows, columns, inner) -> None:
         lanes_per_row = 64
@@ -2188,12 +2238,12 @@ class HIPCodegen(Codegen):
             # view or fused expression, e.g. the gated activation of the first expert product) is
             # evaluated into LDS, then the selected expert's slab is streamed.
             lanes, steps = plan
-            blocks_per_slot = max(1, min(-(-(-(-channels // (64 // lanes * steps))) // 4), STREAM_BLOCKS))
+            blocks_per_slot, threads = self._stream_blocks(channels, lanes, steps), 256
             router = None
             if not per_slot and (blocks_per_slot * tokens * selected <= FOLDED_STAGING_BLOCKS or x.stored or (x.view is not None and x.view.base is not None)):
                 router = self._fusible_router(indices, x, tokens, selected, weight.dtype)  # (x is staged as it is: see _stageable)
             if router is not None:
-                self._routed_expert_stream(router, out, weight, x, tokens, selected, experts, channels, inner, lanes, steps, blocks_per_slot)
+                self._routed_expert_stream(router, out, weight, x, tokens, selected, experts, channels, inner, lanes, steps, blocks_per_slot, threads)
                 self.expert_contractions += 1
                 return out
             x = self._stageable(x, blocks_per_slot * tokens * selected)
@@ -2207,14 +2257,14 @@ class HIPCodegen(Codegen):
             else:
                 coords_of = lambda _row: [k.div(slot, selected)]
             # the slab is requested after the prologue (see _stream_linear)
-            self._stage(k, x, 1, inner, coords_of, 256)
+            self._stage(k, x, 1, inner, coords_of, threads)
             k.line(f"chroma::StreamStep<{inner}, {lanes}, {steps}, {ctype_of(out.dtype)}> prefetched;")
             k.line(f"chroma::stream_expert_fetch(prefetched, {w}, {idx}, {experts}u, {channels}u, error);")
             k.line(
                 f"chroma::stream_expert_linear<{inner}, {lanes}, {steps}, true, {ctype_of(out.dtype)}, {per_expert}>("
                 f"{w}, {idx}, nullptr, xs, {out_slot}, {selected}u, {experts}u, {channels}u, {blocks_per_slot}u, error, prefetched);"
             )
-            self.launch(k, (blocks_per_slot, tokens * selected, 1), 256, [weight, indices, x], kind="expert_stream")
+            self.launch(k, (blocks_per_slot, tokens * selected, 1), threads, [weight, indices, x], kind="expert_stream")
             self.expert_contractions += 1
             return out
         x = self.contiguous(x)
@@ -2251,7 +2301,7 @@ class HIPCodegen(Codegen):
         return router
 
     def _routed_expert_stream(self, router: dict, out: Value, weight: Value, x: Value, tokens: int, selected: int, experts: int,
-                              channels: int, inner: int, lanes: int, steps: int, blocks_per_slot: int) -> None:
+                              channels: int, inner: int, lanes: int, steps: int, blocks_per_slot: int, threads: int) -> None:
         """The router and the first expert product in one kernel (``routed_expert_stream``): the router's
         launch is retracted; every workgroup stages its token's row, selects the token's experts itself and
         streams the slab of its slot's expert; one workgroup per token writes the router's outputs."""
@@ -2260,7 +2310,7 @@ class HIPCodegen(Codegen):
         k = Kernel(1)
         ctype = ctype_of(out.dtype)
         slot = Aff.of(k.atom("blockIdx.y", tokens * selected - 1, prefix="s"))
-        self._stage(k, x, 1, inner, lambda _row: [k.div(slot, selected)], 256)
+        self._stage(k, x, 1, inner, lambda _row: [k.div(slot, selected)], threads)
         gate = self._matrix_slot(k, router["weight"])
         gate_bias = self._matrix_slot(k, router["bias"]) if router["bias"] is not None else "nullptr"
         outputs = [k.slot(router[name].name, router[name].dtype, writable=True, extent=self.extents[router[name].name])
@@ -2274,7 +2324,7 @@ class HIPCodegen(Codegen):
             f"{selected}u, {w}, {out_slot}, {experts}u, {channels}u, {blocks_per_slot}u, error);"
         )
         inputs = [x, router["weight"], weight] + ([router["bias"]] if router["bias"] is not None else [])
-        self.launch(k, (blocks_per_slot, tokens * selected, 1), 256, inputs, kind="routed_experts")
+        self.launch(k, (blocks_per_slot, tokens * selected, 1), threads, inputs, kind="routed_experts")
         self.routed_experts += 1
 
     def _matrix_einsum(self, meta, labels, output, sizes, reduction, values) -> Optional[Value]:

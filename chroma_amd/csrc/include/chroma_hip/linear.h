@@ -175,13 +175,21 @@ template <> struct Chunk16<uint16_t> {
 // One step of ``stream_rows`` for one lane: its 16-byte chunks of ROWS rows of W, all requested before
 // any arithmetic. A kernel may request its first step before its prologue (see ``stream_linear_fetch``),
 // so the weight read overlaps the evaluation of X into LDS.
+// A row of CHUNKS 16-byte chunks need not split evenly over the LPR lanes (RAGGED): the last of a lane's
+// PER_LANE chunks is then past the row's end for some lanes, which load another chunk of the same row
+// instead and leave it out of the arithmetic (``live``).
 template <int K, int LPR, int ROWS, class T>
 struct StreamStep {
     static constexpr int N = Chunk16<T>::N;
-    static constexpr int PER_LANE = K / N / LPR;
+    static constexpr int CHUNKS = K / N;
+    static constexpr int PER_LANE = (CHUNKS + LPR - 1) / LPR;
+    static constexpr bool RAGGED = CHUNKS % LPR != 0;
     static constexpr int G = kWave / LPR;
-    static_assert(K % N == 0 && (K / N) % LPR == 0, "rows must split into 16-byte chunks per lane");
+    static_assert(K % N == 0, "rows must split into 16-byte chunks");
     u32x4_t chunks[ROWS][PER_LANE];
+
+    // whether chunk c of this lane (sub = lane % LPR) lies in the row
+    static __device__ __forceinline__ bool live(int c, uint32_t sub) { return !RAGGED || c + 1 < PER_LANE || c * LPR + sub < uint32_t(CHUNKS); }
 
     __device__ __forceinline__ void fetch(const T* __restrict__ w, uint32_t base, uint32_t rows) {
         const uint32_t lane = threadIdx.x % kWave;
@@ -192,7 +200,8 @@ struct StreamStep {
             const uint32_t safe = row < rows ? row : rows - 1;
 #pragma unroll
             for (int c = 0; c < PER_LANE; ++c) {
-                chunks[r][c] = Chunk16<T>::load(w + size_t(safe) * K + (c * LPR + sub) * N);
+                const uint32_t chunk = live(c, sub) ? c * LPR + sub : sub;
+                chunks[r][c] = Chunk16<T>::load(w + size_t(safe) * K + chunk * N);
             }
         }
     }
@@ -238,6 +247,9 @@ __device__ __forceinline__ void stream_rows(const T* __restrict__ x, const float
             }
 #pragma unroll
             for (int c = 0; c < PER_LANE; ++c) {
+                if (!Step::live(c, sub)) {
+                    continue;  // past the row's end (ragged rows only)
+                }
                 const uint32_t k0 = (c * LPR + sub) * C::N;
 #pragma unroll
                 for (int e = 0; e < C::N; ++e) {
@@ -413,6 +425,7 @@ __device__ __forceinline__ void router_rows(const float* xs, const T* __restrict
                                             T* __restrict__ values, int64_t* __restrict__ indices, T* __restrict__ weights, uint32_t k,
                                             StreamStep<K, (LPR > 0 ? LPR : 1), 1, T>* first, int32_t* chosen_s = nullptr, bool write = true) {
     static_assert(E <= kWave, "one expert per lane");
+    static_assert(LPR == 0 || !StreamStep<K, (LPR > 0 ? LPR : 1), 1, T>::RAGGED, "router rows split evenly over their lanes");
     __shared__ float logit_s[E];
     const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
     if constexpr (LPR > 0) {
@@ -530,6 +543,99 @@ template <int E, int K, int LPR, bool LARGEST, class T>
 __device__ __forceinline__ void router_row(const float* xs, const T* __restrict__ w, const T* __restrict__ bias, T* __restrict__ logits,
                                            T* __restrict__ values, int64_t* __restrict__ indices, T* __restrict__ weights, uint32_t k) {
     router_rows<E, K, LPR, LARGEST, T, false>(xs, w, bias, logits, values, indices, weights, k, nullptr);
+}
+
+// A router whose gate weights are too large for one workgroup's stream (GPT-OSS-20B: 32 x 2880): grid.x
+// parts (the first wave of each; the other waves only share the staging prologue, whose row loads are
+// then all in flight at once) compute G = 64 / LPR experts' logits of row blockIdx.y (bias added, rounded and
+// stored as router_rows stores them); each part then fences its stores and takes a ticket from the row's
+// counter, and the part that takes the last ticket selects: it reads the row's stored logits, picks the
+// top k with router_rows' ranking and tie rules and writes values, int64 indices and the softmax of the
+// values, then resets the counter to 0 for the next launch. No part waits for another. ``counter`` holds
+// one word per row (kRouterTickets at most), zero when the kernel starts: the program's error region,
+// which the runtime clears at load, past its index-error word.
+constexpr uint32_t kRouterTicketWord = 16;  // first word of the tickets in the 64-word error region
+constexpr uint32_t kRouterTickets = 48;
+
+template <int E, int K, int LPR, bool LARGEST, class T>
+__device__ __forceinline__ void router_split(const float* xs, const T* __restrict__ w, const T* __restrict__ bias, T* __restrict__ logits,
+                                             T* __restrict__ values, int64_t* __restrict__ indices, T* __restrict__ weights, uint32_t k,
+                                             unsigned int* counter) {
+    static_assert(E <= kWave && LPR > 0 && !StreamStep<K, LPR, 1, T>::RAGGED, "one expert per lane, rows split evenly over their lanes");
+    using C = Chunk16<T>;
+    using Step = StreamStep<K, LPR, 1, T>;
+    constexpr int PER_LANE = Step::PER_LANE;
+    constexpr int G = Step::G;
+    const uint32_t lane = threadIdx.x % kWave, group = lane / LPR, sub = lane % LPR;
+    const uint32_t row = blockIdx.y, parts = gridDim.x;
+    T* row_logits = logits + size_t(row) * E;
+    if (threadIdx.x < kWave) {
+        const uint32_t e0 = blockIdx.x * G, e = e0 + group;
+        Step step;
+        step.fetch(w, e0, E);
+        float partial = 0.0f;
+#pragma unroll
+        for (int c = 0; c < PER_LANE; ++c) {
+            if (c % 8 == 0) {
+                __asm__ volatile("" ::: "memory");
+            }
+#pragma unroll
+            for (int i = 0; i < C::N; ++i) {
+                partial += C::get(step.chunks[0][c], i) * xs[(c * LPR + sub) * C::N + i];
+            }
+        }
+#pragma unroll
+        for (int offset = LPR / 2; offset > 0; offset >>= 1) {
+            partial += __shfl_xor(partial, offset, kWave);
+        }
+        if (sub == 0 && e < uint32_t(E)) {
+            row_logits[e] = storage_of<T>(partial + (bias ? load1<T>(bias + e) : 0.0f));
+        }
+    }
+    __threadfence();  // this part's logits are visible before its ticket is
+    __shared__ unsigned int ticket;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        ticket = atomicAdd(counter + row, 1u);
+    }
+    __syncthreads();
+    if (ticket != parts - 1 || threadIdx.x >= kWave) {
+        return;
+    }
+    __threadfence();  // every other part's logits are visible to the last one
+    float logit = 0.0f;
+    uint64_t key = 0;
+    if (lane < uint32_t(E)) {
+        logit = widen_of<T>(row_logits[lane]);  // after the acquiring fence: every part's stored, rounded logit
+        key = topk_key(logit, lane, LARGEST);
+    }
+    float chosen[E];
+    for (uint32_t s = 0; s < k; ++s) {
+        const uint64_t top = wave_max_u64(key);
+        const uint32_t winner = 0xffffffffu - uint32_t(top);
+        chosen[s] = __shfl(logit, int(winner), kWave);
+        if (lane == winner) {
+            key = 0;
+        }
+        if (lane == 0) {
+            store1<T>(values + size_t(row) * k + s, chosen[s]);
+            indices[size_t(row) * k + s] = int64_t(winner);
+        }
+    }
+    if (lane == 0) {
+        float peak = -__builtin_inff();
+        for (uint32_t s = 0; s < k; ++s) {
+            peak = __builtin_fmaxf(peak, chosen[s]);
+        }
+        float total = 0.0f;
+        for (uint32_t s = 0; s < k; ++s) {
+            total += fast_exp(chosen[s] - peak);
+        }
+        for (uint32_t s = 0; s < k; ++s) {
+            store1<T>(weights + size_t(row) * k + s, fast_exp(chosen[s] - peak) / total);
+        }
+        atomicExch(counter + row, 0u);
+    }
 }
 
 // A router fused into its first expert product (one kernel instead of two): each workgroup of the expert

@@ -67,6 +67,7 @@ struct Region {
 // through two pinned staging slots of kStagingSlot bytes: the CPU copy into or out of one slot overlaps
 // the DMA of the other (HIP's own pageable path reaches about a third of the link's pinned rate).
 constexpr size_t kDirectBytes = size_t(256) << 10;
+constexpr size_t kErrorRegion = 256;  // bytes the plan reserves at its error offset
 constexpr size_t kStagingSlot = size_t(2) << 20;
 
 std::mutex pinned_mutex;
@@ -170,8 +171,8 @@ Plan read_plan(const std::string& path) {
             }
         }
     }
-    if (!inside(plan.error, sizeof(unsigned)) || !inside(0, plan.weight_bytes)) {
-        throw std::runtime_error("Launch plan error word or weights outside the program allocation");
+    if (!inside(plan.error, kErrorRegion) || !inside(0, plan.weight_bytes)) {
+        throw std::runtime_error("Launch plan error region or weights outside the program allocation");
     }
     return plan;
 }
@@ -209,7 +210,9 @@ public:
             check(hipEventCreate(&stop_), "hipEventCreate");
             check(hipHostMalloc(reinterpret_cast<void**>(&error_host_), sizeof(unsigned), hipHostMallocDefault), "hipHostMalloc");
             check(hipMalloc(&base_, plan_.arena ? plan_.arena : 1), "hipMalloc program allocation");
-            check(hipMemset(static_cast<char*>(base_) + plan_.error, 0, sizeof(unsigned)), "Clear index error");
+            // The whole 256-byte error region starts at zero: word 0 is the index-error flag, words 16-63 are
+            // the per-row tickets of split routers (chroma::router_split), which return them to zero.
+            check(hipMemset(static_cast<char*>(base_) + plan_.error, 0, kErrorRegion), "Clear error region");
             upload_weights(directory + "/" + plan_.weights_file);
             check(hipModuleLoad(&module_, (directory + "/" + plan_.code_object).c_str()), "hipModuleLoad");
             std::map<std::string, hipFunction_t> functions;
