@@ -79,6 +79,7 @@ MATRIX_MIN_WORK = 1 << 18  # smaller batched products stay on the generic contra
 GROUPED_SLOTS = 64  # from this many (token, expert) slots on, expert products are grouped by expert
 FUSED_ROUTER_BYTES = 32 << 10  # a router with gate weights up to this size is recomputed inside its first expert product
 ROUTER_TICKETS = 48  # rows a split router can serve (chroma::kRouterTickets words of the error region)
+NARROW_COLUMNS = 64  # linears of at most this many columns over many rows take one workgroup per 16 rows
 MATRIX_ATTENTION_TOKENS = 64  # bfloat16 attention over at least this many queries runs on the matrix cores
 SPLIT_KEYS = 256  # keys per workgroup when an attention row's keys are split over workgroups
 DECODE_SPLIT_KEYS = 128  # the same for stored key/value rows read with 16-byte loads (decode steps)
@@ -1572,6 +1573,10 @@ class HIPCodegen(Codegen):
         if self.blas and rows <= 16 and inner % 4 == 0:
             self._skinny_linear(out, x, weight, bias, rows, columns, inner)
             self.skinny_matmuls += 1
+        elif (self.blas and columns <= NARROW_COLUMNS and rows >= 64 and inner % (32 if meta.dtype == torch.bfloat16 else 4) == 0
+              and x.view.offset % 8 == 0 and weight.view.offset % 8 == 0):
+            self._narrow_linear(out, x, weight, bias, rows, columns, inner)
+            self.mfma_matmuls += 1
         elif self.blas and inner % (8 if meta.dtype == torch.bfloat16 else 4) == 0:
             self._mfma_linear(out, x, weight, bias, rows, columns, inner)
             self.mfma_matmuls += 1
@@ -1659,6 +1664,15 @@ class HIPCodegen(Codegen):
             f"nullptr, xs, {w_arg}, {b_arg}, {out_slot}, {columns}u, prefetched);"
         )
         self.launch(k, blocks, threads, [x, weight] + ([bias] if bias is not None else []), kind="linear_stream")
+
+    def _narrow_linear(self, out, x, weight, bias, rows, columns, inner) -> None:
+        """Many rows, few columns (a router's gate over a prefill): ``narrow_linear``, one workgroup per 16
+        rows, instead of 128 x 128 tiles that would leave all but a few compute units idle."""
+        k = Kernel(1)
+        args = [self._matrix_slot(k, x), self._matrix_slot(k, weight), self._matrix_slot(k, bias) if bias is not None else "nullptr"]
+        out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        k.line(f"chroma::narrow_linear<{ctype_of(out.dtype)}, {columns}>({args[0]}, {args[1]}, {args[2]}, {out_slot}, {rows}u, {inner}u);")
+        self.launch(k, -(-rows // 16), 256, [x, weight] + ([bias] if bias is not None else []), kind="linear_narrow")
 
     def _skinny_linear(self, out, x, weight, bias, rows, columns, inner) -> None:
         lanes_per_row = 64

@@ -1379,6 +1379,100 @@ __device__ __forceinline__ void mfma_linear_wide(const T* __restrict__ x, const 
 // ---------------------------------------------------------------------------------------------
 // Expert-grouped mixture-of-experts products.
 //
+// Y[M, N] = X[M, K] . W[N, K]^T (+ bias[N]) for few columns (N <= 64: a router's gate) and many rows: one
+// workgroup of 4 waves per 16 rows of X, the waves splitting K into quarters; the matrix-core operands are
+// read straight from global memory (each X row once, W - N x K, small - from L2), 8 k-steps of loads in
+// flight per wave; the waves' float partial sums meet in LDS and are added in wave order, the bias added
+// to the finished sum and the result rounded once (the numerics of every matrix-core product here).
+// bfloat16: v_mfma_f32_16x16x32_bf16 (K % 32 == 0); float: v_mfma_f32_16x16x4f32 (K % 4 == 0). Rows past
+// M and columns past N read the last row or column and are not stored.
+template <class T, int N>
+__device__ __forceinline__ void narrow_linear(const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias,
+                                              T* __restrict__ out, uint32_t m, uint32_t k_total) {
+    static_assert(N >= 1 && N <= 64, "few columns");
+    constexpr int NT = (N + 15) / 16;
+    constexpr bool BF16 = sizeof(T) == 2;
+    constexpr uint32_t KS = BF16 ? 32u : 4u;  // k per MFMA
+    constexpr int UNROLL = 8;
+    __shared__ float partial[4][16][NT * 16];
+    const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, col = lane % 16u, quad = lane / 16u;
+    const uint32_t r0 = blockIdx.x * 16u;
+    const uint32_t row = r0 + col < m ? r0 + col : m - 1u;
+    const uint32_t steps = k_total / KS;
+    const uint32_t begin = steps * wave / 4u, end = steps * (wave + 1u) / 4u;
+    const T* xr = x + size_t(row) * k_total + (BF16 ? quad * 8u : quad);
+    const T* wr[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const uint32_t n = t * 16u + col < uint32_t(N) ? t * 16u + col : uint32_t(N) - 1u;
+        wr[t] = w + size_t(n) * k_total + (BF16 ? quad * 8u : quad);
+    }
+    f32x4_t acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    for (uint32_t s0 = begin; s0 < end; s0 += UNROLL) {
+        if constexpr (BF16) {
+            bf16x8_t fa[UNROLL], fb[UNROLL][NT];
+#pragma unroll
+            for (int u = 0; u < UNROLL; ++u) {
+                const uint32_t s = s0 + u < end ? s0 + u : end - 1u;
+                fa[u] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(xr + s * KS));
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    fb[u][t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(wr[t] + s * KS));
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < UNROLL; ++u) {
+                if (s0 + u < end) {
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) {
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[u], fb[u][t], acc[t], 0, 0, 0);
+                    }
+                }
+            }
+        } else {
+            float fa[UNROLL], fb[UNROLL][NT];
+#pragma unroll
+            for (int u = 0; u < UNROLL; ++u) {
+                const uint32_t s = s0 + u < end ? s0 + u : end - 1u;
+                fa[u] = xr[s * KS];
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    fb[u][t] = wr[t][s * KS];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < UNROLL; ++u) {
+                if (s0 + u < end) {
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) {
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[u], fb[u][t], acc[t], 0, 0, 0);
+                    }
+                }
+            }
+        }
+    }
+    // lane holds rows 4 quad .. + 3 of column ``col`` of each 16-column tile
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            partial[wave][quad * 4u + i][t * 16u + col] = acc[t][i];
+        }
+    }
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < 16u * NT * 16u; e += blockDim.x) {
+        const uint32_t r = e / (NT * 16u), c = e % (NT * 16u);
+        if (r0 + r < m && c < uint32_t(N)) {
+            const float sum = ((partial[0][r][c] + partial[1][r][c]) + partial[2][r][c]) + partial[3][r][c];
+            store1<T>(out + size_t(r0 + r) * N + c, sum + (bias ? load1<T>(bias + c) : 0.0f));
+        }
+    }
+}
+
 // ``route_slots`` (one workgroup) turns the [tokens x selected] expert ids into a slot permutation grouped
 // by expert and a table of 128-slot tiles; ids are checked like every gather (negative ids wrap, an id
 // outside [-experts, experts) raises the error word and counts as expert 0). Layout of ``scratch``

@@ -205,6 +205,28 @@ def test_matrix_core_linear(tmp_path, dtype, rows, inner, columns):
     assert_close(got, want, **tolerance(want))
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows, inner, columns", [(2048, 2880, 32), (257, 128, 12), (64, 96, 64), (1000, 4096, 1), (130, 2880, 40)])
+def test_narrow_matrix_core_linear(tmp_path, dtype, rows, inner, columns):
+    """Few columns over many rows (a router's gate over a prefill) on ``narrow_linear``: one workgroup per
+    16 rows, K split over 4 waves (quarters of 90, 4, 3 or 128 MFMA steps, some of different lengths), a
+    partial last row tile (257, 130 rows) and column tiles padded past N (12, 40, 1 columns); against the
+    oracle."""
+    generator = torch.Generator().manual_seed(rows + columns)
+    layer = torch.nn.Linear(inner, columns).eval()
+    with torch.no_grad():
+        layer.weight.copy_(torch.randn(columns, inner, generator=generator) * 0.05)
+        layer.bias.copy_(torch.randn(columns, generator=generator))
+    layer = layer.to(dtype)
+    x = torch.randn(rows, inner, generator=generator).to(dtype)
+    exported = torch.export.export(layer, (x,))
+    with chroma_amd.compile(exported, tmp_path / "hip") as model:
+        assert model.stats["mfma_matmuls"] == 1 and model.stats["launches"] == 1
+        got = model(x)
+    want = compile_cpu(exported, tmp_path / "cpu")(numpy_of(x))
+    assert_close(got, want, **tolerance(want))
+
+
 @pytest.mark.parametrize("rows, inner, columns", [(2048, 320, 4800), (2000, 96, 4803), (1800, 32, 5000), (2600, 512, 3901)])
 def test_wide_matrix_core_linear(tmp_path, rows, inner, columns):
     """bfloat16 products on the wide 256 x 192 body against the oracle: whole tiles; ragged rows and columns
