@@ -1376,9 +1376,6 @@ __device__ __forceinline__ void mfma_linear_wide(const T* __restrict__ x, const 
                       tx * kWideN);
 }
 
-// ---------------------------------------------------------------------------------------------
-// Expert-grouped mixture-of-experts products.
-//
 // Y[M, N] = X[M, K] . W[N, K]^T (+ bias[N]) for few columns (N <= 64: a router's gate) and many rows: one
 // workgroup of 4 waves per 16 rows of X, the waves splitting K into quarters; the matrix-core operands are
 // read straight from global memory (each X row once, W - N x K, small - from L2), 8 k-steps of loads in
@@ -1473,6 +1470,9 @@ __device__ __forceinline__ void narrow_linear(const T* __restrict__ x, const T* 
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Expert-grouped mixture-of-experts products.
+//
 // ``route_slots`` (one workgroup) turns the [tokens x selected] expert ids into a slot permutation grouped
 // by expert and a table of 128-slot tiles; ids are checked like every gather (negative ids wrap, an id
 // outside [-experts, experts) raises the error word and counts as expert 0). Layout of ``scratch``
