@@ -407,6 +407,17 @@ class Kernel:
         else:
             operands = [self.emit(part) for part in node[2:]] if tag in ("un", "bin") else [self.emit(part) for part in node[1:]]
             varying = any(isinstance(o, list) for o in operands)
+            if tag == "rnd" and varying and self.lanes % 2 == 0:
+                # bfloat16 rounding of an intermediate, two lanes per v_cvt_pk_bf16_f32 (a NaN keeps being a
+                # NaN; stores canonicalise it through f32_to_bf16)
+                names = []
+                for lane in range(0, self.lanes, 2):
+                    first, second = self.fresh("n"), self.fresh("n")
+                    self.line(f"float {first} = {operands[0][lane]}, {second} = {operands[0][lane + 1]};")
+                    self.line(f"chroma::round_bf16_pair({first}, {second});")
+                    names += [first, second]
+                self.nodes[node] = names
+                return names
             lanes = range(self.lanes) if varying else [None]
             names = []
             for lane in lanes:
@@ -416,7 +427,7 @@ class Kernel:
                 elif tag == "bin":
                     code = BINARY_CODE[node[1]].format(a=args[0], b=args[1])
                 elif tag == "rnd":
-                    code = f"chroma::round_bf16({args[0]})"
+                    code = f"chroma::round_bf16_fast({args[0]})"
                 elif tag == "sel":
                     code = f"({args[0]} ? {args[1]} : {args[2]})"
                 else:

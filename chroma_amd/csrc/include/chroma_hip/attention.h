@@ -21,9 +21,11 @@
 
 namespace chroma {
 
+// Rounding of an intermediate value to the storage type (the values stay in registers or LDS; results
+// written to memory go through f32_to_bf16).
 template <bool BF16> __device__ __forceinline__ float storage_round(float x) {
     if constexpr (BF16) {
-        return round_bf16(x);
+        return round_bf16_fast(x);
     } else {
         return x;
     }
@@ -772,9 +774,9 @@ template <int D> __device__ __forceinline__ void attention_mfma_bf16(const Atten
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float s = round_bf16(acc[i / 4][i % 4]);
-            const float s1 = round_bf16(s * a.scale);
-            s2[i] = round_bf16(s1 + m[i]);
+            const float s = round_bf16_fast(acc[i / 4][i % 4]);
+            const float s1 = round_bf16_fast(s * a.scale);
+            s2[i] = round_bf16_fast(s1 + m[i]);
         }
     };
 
@@ -957,16 +959,6 @@ __device__ __forceinline__ void attention_live_tiles(const uint16_t* __restrict_
     if (threadIdx.x == 0) {
         live_tiles[qt * gridDim.y + kb] = any ? (zero ? 2 : 1) : 0;
     }
-}
-
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-
-// Round two floats to bfloat16 with one v_cvt_pk_bf16_f32 and widen them back.
-__device__ __forceinline__ void round_bf16_pair(float& x, float& y) {
-    const uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{x, y}, bf16x2_t));
-    x = __uint_as_float(w << 16);
-    y = __uint_as_float(w & 0xffff0000u);
 }
 
 template <int D, int G, bool POW2> __device__ __forceinline__ void attention_heads_mfma_bf16(const AttentionOperands& a) {

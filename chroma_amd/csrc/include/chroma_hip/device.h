@@ -30,6 +30,16 @@ __device__ __forceinline__ float round_bf16(float value) { return bf16_to_f32(f3
 // shift instead of five integer operations. Stored results keep f32_to_bf16, whose NaN is always 0x7fc0.
 __device__ __forceinline__ float round_bf16_fast(float value) { return float(__bf16(value)); }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two intermediate values rounded the same way with one v_cvt_pk_bf16_f32, then widened back.
+__device__ __forceinline__ void round_bf16_pair(float& x, float& y) {
+    const uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{x, y}, bf16x2_t));
+    x = __uint_as_float(w << 16);
+    y = __uint_as_float(w & 0xffff0000u);
+}
+
 // ---------------------------------------------------------------------------------------------
 // Gather row index with the reference's bounds rule (chroma/_src/codegen/cuda/runtime.h:18-32):
 // an index outside [0, count) - or outside [-count, count) when negative indices are allowed - raises
