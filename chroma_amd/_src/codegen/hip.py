@@ -80,6 +80,7 @@ GROUPED_SLOTS = 64  # from this many (token, expert) slots on, expert products a
 FUSED_ROUTER_BYTES = 32 << 10  # a router with gate weights up to this size is recomputed inside its first expert product
 ROUTER_TICKETS = 48  # rows a split router can serve (chroma::kRouterTickets words of the error region)
 NARROW_COLUMNS = 64  # linears of at most this many columns over many rows take one workgroup per 16 rows
+SMALL_INPUT_BYTES = 64 << 10  # inputs up to this size are staged ahead of the larger ones
 MATRIX_ATTENTION_TOKENS = 64  # bfloat16 attention over at least this many queries runs on the matrix cores
 SPLIT_KEYS = 256  # keys per workgroup when an attention row's keys are split over workgroups
 DECODE_SPLIT_KEYS = 128  # the same for stored key/value rows read with 16-byte loads (decode steps)
@@ -2507,10 +2508,12 @@ class HIPCodegen(Codegen):
         workspace_base = _align(weights_size)
         error_base = workspace_base + _align(stats["workspace_bytes"])
         position = error_base + ALIGN
-        input_regions, output_regions = [], []
-        for spec in inputs:
-            input_regions.append((position, nbytes(spec)))
-            position += _align(max(nbytes(spec), 1))
+        input_regions, output_regions = [None] * len(inputs), []
+        # Small inputs first, then large ones (each in input order): a caller that keeps the large ones on
+        # the device (the decoder's caches) uploads all the small ones of a step as one copy.
+        for index in sorted(range(len(inputs)), key=lambda i: nbytes(inputs[i]) > SMALL_INPUT_BYTES):
+            input_regions[index] = (position, nbytes(inputs[index]))
+            position += _align(max(nbytes(inputs[index]), 1))
         for spec in outputs:
             output_regions.append((position, nbytes(spec)))
             position += _align(max(nbytes(spec), 1))

@@ -71,12 +71,19 @@ def _interrupts_deferred() -> Iterator[None]:
 def _staging_mirror(model: Program) -> List[Optional[np.ndarray]]:
     """The decoder's host input arrays (all but the caches, inputs 2 and 3) for a hip program: page-locked
     and placed at the same distances from each other as the program's input staging regions, one block
-    per run of adjacent inputs."""
+    per run of inputs adjacent in the staging (the caches end a run; a step's small inputs, staged ahead of
+    the caches, form one run and go up as one copy)."""
     native = model.native
     specs = model.inputs
     arrays: List[Optional[np.ndarray]] = [None] * len(specs)
-    runs = [[0, 1], [i for i in range(4, len(specs))]]
-    for run in runs:
+    staged = sorted(range(len(specs)), key=native.input_pointer)
+    runs: List[List[int]] = [[]]
+    for i in staged:
+        if i in (2, 3):
+            runs.append([])
+        else:
+            runs[-1].append(i)
+    for run in (run for run in runs if run):
         start = native.input_pointer(run[0])
         sizes = [int(np.prod(specs[i]["shape"])) * numpy_dtype(specs[i]["dtype"]).itemsize for i in run]
         span = native.input_pointer(run[-1]) - start + sizes[-1]
@@ -279,13 +286,15 @@ class Decoder:
         row, layers = self._row_bytes, self._shape[0]
         first = start % self.context
         head = min(count, self.context - first)
-        # Queued on the program's stream: its next run (or a synchronize before another program copies
-        # the cache) comes after them.
+        # Queued on the program's stream, all in one launch: its next run (or a synchronize before another
+        # program copies the cache) comes after them.
+        rects = []
         for output, cache in ((1, 2), (2, 3)):
             src, dst = program.output_pointer(output), program.input_pointer(cache)
-            program.copy_2d(dst + first * row, self.context * row, src, steps * row, head * row, layers, queued=True)
+            rects.append((dst + first * row, self.context * row, src, steps * row, head * row, layers))
             if count > head:
-                program.copy_2d(dst, self.context * row, src + head * row, steps * row, (count - head) * row, layers, queued=True)
+                rects.append((dst, self.context * row, src + head * row, steps * row, (count - head) * row, layers))
+        program.copy_2d_batch(rects)
 
     @property
     def position(self) -> int:

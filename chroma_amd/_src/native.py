@@ -20,6 +20,7 @@ REPO = PACKAGE.parent
 LIBRARY = PACKAGE / "lib" / "libchroma_hip.so"
 RUNTIME_SOURCE = PACKAGE / "csrc" / "runtime.cpp"
 SELECT_SOURCE = PACKAGE / "csrc" / "select.hip"
+COPY_SOURCE = PACKAGE / "csrc" / "copy.hip"
 DEVICE_INCLUDE = PACKAGE / "csrc" / "include"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 
@@ -41,13 +42,15 @@ def build_runtime(output: Path = LIBRARY) -> Path:
     hipcc = shlex.split(os.environ.get("HIPCC", str(ROCM / "bin" / "hipcc")))
     device_flags = [flag for flag in DEVICE_FLAGS if flag != "--genco"]
     with tempfile.TemporaryDirectory(prefix="chroma-runtime-") as work:
-        host_object, device_object = Path(work) / "runtime.o", Path(work) / "select.o"
+        host_object, device_object, copy_object = Path(work) / "runtime.o", Path(work) / "select.o", Path(work) / "copy.o"
         commands = [
             [*shlex.split(os.environ.get("CXX", "g++")), "-std=c++17", "-O2", "-c", "-fPIC", "-fvisibility=hidden", "-D__HIP_PLATFORM_AMD__",
              f"-I{ROCM / 'include'}", str(RUNTIME_SOURCE), "-o", str(host_object)],
             [*hipcc, f"--offload-arch={architecture()}", *device_flags, "-c", "-fPIC", "-fvisibility=hidden", f"-I{DEVICE_INCLUDE}",
              str(SELECT_SOURCE), "-o", str(device_object)],
-            [*hipcc, f"--offload-arch={architecture()}", "-shared", "-fPIC", str(host_object), str(device_object), "-o", str(temporary),
+            [*hipcc, f"--offload-arch={architecture()}", *device_flags, "-c", "-fPIC", "-fvisibility=hidden", f"-I{DEVICE_INCLUDE}",
+             str(COPY_SOURCE), "-o", str(copy_object)],
+            [*hipcc, f"--offload-arch={architecture()}", "-shared", "-fPIC", str(host_object), str(device_object), str(copy_object), "-o", str(temporary),
              f"-L{ROCM / 'lib'}", f"-Wl,-rpath,{ROCM / 'lib'}", "-lamdhip64"],
         ]
         for command in commands:
@@ -56,6 +59,13 @@ def build_runtime(output: Path = LIBRARY) -> Path:
                 raise RuntimeError(f"Building the hip runtime failed:\n{' '.join(command)}\n{result.stderr[-4000:]}")
     os.replace(temporary, output)
     return output
+
+
+class Rect(ctypes.Structure):
+    """``chroma_hip_rect``: one device-to-device rectangle copy."""
+
+    _fields_ = [("dst", ctypes.c_void_p), ("dst_pitch", ctypes.c_size_t), ("src", ctypes.c_void_p), ("src_pitch", ctypes.c_size_t),
+                ("width", ctypes.c_size_t), ("height", ctypes.c_size_t)]
 
 
 def library() -> ctypes.CDLL:
@@ -90,6 +100,7 @@ def library() -> ctypes.CDLL:
             getattr(lib, name).restype = c.c_void_p
         lib.chroma_hip_copy_2d.argtypes = [c.c_void_p, c.c_void_p, c.c_size_t, c.c_void_p, c.c_size_t, c.c_size_t, c.c_size_t, c.c_char_p, c.c_size_t]
         lib.chroma_hip_copy_2d_queued.argtypes = lib.chroma_hip_copy_2d.argtypes
+        lib.chroma_hip_copy_2d_batch_queued.argtypes = [c.c_void_p, c.POINTER(Rect), c.c_int, c.c_char_p, c.c_size_t]
         lib.chroma_hip_synchronize.argtypes = [c.c_void_p, c.c_char_p, c.c_size_t]
         lib.chroma_hip_host_alloc.argtypes = [c.c_size_t, c.POINTER(c.c_void_p), c.c_char_p, c.c_size_t]
         lib.chroma_hip_host_free.argtypes = [c.c_void_p]
@@ -122,6 +133,7 @@ EXPORTED = (
     "chroma_hip_output_pointer",
     "chroma_hip_copy_2d",
     "chroma_hip_copy_2d_queued",
+    "chroma_hip_copy_2d_batch_queued",
     "chroma_hip_synchronize",
     "chroma_hip_host_alloc",
     "chroma_hip_host_free",

@@ -5,6 +5,7 @@
 // arguments are pre-resolved device pointers. ``run`` uploads inputs, launches every kernel (or replays
 // the captured hipGraph), downloads the error word and the outputs, and synchronizes once.
 #include "../../include/chroma_hip.h"
+#include "copy.h"
 #include "select.h"
 
 #include <hip/hip_runtime_api.h>
@@ -410,28 +411,37 @@ public:
     // staging regions go up as one copy (the gaps are padding on both sides).
     void upload(const void* const* inputs) {
         DeviceGuard guard(device_);
+        // Inputs in staging order; a run of adjacent given inputs whose host arrays lie at the same distances
+        // as their staging regions (a page-locked mirror of the staging) goes up as one copy.
         const size_t count = plan_.inputs.size();
-        for (size_t i = 0; i < count;) {
+        std::vector<size_t> order(count);
+        for (size_t i = 0; i < count; ++i) {
+            order[i] = i;
+        }
+        std::sort(order.begin(), order.end(), [&](size_t a, size_t b) { return plan_.inputs[a].offset < plan_.inputs[b].offset; });
+        for (size_t n = 0; n < count;) {
+            const size_t i = order[n];
             if (!plan_.inputs[i].bytes || !inputs[i]) {
-                ++i;
+                ++n;
                 continue;
             }
             const char* first = static_cast<const char*>(inputs[i]);
             const size_t start = plan_.inputs[i].offset;
-            size_t end = i + 1;
-            while (end < count && plan_.inputs[end].bytes && inputs[end] &&
-                   static_cast<const char*>(inputs[end]) - first == std::ptrdiff_t(plan_.inputs[end].offset - start)) {
+            size_t end = n + 1;
+            while (end < count && plan_.inputs[order[end]].bytes && inputs[order[end]] &&
+                   static_cast<const char*>(inputs[order[end]]) - first == std::ptrdiff_t(plan_.inputs[order[end]].offset - start)) {
                 ++end;
             }
-            const size_t span = plan_.inputs[end - 1].offset + plan_.inputs[end - 1].bytes - start;
-            if (end - i > 1 && is_pinned(first, span)) {
+            const size_t last = order[end - 1];
+            const size_t span = plan_.inputs[last].offset + plan_.inputs[last].bytes - start;
+            if (end - n > 1 && is_pinned(first, span)) {
                 to_device(static_cast<char*>(base_) + start, first, span);
             } else {
-                for (size_t k = i; k < end; ++k) {
-                    to_device(static_cast<char*>(base_) + plan_.inputs[k].offset, inputs[k], plan_.inputs[k].bytes);
+                for (size_t k = n; k < end; ++k) {
+                    to_device(static_cast<char*>(base_) + plan_.inputs[order[k]].offset, inputs[order[k]], plan_.inputs[order[k]].bytes);
                 }
             }
-            i = end;
+            n = end;
         }
     }
 
@@ -468,6 +478,28 @@ public:
         check(hipMemcpy2DAsync(dst, dst_pitch, src, src_pitch, width, height, hipMemcpyDeviceToDevice, stream_), "hipMemcpy2DAsync");
         if (!queued) {
             check(hipStreamSynchronize(stream_), "Device copy");
+        }
+    }
+
+    // Queued rectangle copies in one kernel launch (copy.hip).
+    void copy_2d_batch(const chroma_hip_rect* rects, int count) {
+        DeviceGuard guard(device_);
+        if (count < 1 || count > chroma_copy::kMaxRects) {
+            throw std::runtime_error("copy_2d_batch takes 1 to 4 rectangles");
+        }
+        chroma_copy::Rect copies[chroma_copy::kMaxRects];
+        int used = 0;
+        for (int i = 0; i < count; ++i) {
+            if (rects[i].width && rects[i].height) {
+                copies[used++] = chroma_copy::Rect{rects[i].dst, rects[i].dst_pitch, rects[i].src, rects[i].src_pitch, rects[i].width, rects[i].height};
+            }
+        }
+        if (!used) {
+            return;
+        }
+        char message[256] = {0};
+        if (chroma_copy::launch_copy_rects(copies, used, stream_, message, sizeof(message))) {
+            throw std::runtime_error(message);
         }
     }
 
@@ -755,6 +787,11 @@ __attribute__((visibility("default"))) void chroma_hip_host_free(void* pointer) 
 __attribute__((visibility("default"))) int chroma_hip_copy_2d(void* handle, void* dst, size_t dst_pitch, const void* src, size_t src_pitch,
                                                               size_t width, size_t height, char* error, size_t error_size) {
     return guarded(error, error_size, [&] { program(handle)->copy_2d(dst, dst_pitch, src, src_pitch, width, height, false); });
+}
+
+__attribute__((visibility("default"))) int chroma_hip_copy_2d_batch_queued(void* handle, const chroma_hip_rect* rects, int count, char* error,
+                                                                            size_t error_size) {
+    return guarded(error, error_size, [&] { program(handle)->copy_2d_batch(rects, count); });
 }
 
 __attribute__((visibility("default"))) int chroma_hip_copy_2d_queued(void* handle, void* dst, size_t dst_pitch, const void* src, size_t src_pitch,

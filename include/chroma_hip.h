@@ -94,6 +94,19 @@ int chroma_hip_copy_2d_queued(void* handle, void* dst, size_t dst_pitch, const v
                               size_t height, char* error, size_t error_size);
 int chroma_hip_synchronize(void* handle, char* error, size_t error_size);
 
+/* Up to four queued device-to-device rectangle copies (as ``chroma_hip_copy_2d_queued``) in one kernel
+ * launch on the program's stream. No counterpart in the reference: the decoder commits a step's new key
+ * and value rows with it (a runtime 2-D copy call costs several times a kernel launch in host time). */
+typedef struct chroma_hip_rect {
+    void* dst;
+    size_t dst_pitch;
+    const void* src;
+    size_t src_pitch;
+    size_t width;  /* bytes per row */
+    size_t height; /* rows */
+} chroma_hip_rect;
+int chroma_hip_copy_2d_batch_queued(void* handle, const chroma_hip_rect* rects, int count, char* error, size_t error_size);
+
 /* Page-locked host memory for arrays that programs read and write: copies to and from it go straight to
  * the DMA engines, while other host arrays above 256 KiB move through two pinned staging slots of the
  * program. ``chroma_hip_host_free`` takes only pointers from ``chroma_hip_host_alloc``. No counterpart

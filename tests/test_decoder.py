@@ -194,6 +194,12 @@ class FakeNative:
         if not queued:
             self.synchronize()
 
+    def copy_2d_batch(self, rects) -> None:
+        # one queued launch copying every rectangle, in order
+        assert 1 <= len(rects) <= 4
+        for rect in rects:
+            self.copy_2d(*rect, queued=True)
+
     def synchronize(self) -> None:
         for copy in self.pending:
             copy()
