@@ -95,17 +95,15 @@ def _staging_mirror(model: Program) -> List[Optional[np.ndarray]]:
 
 
 def _fill_row(mask: np.ndarray, allowed: np.ndarray) -> None:
-    """A one-step mask [1, context + 1]: 0 where ``allowed`` over the cached keys, and 0 for the new key."""
+    """A one-step mask [1, context + 1]: 0 where ``allowed`` over the cached keys, and 0 for the new key.
+    Written through the bit patterns: (not allowed) x the -inf pattern, one ufunc per row."""
     if mask.dtype == np.float32:
-        row = mask[0]
-        np.copyto(row[:-1], np.float32(-np.inf))
-        row[:-1][allowed] = 0
-        row[-1] = 0
+        bits = mask.view(np.uint32)[0]
+        np.multiply(~allowed, np.uint32(0xFF800000), out=bits[:-1])
     else:
         bits = mask.view(np.uint16)[0]
-        bits[:-1] = 0xFF80
-        bits[:-1][allowed] = 0
-        bits[-1] = 0
+        np.multiply(~allowed, np.uint16(0xFF80), out=bits[:-1])
+    bits[-1] = 0
 
 
 def _fill_mask(mask: np.ndarray, allowed: np.ndarray) -> None:
@@ -425,10 +423,13 @@ class Decoder:
                 positions[:] = times
                 if steps == 1:
                     # One new key at the current position: every committed key is older, so the causal
-                    # test reduces to validity and each window test to one comparison.
-                    valid = state.slots >= 0
-                    for mask, window in ((full_mask, self.context), (window_mask, self._window)):
-                        _fill_row(mask, valid & (state.slots > state.position - window))
+                    # test reduces to validity (slot >= 0) and each window test to one comparison; the two
+                    # combine into slot > max(position - window, -1). Equal windows share one row.
+                    _fill_row(full_mask, state.slots > max(state.position - self.context, -1))
+                    if self._window == self.context:
+                        np.copyto(window_mask, full_mask)
+                    else:
+                        _fill_row(window_mask, state.slots > max(state.position - self._window, -1))
                 else:
                     _fill_masks(((full_mask, self.context), (window_mask, self._window)), np.concatenate((state.slots, times)),
                                 np.concatenate((state.slots >= 0, np.ones(steps, dtype=bool))), times)
