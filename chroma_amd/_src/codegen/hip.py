@@ -78,6 +78,7 @@ SMALL_OPERAND_COST = 8  # ...over operands that cost at most this much per eleme
 MATRIX_MIN_WORK = 1 << 18  # smaller batched products stay on the generic contraction kernel
 GROUPED_SLOTS = 64  # from this many (token, expert) slots on, expert products are grouped by expert
 FUSED_ROUTER_BYTES = 32 << 10  # a router with gate weights up to this size is recomputed inside its first expert product
+EARLY_FETCH_BYTES = 1 << 20  # weight streams up to this size are requested before their staging prologue
 ROUTER_TICKETS = 48  # rows a split router can serve (chroma::kRouterTickets words of the error region)
 NARROW_COLUMNS = 64  # linears of at most this many columns over many rows take one workgroup per 16 rows
 SMALL_INPUT_BYTES = 64 << 10  # inputs up to this size are staged ahead of the larger ones
@@ -174,7 +175,7 @@ class HIPCodegen(Codegen):
         self.store_expressions: Dict[str, Value] = {}  # arena buffer -> the expression it holds
         self.pending_stores: Set[str] = set()  # buffers not written yet
         self.resolved_by_launch: Dict[int, List[str]] = {}  # launch index -> buffers that launch writes
-        self.write_through_stores = 0
+        self.write_through_stores: Set[str] = set()  # buffers written by the first kernel that stages them
         self.folded_norms = 0
         self.fused_routers = 0
 
@@ -250,7 +251,7 @@ class HIPCodegen(Codegen):
         return node
 
     def read_flat(self, k: Kernel, value: Value, flat: Aff) -> tuple:
-        if value.stored and value.view.base is None and value.name not in k.unstored:
+        if value.stored and value.view.base is None and value.name not in k.unstored and value.name not in k.staged_values:
             return ("ld", k.slot(value.name, value.dtype, extent=self.extents[value.name]), value.dtype, flat)
         return self.read(k, value, k.unflatten(flat, value.shape))
 
@@ -1131,7 +1132,7 @@ class HIPCodegen(Codegen):
             k.resolved_stores.append(buffer)
             self.pending_stores.discard(buffer)
             resolved.append(buffer)
-            self.write_through_stores += 1
+            self.write_through_stores.add(buffer)  # (a retracted launch's buffers are resolved again by its replacement)
         budget = [LDS_STAGED_FLOATS - rows * inner]
 
         def staging_loop(count: int, element: Callable[[List[Aff]], object], shape: Sequence[int]) -> None:
@@ -1654,12 +1655,20 @@ class HIPCodegen(Codegen):
         b_arg = self._matrix_slot(k, bias) if bias is not None else "nullptr"
         out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
         lead = tuple(x.shape[:-1])
-        # W is requested after the prologue that stages X: vector loads complete in order, so a stream
-        # requested first makes every dependent load of the prologue wait for it (and queue behind it);
-        # measured on the GPT-OSS-20B decode products, the prologue then costs several times its own latency.
+        # A large W is requested after the prologue that stages X: vector loads complete in order, so a
+        # stream requested first makes every dependent load of the prologue wait for it (and queue behind
+        # it); measured on the GPT-OSS-20B decode products, the prologue then costs several times its own
+        # latency. A small W (a few KiB per workgroup) arrives while the prologue runs, so it goes first.
+        early = columns * inner * ITEMSIZE[weight.dtype] <= EARLY_FETCH_BYTES
+        fetch = [f"chroma::StreamStep<{inner}, {lanes}, {steps}, {ctype_of(out.dtype)}> prefetched;",
+                 f"chroma::stream_linear_fetch(prefetched, {w_arg}, {columns}u);"]
+        if early:
+            for line in fetch:
+                k.line(line)
         self._stage(k, x, rows, inner, lambda row: k.unflatten(row, lead) if lead else [], threads)
-        k.line(f"chroma::StreamStep<{inner}, {lanes}, {steps}, {ctype_of(out.dtype)}> prefetched;")
-        k.line(f"chroma::stream_linear_fetch(prefetched, {w_arg}, {columns}u);")
+        if not early:
+            for line in fetch:
+                k.line(line)
         k.line(
             f"chroma::stream_linear<{rows}, {inner}, {lanes}, {steps}, true, {ctype_of(out.dtype)}>("
             f"nullptr, xs, {w_arg}, {b_arg}, {out_slot}, {columns}u, prefetched);"
@@ -1819,7 +1828,7 @@ class HIPCodegen(Codegen):
         if epilogue is not None:
             weight, bias, linear_out, lanes, steps = epilogue
             ctype, inner, columns = ctype_of(out.dtype), group * dim, weight.shape[0]
-            prelude = [lambda k: f"__shared__ float attention_row[{inner}];"]
+            prelude.append(lambda k: f"__shared__ float attention_row[{inner}];")
             store_extra = [f"attention_row[g * {dim}u + d] = chroma::storage_round<{str(bf16).lower()}>(value);"]
         k, _, _ = self._attention_kernel(out, q, k_past, k_new, v_past, v_new, mask, sinks, None, prelude=prelude, store_extra=store_extra)
         k.line(f"chroma::attention_waves<{dim}, {group}, {str(bf16).lower()}>({keys}u, {float_literal(scale)}, "
@@ -2271,10 +2280,17 @@ class HIPCodegen(Codegen):
                 coords_of = lambda _row: [k.div(slot, selected), k.mod(slot, selected)]
             else:
                 coords_of = lambda _row: [k.div(slot, selected)]
-            # the slab is requested after the prologue (see _stream_linear)
+            # the slab is requested after the prologue, or before it when the experts are small (see _stream_linear)
+            early = channels * inner * ITEMSIZE[weight.dtype] <= EARLY_FETCH_BYTES
+            fetch = [f"chroma::StreamStep<{inner}, {lanes}, {steps}, {ctype_of(out.dtype)}> prefetched;",
+                     f"chroma::stream_expert_fetch(prefetched, {w}, {idx}, {experts}u, {channels}u, error);"]
+            if early:
+                for line in fetch:
+                    k.line(line)
             self._stage(k, x, 1, inner, coords_of, threads)
-            k.line(f"chroma::StreamStep<{inner}, {lanes}, {steps}, {ctype_of(out.dtype)}> prefetched;")
-            k.line(f"chroma::stream_expert_fetch(prefetched, {w}, {idx}, {experts}u, {channels}u, error);")
+            if not early:
+                for line in fetch:
+                    k.line(line)
             k.line(
                 f"chroma::stream_expert_linear<{inner}, {lanes}, {steps}, true, {ctype_of(out.dtype)}, {per_expert}>("
                 f"{w}, {idx}, nullptr, xs, {out_slot}, {selected}u, {experts}u, {channels}u, {blocks_per_slot}u, error, prefetched);"
@@ -2562,7 +2578,7 @@ class HIPCodegen(Codegen):
             routed_experts=self.routed_experts,
             small_contractions=self.small_contractions,
             attention_epilogues=self.attention_epilogues,
-            write_through_stores=self.write_through_stores,
+            write_through_stores=len(self.write_through_stores),
             unique_kernels=len(self.kernel_sources),
             launches=len(self.launches),
         )
