@@ -1945,7 +1945,7 @@ class HIPCodegen(Codegen):
                 base = k.slot(root.name, root.dtype, extent=self.extents[root.name])
                 staged_rows = f"load_{name}_new" if name == needed else "nullptr"
                 sources.append(f"chroma::KeyRows<{ctype}>{{{base} + {offset}u + blockIdx.y * {strides[1]}u, {strides[0]}u, {past}u, {staged_rows}}}")
-            k.line(f"chroma::attention_decode<{phase}, {dim}, {group}, {str(bf16).lower()}, {ctype}>(begin, end, {keys}u, {float_literal(scale)}, "
+            k.line(f"chroma::attention_decode<{phase}, {dim}, {group}, {str(bf16).lower()}, {ctype}, {DECODE_SPLIT_KEYS}>(begin, end, {keys}u, {float_literal(scale)}, "
                    f"load_q, {sources[0]}, {sources[1]}, load_mask, load_sink, {split}, "
                    f"{scores_slot} + (size_t(blockIdx.x) * {kv_heads}u + blockIdx.y) * {keys * group}u);")
             self.launch(k, (tokens, kv_heads, splits), 256, inputs + [stats, scores] + ([partial] if phase == 2 else []), kind=f"attention_decode{phase}")
@@ -1981,12 +1981,18 @@ class HIPCodegen(Codegen):
             with k.block(f"auto {name} = [&]({signature}) -> float {{", "};"):
                 coords = [Aff.of(Atom(p, hi)) for p, hi in params]
                 if split is None:
-                    k.line(f"return {k.emit(body(coords))};")
+                    node = body(coords)
+                    k.hoist_loads(node)
+                    k.line(f"return {k.emit(node)};")
                     return
                 bound, first, second = split
                 with k.block(f"if ({params[0][0]} < {bound}u) {{"):
-                    k.line(f"return {k.emit(first(coords))};")
-                k.line(f"return {k.emit(second(coords))};")
+                    node = first(coords)
+                    k.hoist_loads(node)
+                    k.line(f"return {k.emit(node)};")
+                node = second(coords)
+                k.hoist_loads(node)
+                k.line(f"return {k.emit(node)};")
 
         fresh_only = fresh
         fresh = keys - past
@@ -2002,10 +2008,18 @@ class HIPCodegen(Codegen):
                 # cooperatively, into LDS; the key loops then read plain LDS values.
                 k.line(f"__shared__ float {name}_new[{fresh * dim}];")
                 with k.block(f"if ({fresh_only[1]}) {{" if fresh_only is not None else "{"):
-                    with k.block(f"for (uint32_t i = threadIdx.x; i < {fresh * dim}u; i += blockDim.x) {{"):
-                        i = Aff.of(Atom("i", fresh * dim - 1))
-                        row, column = k.div(i, dim), k.mod(i, dim)
-                        k.line(f"{name}_new[i] = {k.emit(self.read(k, new_value, [row, h, column]))};")
+                    # Runs of 32 elements, one per wave (its other 32 lanes idle): each half of a head's
+                    # row (the two sides of a rotary embedding) is evaluated by whole waves, without
+                    # diverging.
+                    runs = -(-fresh * dim // 32)
+                    with k.block(f"for (uint32_t slot = threadIdx.x; slot < {runs * 64}u; slot += blockDim.x) {{"):
+                        k.line("const uint32_t i = slot / 64u * 32u + slot % 64u;")
+                        with k.block(f"if (slot % 64u < 32u && i < {fresh * dim}u) {{"):
+                            i = Aff.of(Atom("i", fresh * dim - 1))
+                            row, column = k.div(i, dim), k.mod(i, dim)
+                            node = self.read(k, new_value, [row, h, column])
+                            k.hoist_loads(node)
+                            k.line(f"{name}_new[i] = {k.emit(node)};")
                 if fresh_only is not None:
                     return
 

@@ -440,6 +440,30 @@ class Kernel:
         self.nodes[node] = result
         return result
 
+    def hoist_loads(self, node: Node) -> None:
+        """Emit every memory load of ``node`` before any of its arithmetic (the loads of a piecewise part
+        are hoisted to the top of that part's branch instead), so they are all requested at once: emitted
+        where the expression needs them, a load after a libm call (whose branches split basic blocks) waits
+        a round trip of its own. Every generated address is proven in bounds for its atoms' whole ranges
+        and gathered indices are checked when the expression is built, so an earlier load reads nothing
+        the expression would not have read. Not while chunk loads are logged or replayed (their order is
+        fixed)."""
+        if self.load_log is not None or self.load_replay is not None:
+            return
+        stack, seen = [node], set()
+        while stack:
+            current = stack.pop()
+            if not isinstance(current, tuple) or current in seen:
+                continue
+            seen.add(current)
+            tag = current[0]
+            if tag == "ld":
+                self.emit(current)
+            elif tag in ("un", "bin"):
+                stack.extend(reversed(current[2:]))
+            elif tag in ("rnd", "sel"):
+                stack.extend(reversed(current[1:]))
+
     def _emit_cases(self, node: Node) -> Union[str, List[str]]:
         """("cases", tests, parts): parts[i] for the first true tests[i] (the last part otherwise). With
         uniform tests only the selected part is evaluated (one branch each); tests that vary across lanes
@@ -463,6 +487,7 @@ class Kernel:
                 self.line("} else {" if tests else "{")
             saved = (dict(self.atoms), dict(self.nodes), dict(self.values))
             self.indent += 1
+            self.hoist_loads(part)
             value = self.emit(part)
             for lane, name in enumerate(names):
                 self.line(f"{name} = {value[lane] if isinstance(value, list) else value};")

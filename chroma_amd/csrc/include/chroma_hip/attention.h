@@ -357,17 +357,66 @@ template <class T> struct KeyRows {
     const float* fresh;
 };
 
-// Workgroup: 4 waves over keys [begin, end) of one (query row, key/value head). A key's D elements are
-// LPK lanes x one 16-byte chunk each (N elements), so a wave takes 64 / LPK consecutive keys per load and
-// every load instruction reads whole rows; the mask values of those keys are requested with them.
-// Query heads' dot products meet through a butterfly over the LPK lanes. PHASE 1 writes the masked
-// scores of the keys ([keys][G] at ``scores``) and the split's statistics; PHASE 2 merges every split's
-// statistics with the sink (32 lanes per head, each merging every 32nd split, then a butterfly: the loads
-// go out together instead of one dependent round trip per split), then writes the split's partial p . v
-// sums (``attention_combine`` adds the splits in order). A split whose mask is -inf for every key and head
-// reads no rows and writes no scores (its statistics are (-inf, 0) and its partial sums 0: exactly what
-// its keys contribute as long as their rows are finite).
-template <int PHASE, int D, int G, bool BF16, class T, class LoadQ, class LoadMask, class LoadSink>
+// Sum of v over the LPK consecutive lanes of a key group (LPK a power of two): DPP quad permutations,
+// then the half-row and row mirrors (within a group whose quads already agree, a mirror partner holds the
+// same quad sum as the xor partner), then permlane swaps across rows and half-waves, so every lane of the
+// group holds the same sum, added in the order of an xor butterfly.
+template <int LPK> __device__ __forceinline__ float key_group_sum(float v) {
+    if constexpr (LPK >= 2) v += dpp_partner<0xB1>(v);   // lane ^ 1
+    if constexpr (LPK >= 4) v += dpp_partner<0x4E>(v);   // lane ^ 2
+    if constexpr (LPK >= 8) v += dpp_partner<0x141>(v);  // the other quad of each 8 lanes
+    if constexpr (LPK >= 16) v += dpp_partner<0x140>(v); // the other half of each 16-lane row
+    if constexpr (LPK >= 32) {
+        const auto rows = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(rows[0]) + __uint_as_float(rows[1]);
+    }
+    if constexpr (LPK >= 64) {
+        const auto halves = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(halves[0]) + __uint_as_float(halves[1]);
+    }
+    return v;
+}
+
+// Sum of v over the lanes of a wave that share lane % FROM (FROM a power of two), added in the order of an
+// xor butterfly over the offsets FROM, 2 FROM, .., 32: lanes 8 apart meet through DPP (row_ror:8 within
+// 16-lane rows), rows and half-waves through gfx950's permlane swaps; smaller offsets through
+// ``__shfl_xor``.
+template <int FROM> __device__ __forceinline__ float lane_groups_sum(float v) {
+    if constexpr (FROM >= 8) {
+        if constexpr (FROM == 8) {
+            v += dpp_partner<0x128>(v);  // row_ror:8 = lane ^ 8 within each 16-lane row
+        }
+        if constexpr (FROM <= 16) {
+            const auto rows = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+            v = __uint_as_float(rows[0]) + __uint_as_float(rows[1]);
+        }
+        if constexpr (FROM <= 32) {
+            const auto halves = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+            v = __uint_as_float(halves[0]) + __uint_as_float(halves[1]);
+        }
+        return v;
+    } else {
+#pragma unroll
+        for (int offset = FROM; offset < kWave; offset <<= 1) {
+            v += __shfl_xor(v, offset, kWave);
+        }
+        return v;
+    }
+}
+
+// Workgroup: 4 waves over keys [begin, end) of one (query row, key/value head), end - begin <= SPAN. A
+// key's D elements are LPK lanes x one 16-byte chunk each (N elements), so a wave takes 64 / LPK
+// consecutive keys per load and every load instruction reads whole rows; a thread takes U keys, all
+// requested at once. Query heads' dot products meet through the LPK lanes (DPP). PHASE 1 writes the
+// masked scores of the keys ([keys][G] at ``scores``) and the split's statistics; PHASE 2 merges every
+// split's statistics with the sink (32 lanes per head, each merging every 32nd split, then a butterfly),
+// then writes the split's partial p . v sums (``attention_combine`` adds the splits in order). Each
+// phase requests its stored rows (and phase 2 its scores) before the barrier at which the workgroup
+// decides whether the split is live, so that round trip overlaps the mask vote or the statistics merge;
+// rows the staging prologue evaluated into LDS are read after that barrier. A split whose mask is -inf
+// for every key and head computes nothing and writes no scores (its statistics are (-inf, 0) and its
+// partial sums 0: exactly what its keys contribute as long as their rows are finite).
+template <int PHASE, int D, int G, bool BF16, class T, int SPAN, class LoadQ, class LoadMask, class LoadSink>
 __device__ __forceinline__ void attention_decode(uint32_t begin, uint32_t end, uint32_t keys, float scale, LoadQ load_q, KeyRows<T> k_rows,
                                                  KeyRows<T> v_rows, LoadMask load_mask, LoadSink load_sink, AttentionSplit split,
                                                  float* scores) {
@@ -376,7 +425,8 @@ __device__ __forceinline__ void attention_decode(uint32_t begin, uint32_t end, u
     constexpr int LPK = D / N;
     constexpr int KPW = kWave / LPK;
     constexpr int WAVES = 4;
-    static_assert(D % N == 0 && LPK <= kWave && (LPK & (LPK - 1)) == 0, "attention_decode shape");
+    constexpr int U = (SPAN + WAVES * KPW - 1) / (WAVES * KPW);
+    static_assert(D % N == 0 && LPK <= kWave && (LPK & (LPK - 1)) == 0 && U <= 8, "attention_decode shape");
     __shared__ float q_s[G][D];
     __shared__ float wave_peak[WAVES][G], wave_total[WAVES][G];
     __shared__ float peak_s[G], total_s[G];
@@ -384,31 +434,50 @@ __device__ __forceinline__ void attention_decode(uint32_t begin, uint32_t end, u
     const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
     const uint32_t kq = lane / LPK, c = lane % LPK;
     const float neg_inf = -__builtin_inff();
+    (void)keys;
 
-    auto chunk = [&](const KeyRows<T>& source, uint32_t j, float (&out)[N]) {
-        if (j < source.past) {
-            const u32x4_t bits = C::load(source.rows + size_t(j) * source.stride + c * N);
+    // A key's chunk: the stored row's 16 bytes, requested unconditionally (a new key requests the last
+    // stored row instead, so no load waits inside a branch), widened after the barrier; a new key's
+    // values come from the LDS rows the staging prologue evaluated.
+    auto key_of = [&](int u) { return begin + uint32_t(u) * WAVES * KPW + wave * KPW + kq; };
+    auto request = [&](const KeyRows<T>& source, uint32_t j) -> u32x4_t {
+        const uint32_t row = j < source.past ? j : source.past - 1;
+        return C::load(source.rows + size_t(row) * source.stride + c * N);
+    };
+    auto widen = [&](const KeyRows<T>& source, uint32_t j, const u32x4_t& bits, float (&out)[N]) {
+        const bool stored = j < source.past;
+        const uint32_t at = (stored ? 0u : j - source.past) * D + c * N;
 #pragma unroll
-            for (int e = 0; e < N; ++e) {
-                out[e] = C::get(bits, e);
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < N; ++e) {
-                out[e] = source.fresh[(j - source.past) * D + c * N + e];
-            }
+        for (int e = 0; e < N; ++e) {
+            out[e] = stored ? C::get(bits, e) : source.fresh[at + e];
         }
     };
 
     if constexpr (PHASE == 1) {
-        // Is any key of the split unmasked for any head? (The mask and query loads go out together; one
-        // barrier both publishes the staged queries and answers.)
-        bool live = false;
-        for (uint32_t i = tid; i < (end - begin) * G; i += blockDim.x) {
-            live |= load_mask(begin + i / G, i % G) != neg_inf;
+        // Is any key of the split unmasked for any head? The query, the stored key rows and the mask
+        // values of this thread's keys (which cover the split) are all requested before the barrier that
+        // both publishes the staged queries and answers.
+        // Element e of the query in the order (half of D, head, position in the half): a wave's 64
+        // elements lie in one half of a head (the two sides of a rotary embedding), so the loader's
+        // branch on the half does not diverge.
+        constexpr uint32_t HALF = D / 2;
+#pragma unroll
+        for (uint32_t e = tid; e < uint32_t(G * D); e += WAVES * kWave) {
+            const uint32_t half = e / (G * HALF), g = e % (G * HALF) / HALF, d = half * HALF + e % HALF;
+            q_s[g][d] = load_q(g, d);
         }
-        for (uint32_t i = tid; i < uint32_t(G * D); i += blockDim.x) {
-            q_s[i / D][i % D] = load_q(i / D, i % D);
+        u32x4_t k_bits[U];
+        float mk[U][G];
+        bool live = false;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t jj = key_of(u) < end ? key_of(u) : end - 1;
+            k_bits[u] = request(k_rows, jj);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                mk[u][g] = load_mask(jj, g);
+                live |= key_of(u) < end && mk[u][g] != neg_inf;
+            }
         }
         if (!__syncthreads_or(live)) {
             if (tid < uint32_t(G)) {
@@ -417,59 +486,32 @@ __device__ __forceinline__ void attention_decode(uint32_t begin, uint32_t end, u
             }
             return;
         }
-        float q[G][N];
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-#pragma unroll
-            for (int e = 0; e < N; ++e) {
-                q[g][e] = q_s[g][c * N + e];
-            }
-        }
         float peak[G], total[G];
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             peak[g] = neg_inf;
             total[g] = 0.0f;
         }
-        constexpr int U = 4;  // key steps whose rows are requested together
-        for (uint32_t j0 = begin + wave * KPW + kq; j0 < end; j0 += U * WAVES * KPW) {
-            float kv[U][N], mk[U][G];
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const uint32_t j = j0 + u * WAVES * KPW;
-                const uint32_t jj = j < end ? j : end - 1;
-                chunk(k_rows, jj, kv[u]);
+        for (int u = 0; u < U; ++u) {
+            const uint32_t j = key_of(u);
+            float kv[N];
+            widen(k_rows, j < end ? j : end - 1, k_bits[u], kv);
 #pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    mk[u][g] = load_mask(jj, g);
+            for (int g = 0; g < G; ++g) {
+                float dot = 0.0f;
+#pragma unroll
+                for (int e = 0; e < N; ++e) {
+                    dot += q_s[g][c * N + e] * kv[e];
                 }
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const uint32_t j = j0 + u * WAVES * KPW;
-                float s2[G];
-#pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    float dot = 0.0f;
-#pragma unroll
-                    for (int e = 0; e < N; ++e) {
-                        dot += q[g][e] * kv[u][e];
-                    }
-#pragma unroll
-                    for (int offset = 1; offset < LPK; offset <<= 1) {
-                        dot += __shfl_xor(dot, offset, kWave);
-                    }
-                    const float s = storage_round<BF16>(dot);
-                    const float s1 = storage_round<BF16>(s * scale);
-                    s2[g] = storage_round<BF16>(s1 + mk[u][g]);
-                }
+                dot = key_group_sum<LPK>(dot);
+                const float s = storage_round<BF16>(dot);
+                const float s1 = storage_round<BF16>(s * scale);
+                const float s2 = storage_round<BF16>(s1 + mk[u][g]);
                 if (j < end) {
-#pragma unroll
-                    for (int g = 0; g < G; ++g) {
-                        softmax_stats_add(peak[g], total[g], s2[g]);
-                        if (uint32_t(g % LPK) == c) {
-                            scores[size_t(j) * G + g] = s2[g];
-                        }
+                    softmax_stats_add(peak[g], total[g], s2);
+                    if (uint32_t(g % LPK) == c) {
+                        scores[size_t(j) * G + g] = s2;
                     }
                 }
             }
@@ -496,15 +538,45 @@ __device__ __forceinline__ void attention_decode(uint32_t begin, uint32_t end, u
             split.stats[(split.split * G + tid) * 2 + 1] = sum;
         }
     } else {
+        // The stored value rows and the scores of this thread's keys go out first (a live split reads
+        // them; a split without unmasked keys wrote no scores, and its loads are never used).
+        u32x4_t v_bits[U];
+        float sc[U][G];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t jj = key_of(u) < end ? key_of(u) : end - 1;
+            v_bits[u] = request(v_rows, jj);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                sc[u][g] = scores[size_t(jj) * G + g];
+            }
+        }
         // The row's statistics: every split's, then the sink; the split is live if any head's own
         // statistics are.
         static_assert(G * 32 <= WAVES * kWave, "one 32-lane group per query head");
         bool live = false;
         {
-            const uint32_t g = tid / 32u, l = tid % 32u;
+            // the first FIRST splits of each lane (and this split's own peak) are requested together
+            constexpr int FIRST = 2;
+            const uint32_t g = tid / 32u, l = tid % 32u, gg = g < uint32_t(G) ? g : 0u;
             float top = neg_inf, sum = 0.0f;
+            float split_peak[FIRST], split_total[FIRST];
+#pragma unroll
+            for (int i = 0; i < FIRST; ++i) {
+                const uint32_t w = l + 32u * i < split.splits ? l + 32u * i : 0u;
+                split_peak[i] = split.stats[(w * G + gg) * 2];
+                split_total[i] = split.stats[(w * G + gg) * 2 + 1];
+            }
+            const float own_peak = split.stats[(split.split * G + gg) * 2];
+            // a lane past the last split merges (-inf, 0), which changes nothing (the merges stay
+            // unconditional so that the loads are not sunk into a branch)
+#pragma unroll
+            for (int i = 0; i < FIRST; ++i) {
+                const bool real = l + 32u * i < split.splits;
+                softmax_stats_merge(top, sum, real ? split_peak[i] : neg_inf, real ? split_total[i] : 0.0f);
+            }
             if (g < uint32_t(G)) {
-                for (uint32_t w = l; w < split.splits; w += 32u) {
+                for (uint32_t w = l + 32u * FIRST; w < split.splits; w += 32u) {
                     softmax_stats_merge(top, sum, split.stats[(w * G + g) * 2], split.stats[(w * G + g) * 2 + 1]);
                 }
             }
@@ -516,7 +588,7 @@ __device__ __forceinline__ void attention_decode(uint32_t begin, uint32_t end, u
                 softmax_stats_add(top, sum, load_sink(g));
                 peak_s[g] = top;
                 total_s[g] = sum;
-                live = split.stats[(split.split * G + g) * 2] != neg_inf;
+                live = own_peak != neg_inf;
             }
         }
         float* partial = split.partial + size_t(split.split) * G * D;
@@ -526,12 +598,6 @@ __device__ __forceinline__ void attention_decode(uint32_t begin, uint32_t end, u
             }
             return;
         }
-        float peak[G], total[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            peak[g] = peak_s[g];
-            total[g] = total_s[g];
-        }
         float acc[G][N];
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -540,30 +606,18 @@ __device__ __forceinline__ void attention_decode(uint32_t begin, uint32_t end, u
                 acc[g][e] = 0.0f;
             }
         }
-        constexpr int U = 4;
-        for (uint32_t j0 = begin + wave * KPW + kq; j0 < end; j0 += U * WAVES * KPW) {
-            float vv[U][N];
-            float sc[U][G];
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const uint32_t j = j0 + u * WAVES * KPW;
-                const uint32_t jj = j < end ? j : end - 1;
-                chunk(v_rows, jj, vv[u]);
+        for (int u = 0; u < U; ++u) {
+            const uint32_t j = key_of(u);
+            float vv[N];
+            widen(v_rows, j < end ? j : end - 1, v_bits[u], vv);
+            if (j < end) {
 #pragma unroll
                 for (int g = 0; g < G; ++g) {
-                    sc[u][g] = scores[size_t(jj) * G + g];
-                }
-            }
+                    const float p = storage_round<BF16>(fast_exp(sc[u][g] - peak_s[g]) / total_s[g]);
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                if (j0 + u * WAVES * KPW < end) {
-#pragma unroll
-                    for (int g = 0; g < G; ++g) {
-                        const float p = storage_round<BF16>(fast_exp(sc[u][g] - peak[g]) / total[g]);
-#pragma unroll
-                        for (int e = 0; e < N; ++e) {
-                            acc[g][e] += p * vv[u][e];
-                        }
+                    for (int e = 0; e < N; ++e) {
+                        acc[g][e] += p * vv[e];
                     }
                 }
             }
@@ -573,10 +627,7 @@ __device__ __forceinline__ void attention_decode(uint32_t begin, uint32_t end, u
         for (int g = 0; g < G; ++g) {
 #pragma unroll
             for (int e = 0; e < N; ++e) {
-#pragma unroll
-                for (int offset = LPK; offset < kWave; offset <<= 1) {
-                    acc[g][e] += __shfl_xor(acc[g][e], offset, kWave);
-                }
+                acc[g][e] = lane_groups_sum<LPK>(acc[g][e]);
             }
         }
         if (kq == 0) {
