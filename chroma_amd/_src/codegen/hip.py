@@ -1135,15 +1135,25 @@ class HIPCodegen(Codegen):
             self.write_through_stores.add(buffer)  # (a retracted launch's buffers are resolved again by its replacement)
         budget = [LDS_STAGED_FLOATS - rows * inner]
 
-        def staging_loop(count: int, element: Callable[[List[Aff]], object], shape: Sequence[int]) -> None:
-            """Before a loop over ``count`` staged elements: element 0 is evaluated at the enclosing scope,
-            so row indices gathered through values that do not depend on the element (a token's id, the
-            selected experts) are loaded and checked once instead of once per unrolled batch (the unused
-            element-0 loads are dropped by the compiler); loops of up to 16 iterations are unrolled whole,
-            so every element's loads are in flight together."""
+        def staging_loop(count: int, element: Callable[[List[Aff]], object], shape: Sequence[int], target: str) -> None:
+            """``target[i] = element(i)`` for the ``count`` staged elements. Element 0 is evaluated at the
+            enclosing scope first, so row indices gathered through values that do not depend on the element
+            (a token's id, the selected experts) are loaded and checked once instead of once per unrolled
+            batch (the unused element-0 loads are dropped by the compiler). The loop runs a fixed number of
+            trips per thread, unrolled whole up to 16 (else by 8): a thread past the end evaluates the last
+            element again (its loads stay in bounds) and stores that same value to it, so no load sits
+            behind a per-trip branch (the compiler would sink it into the guarded store) and every trip's
+            loads are in flight together."""
             k.emit(element(k.unflatten(ZERO, shape) if shape else []))
             iterations = -(-count // threads)
+            ragged = count % threads != 0
             k.line(f"#pragma unroll {iterations if iterations <= 16 else 8}")
+            with k.block(f"for (uint32_t trip = 0; trip < {iterations}u; ++trip) {{"):
+                k.line(f"const uint32_t slot = threadIdx.x + trip * {threads}u;")
+                k.line(f"const uint32_t i = slot < {count}u ? slot : {count - 1}u;" if ragged else "const uint32_t i = slot;")
+                i = Aff.of(Atom("i", count - 1))
+                value = k.emit(element(k.unflatten(i, shape) if shape else []))
+                k.line(f"{target}[i] = {value};")
 
         def stage_rows(value: Value, key: str) -> bool:
             """Evaluate ``value`` once into a __shared__ float array (row-major) read in its place."""
@@ -1154,10 +1164,7 @@ class HIPCodegen(Codegen):
             budget[0] -= count
             array = k.fresh("hs")
             k.line(f"__shared__ float {array}[{count}];")
-            staging_loop(count, lambda coords: self.read(k, value, coords), shape if value.shape else [])
-            with k.block(f"for (uint32_t i = threadIdx.x; i < {count}u; i += {threads}u) {{"):
-                i = Aff.of(Atom("i", count - 1))
-                k.line(f"{array}[i] = {k.emit(self.read(k, value, k.unflatten(i, shape) if value.shape else []))};")
+            staging_loop(count, lambda coords: self.read(k, value, coords), shape if value.shape else [], array)
             k.staged_values[key] = array
             return True
 
@@ -1229,11 +1236,7 @@ class HIPCodegen(Codegen):
         if k.norm_scales:
             k.line("chroma::lds_barrier();")
         k.line(f"__shared__ float {array}[{rows * inner}];")
-        staging_loop(rows * inner, lambda coords: self.read(k, x, [*coords_of(coords[0]), coords[1]]), (rows, inner))
-        with k.block(f"for (uint32_t i = threadIdx.x; i < {rows * inner}u; i += {threads}u) {{"):
-            i = Aff.of(Atom("i", rows * inner - 1))
-            row, column = k.div(i, inner), k.mod(i, inner)
-            k.line(f"{array}[i] = {k.emit(self.read(k, x, [*coords_of(row), column]))};")
+        staging_loop(rows * inner, lambda coords: self.read(k, x, [*coords_of(coords[0]), coords[1]]), (rows, inner), array)
         k.line("chroma::lds_barrier();")
         k.norm_scales = {}
 
