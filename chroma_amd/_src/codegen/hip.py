@@ -92,6 +92,8 @@ STAGED_FLOATS = 8192  # X rows up to this many floats are widened into LDS once 
 STAGED_ROWS = 4096  # new key/value rows of an attention up to this many floats are evaluated into LDS once
 FOLDED_NORM_ROWS = 16  # RMSNorms over at most this many rows are folded into the kernels that stage them
 LDS_STAGED_FLOATS = 12288  # floats a staging prologue may keep in LDS (X rows and evaluated operands)
+SPLIT_STAGING_TRIPS = 8  # staging loops of at least this many trips request every trip's loads first...
+STAGED_LOAD_REGISTERS = 128  # ...when those loads fit this many registers
 FOLDED_STAGING_BLOCKS = 1024  # staging kernels with more workgroups read a stored copy of an expression operand
 
 UNARY_OPS = {
@@ -1147,13 +1149,41 @@ class HIPCodegen(Codegen):
             k.emit(element(k.unflatten(ZERO, shape) if shape else []))
             iterations = -(-count // threads)
             ragged = count % threads != 0
-            k.line(f"#pragma unroll {iterations if iterations <= 16 else 8}")
-            with k.block(f"for (uint32_t trip = 0; trip < {iterations}u; ++trip) {{"):
+
+            def trip_header() -> List[Node]:
                 k.line(f"const uint32_t slot = threadIdx.x + trip * {threads}u;")
                 k.line(f"const uint32_t i = slot < {count}u ? slot : {count - 1}u;" if ragged else "const uint32_t i = slot;")
-                i = Aff.of(Atom("i", count - 1))
-                value = k.emit(element(k.unflatten(i, shape) if shape else []))
-                k.line(f"{target}[i] = {value};")
+                node = element(k.unflatten(Aff.of(Atom("i", count - 1)), shape) if shape else [])
+                return node
+
+            # Whole-unrolled loops of many trips whose loads fit in registers are split in two: every trip's
+            # loads first (into per-trip arrays), then, past a scheduling barrier, every trip's arithmetic.
+            # In one loop the compiler interleaves later trips' loads with earlier trips' arithmetic and
+            # waits for each; a few trips it already requests together.
+            probe = k.load_nodes(element(k.unflatten(ZERO, shape) if shape else []))
+            words = sum(2 if is_int(node[2]) else 1 for node in probe)
+            split = SPLIT_STAGING_TRIPS <= iterations <= 16 and 0 < words * iterations <= STAGED_LOAD_REGISTERS
+            arrays: List[str] = []
+            if split:
+                for load in probe:
+                    arrays.append(k.fresh("pre"))
+                    k.line(f"{'int64_t' if is_int(load[2]) else 'float'} {arrays[-1]}[{iterations}];")
+                k.line("#pragma unroll")
+                with k.block(f"for (uint32_t trip = 0; trip < {iterations}u; ++trip) {{"):
+                    loads = k.load_nodes(trip_header())
+                    assert len(loads) == len(arrays), "two traversals of one staged element differ"
+                    for load, array in zip(loads, arrays):
+                        k.line(f"{array}[trip] = {k.emit(load)};")
+                k.line('__asm__ volatile("" ::: "memory");')
+            k.line(f"#pragma unroll {iterations if iterations <= 16 else 8}")
+            with k.block(f"for (uint32_t trip = 0; trip < {iterations}u; ++trip) {{"):
+                node = trip_header()
+                if split:
+                    loads = k.load_nodes(node)
+                    assert len(loads) == len(arrays), "two traversals of one staged element differ"
+                    for load, array in zip(loads, arrays):
+                        k.nodes[load] = f"{array}[trip]"
+                k.line(f"{target}[i] = {k.emit(node)};")
 
         def stage_rows(value: Value, key: str) -> bool:
             """Evaluate ``value`` once into a __shared__ float array (row-major) read in its place."""

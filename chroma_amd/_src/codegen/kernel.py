@@ -22,7 +22,7 @@ from __future__ import annotations
 import contextlib
 import itertools
 import math
-from typing import Dict, Iterator, List, Optional, Sequence, Tuple, Union
+from typing import Set, Dict, Iterator, List, Optional, Sequence, Tuple, Union
 
 import torch
 
@@ -463,6 +463,30 @@ class Kernel:
                 stack.extend(reversed(current[2:]))
             elif tag in ("rnd", "sel"):
                 stack.extend(reversed(current[1:]))
+
+    @staticmethod
+    def load_nodes(node: Node) -> List[Node]:
+        """The memory loads of ``node`` outside its piecewise parts, each once, in a fixed order (the same
+        for two expressions of the same structure)."""
+        order: List[Node] = []
+        seen: Set[Node] = set()
+
+        def walk(current) -> None:
+            if not isinstance(current, tuple) or current in seen:
+                return
+            seen.add(current)
+            tag = current[0]
+            if tag == "ld":
+                order.append(current)
+            elif tag in ("un", "bin"):
+                for part in current[2:]:
+                    walk(part)
+            elif tag in ("rnd", "sel"):
+                for part in current[1:]:
+                    walk(part)
+
+        walk(node)
+        return order
 
     def _emit_cases(self, node: Node) -> Union[str, List[str]]:
         """("cases", tests, parts): parts[i] for the first true tests[i] (the last part otherwise). With
