@@ -1160,26 +1160,31 @@ class HIPCodegen(Codegen):
             # loads first (into per-trip arrays), then, past a scheduling barrier, every trip's arithmetic.
             # In one loop the compiler interleaves later trips' loads with earlier trips' arithmetic and
             # waits for each; a few trips it already requests together.
-            probe = k.load_nodes(element(k.unflatten(ZERO, shape) if shape else []))
-            words = sum(2 if is_int(node[2]) else 1 for node in probe)
-            split = SPLIT_STAGING_TRIPS <= iterations <= 16 and 0 < words * iterations <= STAGED_LOAD_REGISTERS
+            # (Loads that do not depend on the trip were emitted with element 0 and are not repeated.)
             arrays: List[str] = []
+            split = SPLIT_STAGING_TRIPS <= iterations <= 16
             if split:
-                for load in probe:
-                    arrays.append(k.fresh("pre"))
-                    k.line(f"{'int64_t' if is_int(load[2]) else 'float'} {arrays[-1]}[{iterations}];")
+                mark, indent = len(k.lines), k.indent
+                declarations = []
                 k.line("#pragma unroll")
                 with k.block(f"for (uint32_t trip = 0; trip < {iterations}u; ++trip) {{"):
-                    loads = k.load_nodes(trip_header())
-                    assert len(loads) == len(arrays), "two traversals of one staged element differ"
-                    for load, array in zip(loads, arrays):
-                        k.line(f"{array}[trip] = {k.emit(load)};")
-                k.line('__asm__ volatile("" ::: "memory");')
+                    loads = [load for load in k.load_nodes(trip_header()) if load not in k.nodes]
+                    words = sum(2 if is_int(load[2]) else 1 for load in loads)
+                    split = 0 < words * iterations <= STAGED_LOAD_REGISTERS
+                    for load in loads if split else []:
+                        arrays.append(k.fresh("pre"))
+                        declarations.append(f"{'int64_t' if is_int(load[2]) else 'float'} {arrays[-1]}[{iterations}];")
+                        k.line(f"{arrays[-1]}[trip] = {k.emit(load)};")
+                if split:
+                    k.lines[mark:mark] = ["    " * indent + line for line in declarations]
+                    k.line('__asm__ volatile("" ::: "memory");')
+                else:
+                    del k.lines[mark:]
             k.line(f"#pragma unroll {iterations if iterations <= 16 else 8}")
             with k.block(f"for (uint32_t trip = 0; trip < {iterations}u; ++trip) {{"):
                 node = trip_header()
                 if split:
-                    loads = k.load_nodes(node)
+                    loads = [load for load in k.load_nodes(node) if load not in k.nodes]
                     assert len(loads) == len(arrays), "two traversals of one staged element differ"
                     for load, array in zip(loads, arrays):
                         k.nodes[load] = f"{array}[trip]"
