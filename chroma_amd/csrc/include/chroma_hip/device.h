@@ -86,6 +86,18 @@ __device__ __forceinline__ float fast_tanh(float x) {
 __device__ __forceinline__ float fast_silu(float x) { return x * fast_sigmoid(x); }
 
 // ---------------------------------------------------------------------------------------------
+// Words that one workgroup hands to another within a kernel. A device-scope store writes through the
+// XCD's L2 (``global_store ... sc1``) and a device-scope load does not take a stale L2 line, so once the
+// storing thread's stores are complete (s_waitcnt vmcnt(0)) a later device-scope load in any workgroup
+// sees them, without the whole-L2 write-back and invalidate of a device-scope fence. The handoff itself
+// (a ticket) is a device-scope atomic taken after the stores complete.
+template <class T> __device__ __forceinline__ void store_device(T* p, T v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+template <class T> __device__ __forceinline__ T load_device(const T* p) {
+    return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void device_stores_complete() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// ---------------------------------------------------------------------------------------------
 // Streaming (non-temporal) vector stores for results no later instruction of the same kernel reads.
 typedef float float2_nt __attribute__((ext_vector_type(2)));
 typedef float float4_nt __attribute__((ext_vector_type(4)));

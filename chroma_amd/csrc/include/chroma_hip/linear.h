@@ -548,8 +548,9 @@ __device__ __forceinline__ void router_row(const float* xs, const T* __restrict_
 // A router whose gate weights are too large for one workgroup's stream (GPT-OSS-20B: 32 x 2880): grid.x
 // parts (the first wave of each; the other waves only share the staging prologue, whose row loads are
 // then all in flight at once) compute G = 64 / LPR experts' logits of row blockIdx.y (bias added, rounded and
-// stored as router_rows stores them); each part then fences its stores and takes a ticket from the row's
-// counter, and the part that takes the last ticket selects: it reads the row's stored logits, picks the
+// stored as router_rows stores them, with device-scope stores); each part then waits for its stores to
+// complete and takes a ticket from the row's counter, and the part that takes the last ticket selects: it
+// reads the row's stored logits with device-scope loads, picks the
 // top k with router_rows' ranking and tie rules and writes values, int64 indices and the softmax of the
 // values, then resets the counter to 0 for the next launch. No part waits for another. ``counter`` holds
 // one word per row (kRouterTickets at most), zero when the kernel starts: the program's error region,
@@ -589,10 +590,10 @@ __device__ __forceinline__ void router_split(const float* xs, const T* __restric
             partial += __shfl_xor(partial, offset, kWave);
         }
         if (sub == 0 && e < uint32_t(E)) {
-            row_logits[e] = storage_of<T>(partial + (bias ? load1<T>(bias + e) : 0.0f));
+            store_device(row_logits + e, storage_of<T>(partial + (bias ? load1<T>(bias + e) : 0.0f)));
         }
     }
-    __threadfence();  // this part's logits are visible before its ticket is
+    device_stores_complete();  // this part's logits are visible to device-scope loads before its ticket is taken
     __shared__ unsigned int ticket;
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -602,11 +603,10 @@ __device__ __forceinline__ void router_split(const float* xs, const T* __restric
     if (ticket != parts - 1 || threadIdx.x >= kWave) {
         return;
     }
-    __threadfence();  // every other part's logits are visible to the last one
     float logit = 0.0f;
     uint64_t key = 0;
     if (lane < uint32_t(E)) {
-        logit = widen_of<T>(row_logits[lane]);  // after the acquiring fence: every part's stored, rounded logit
+        logit = widen_of<T>(load_device(row_logits + lane));  // every part's stored, rounded logit
         key = topk_key(logit, lane, LARGEST);
     }
     float chosen[E];
