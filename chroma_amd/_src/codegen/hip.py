@@ -80,6 +80,8 @@ GROUPED_SLOTS = 64  # from this many (token, expert) slots on, expert products a
 FUSED_ROUTER_BYTES = 32 << 10  # a router with gate weights up to this size is recomputed inside its first expert product
 EARLY_FETCH_BYTES = 1 << 20  # weight streams up to this size are requested before their staging prologue
 ROUTER_TICKETS = 48  # rows a split router can serve (chroma::kRouterTickets words of the error region)
+ERROR_REGION = 1024  # bytes of the error region: error word, router tickets, decode-attention tickets
+ATTENTION_TICKETS = 64  # (query row, head) rows a split-key decode attention can serve (chroma::kAttentionTickets)
 NARROW_COLUMNS = 64  # linears of at most this many columns over many rows take one workgroup per 16 rows
 SMALL_INPUT_BYTES = 64 << 10  # inputs up to this size are staged ahead of the larger ones
 MATRIX_ATTENTION_TOKENS = 64  # bfloat16 attention over at least this many queries runs on the matrix cores
@@ -1817,7 +1819,7 @@ class HIPCodegen(Codegen):
                 return out
         inputs = [v for v in (q, k_past, k_new, v_past, v_new, mask, sinks) if v is not None]
         rows = self._decode_rows(k_past, v_past, keys - past, dim)
-        if rows is not None and keys > 4 * DECODE_SPLIT_KEYS and tokens * kv_heads < 64:
+        if rows is not None and keys > 4 * DECODE_SPLIT_KEYS and tokens * kv_heads <= min(63, ATTENTION_TICKETS):
             self._decode_attention(out, q, k_past, k_new, v_past, v_new, mask, sinks, scale, rows, inputs)
             self.fused_attentions += 1
             return out
@@ -1958,7 +1960,8 @@ class HIPCodegen(Codegen):
     def _decode_attention(self, out, q, k_past, k_new, v_past, v_new, mask, sinks, scale, rows: dict, inputs: List[Value]) -> None:
         """Long key ranges for a few query rows (decode steps) with ``attention_decode``: the keys are split
         over workgroups of ``DECODE_SPLIT_KEYS``; phase 1 writes the masked scores and each split's
-        statistics, phase 2 the split's partial p . v sums, and the combine kernel adds the splits in order."""
+        statistics, phase 2 the split's partial p . v sums, and its last split to finish adds the splits in
+        order (a ticket per (query row, head) in the program's error region, returned to zero)."""
         tokens, kv_heads, group, dim = q.shape
         past = k_past.shape[0]
         keys = past + k_new.shape[0]
@@ -1983,16 +1986,12 @@ class HIPCodegen(Codegen):
                 base = k.slot(root.name, root.dtype, extent=self.extents[root.name])
                 staged_rows = f"load_{name}_new" if name == needed else "nullptr"
                 sources.append(f"chroma::KeyRows<{ctype}>{{{base} + {offset}u + blockIdx.y * {strides[1]}u, {strides[0]}u, {past}u, {staged_rows}}}")
+            k.uses_error = True  # phase 2's last split takes its ticket from the error region
             k.line(f"chroma::attention_decode<{phase}, {dim}, {group}, {str(bf16).lower()}, {ctype}, {DECODE_SPLIT_KEYS}>(begin, end, {keys}u, {float_literal(scale)}, "
                    f"load_q, {sources[0]}, {sources[1]}, load_mask, load_sink, {split}, "
-                   f"{scores_slot} + (size_t(blockIdx.x) * {kv_heads}u + blockIdx.y) * {keys * group}u);")
+                   f"{scores_slot} + (size_t(blockIdx.x) * {kv_heads}u + blockIdx.y) * {keys * group}u, store, "
+                   f"error + chroma::kAttentionTicketWord + blockIdx.x * {kv_heads}u + blockIdx.y);")
             self.launch(k, (tokens, kv_heads, splits), 256, inputs + [stats, scores] + ([partial] if phase == 2 else []), kind=f"attention_decode{phase}")
-        # the splits are added in a launch of their own: a last-split combine needs a device-scope release
-        # in every split (an L2 write-back on this chip), which costs more than the launch
-        k, _, row = self._attention_kernel(out, q, k_past, k_new, v_past, v_new, mask, sinks, (stats, partial, splits), loaders=False)
-        table = k.slot(partial.name, torch.float32, extent=self.extents[partial.name])
-        k.line(f"chroma::attention_combine<{dim}, {group}>({table} + {row} * {group * dim}u, {splits}u, store);")
-        self.launch(k, (tokens, kv_heads, 1), 256, [partial], kind="attention_combine")
 
     def _attention_kernel(self, out, q, k_past, k_new, v_past, v_new, mask, sinks, split, loaders: bool = True,
                           prelude: Sequence = (), fresh: Optional[Tuple[Tuple[str, ...], str]] = None,
@@ -2575,7 +2574,7 @@ class HIPCodegen(Codegen):
         weights_size = len(self.weights)
         workspace_base = _align(weights_size)
         error_base = workspace_base + _align(stats["workspace_bytes"])
-        position = error_base + ALIGN
+        position = error_base + ERROR_REGION
         input_regions, output_regions = [None] * len(inputs), []
         # Small inputs first, then large ones (each in input order): a caller that keeps the large ones on
         # the device (the decoder's caches) uploads all the small ones of a step as one copy.

@@ -410,16 +410,19 @@ template <int FROM> __device__ __forceinline__ float lane_groups_sum(float v) {
 // requested at once. Query heads' dot products meet through the LPK lanes (DPP). PHASE 1 writes the
 // masked scores of the keys ([keys][G] at ``scores``) and the split's statistics; PHASE 2 merges every
 // split's statistics with the sink (32 lanes per head, each merging every 32nd split, then a butterfly),
-// then writes the split's partial p . v sums (``attention_combine`` adds the splits in order). Each
+// then writes the split's partial p . v sums, and the last split to finish adds the splits in order. Each
 // phase requests its stored rows (and phase 2 its scores) before the barrier at which the workgroup
 // decides whether the split is live, so that round trip overlaps the mask vote or the statistics merge;
 // rows the staging prologue evaluated into LDS are read after that barrier. A split whose mask is -inf
 // for every key and head computes nothing and writes no scores (its statistics are (-inf, 0) and its
 // partial sums 0: exactly what its keys contribute as long as their rows are finite).
-template <int PHASE, int D, int G, bool BF16, class T, int SPAN, class LoadQ, class LoadMask, class LoadSink>
+constexpr uint32_t kAttentionTicketWord = 64;  // first word of the decode attentions' tickets in the error region
+constexpr uint32_t kAttentionTickets = 64;     // (query row, key/value head) rows with a ticket word
+
+template <int PHASE, int D, int G, bool BF16, class T, int SPAN, class LoadQ, class LoadMask, class LoadSink, class Store>
 __device__ __forceinline__ void attention_decode(uint32_t begin, uint32_t end, uint32_t keys, float scale, LoadQ load_q, KeyRows<T> k_rows,
                                                  KeyRows<T> v_rows, LoadMask load_mask, LoadSink load_sink, AttentionSplit split,
-                                                 float* scores) {
+                                                 float* scores, Store store, unsigned int* ticket_word) {
     using C = Chunk16<T>;
     constexpr int N = C::N;
     constexpr int LPK = D / N;
@@ -592,10 +595,48 @@ __device__ __forceinline__ void attention_decode(uint32_t begin, uint32_t end, u
             }
         }
         float* partial = split.partial + size_t(split.split) * G * D;
+        // The last split to finish adds every split's partial sums in split order (``attention_combine``'s
+        // sum) and returns the ticket word to 0; the partial sums pass between workgroups through
+        // device-scope stores and loads around the ticket.
+        auto finish = [&]() {
+            device_stores_complete();
+            __shared__ unsigned int ticket_s;
+            __syncthreads();
+            if (tid == 0) {
+                ticket_s = atomicAdd(ticket_word, 1u);
+            }
+            __syncthreads();
+            if (ticket_s != split.splits - 1) {
+                return;
+            }
+            constexpr uint32_t BATCH = 64;  // splits whose loads go out together
+            for (uint32_t i = tid; i < uint32_t(G * D); i += blockDim.x) {
+                float sum = 0.0f;
+                for (uint32_t s0 = 0; s0 < split.splits; s0 += BATCH) {
+                    float part[BATCH];
+#pragma unroll
+                    for (uint32_t j = 0; j < BATCH; ++j) {
+                        const uint32_t s = s0 + j < split.splits ? s0 + j : split.splits - 1;
+                        part[j] = load_device(split.partial + size_t(s) * G * D + i);
+                    }
+#pragma unroll
+                    for (uint32_t j = 0; j < BATCH; ++j) {
+                        if (s0 + j < split.splits) {
+                            sum += part[j];
+                        }
+                    }
+                }
+                store(i / D, i % D, sum);
+            }
+            if (tid == 0) {
+                atomicExch(ticket_word, 0u);
+            }
+        };
         if (!__syncthreads_or(live)) {
             for (uint32_t i = tid; i < uint32_t(G * D); i += blockDim.x) {
-                partial[i] = 0.0f;
+                store_device(partial + i, 0.0f);
             }
+            finish();
             return;
         }
         float acc[G][N];
@@ -645,8 +686,9 @@ __device__ __forceinline__ void attention_decode(uint32_t begin, uint32_t end, u
             for (int w = 0; w < WAVES; ++w) {
                 sum += acc_s[w][i / D][i % D];
             }
-            partial[i] = sum;
+            store_device(partial + i, sum);
         }
+        finish();
     }
 }
 

@@ -68,7 +68,7 @@ struct Region {
 // through two pinned staging slots of kStagingSlot bytes: the CPU copy into or out of one slot overlaps
 // the DMA of the other (HIP's own pageable path reaches about a third of the link's pinned rate).
 constexpr size_t kDirectBytes = size_t(256) << 10;
-constexpr size_t kErrorRegion = 256;  // bytes the plan reserves at its error offset
+constexpr size_t kErrorRegion = 1024;  // bytes the plan reserves at its error offset
 constexpr size_t kStagingSlot = size_t(2) << 20;
 
 std::mutex pinned_mutex;
@@ -211,8 +211,9 @@ public:
             check(hipEventCreate(&stop_), "hipEventCreate");
             check(hipHostMalloc(reinterpret_cast<void**>(&error_host_), sizeof(unsigned), hipHostMallocDefault), "hipHostMalloc");
             check(hipMalloc(&base_, plan_.arena ? plan_.arena : 1), "hipMalloc program allocation");
-            // The whole 256-byte error region starts at zero: word 0 is the index-error flag, words 16-63 are
-            // the per-row tickets of split routers (chroma::router_split), which return them to zero.
+            // The whole error region starts at zero: word 0 is the index-error flag, words 16-63 the per-row
+            // tickets of split routers (chroma::router_split) and words 64-127 those of split-key decode
+            // attentions (chroma::attention_decode); both return them to zero.
             check(hipMemset(static_cast<char*>(base_) + plan_.error, 0, kErrorRegion), "Clear error region");
             upload_weights(directory + "/" + plan_.weights_file);
             check(hipModuleLoad(&module_, (directory + "/" + plan_.code_object).c_str()), "hipModuleLoad");
