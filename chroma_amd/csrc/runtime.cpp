@@ -15,6 +15,7 @@
 #include <cstring>
 #include <fstream>
 #include <algorithm>
+#include <array>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -262,6 +263,7 @@ public:
         if (graph_) {
             hipGraphDestroy(graph_);
         }
+        drop_select_graph();
         if (module_) {
             hipModuleUnload(module_);
         }
@@ -298,6 +300,8 @@ public:
         }
         graph_exec_ = nullptr;
         graph_ = nullptr;
+        select_exec_ = nullptr;
+        select_graph_ = nullptr;
         module_ = nullptr;
         base_ = nullptr;
         select_ = nullptr;
@@ -376,6 +380,7 @@ public:
                 select_host_ = nullptr;
                 select_host_bytes_ = 0;
             }
+            drop_select_graph();
             check(hipMalloc(&select_, need), "hipMalloc selection scratch");
             select_bytes_ = need;
             check(hipHostMalloc(&select_host_, result_bytes, hipHostMallocDefault), "hipHostMalloc selection results");
@@ -386,12 +391,14 @@ public:
         void* device_values = base + align(scratch) + id_bytes;
         try {
             upload(inputs);
-            launch_all();
-            char message[256] = {0};
-            if (chroma_select::launch_rows_topk(static_cast<char*>(base_) + plan_.outputs[index].offset, dtype, rows, width, k, 1,
-                                                device_values, device_ids, select_, scratch, stream_, message, sizeof(message))) {
-                throw HipError(message);
-            }
+            const std::array<size_t, 6> key{size_t(index), size_t(dtype), rows, width, size_t(k), reinterpret_cast<size_t>(select_)};
+            launch_all_then(key, [&]() {
+                char message[256] = {0};
+                if (chroma_select::launch_rows_topk(static_cast<char*>(base_) + plan_.outputs[index].offset, dtype, rows, width, k, 1,
+                                                    device_values, device_ids, select_, scratch, stream_, message, sizeof(message))) {
+                    throw HipError(message);
+                }
+            });
             check(hipMemcpyAsync(error_host_, static_cast<char*>(base_) + plan_.error, sizeof(unsigned), hipMemcpyDeviceToHost, stream_),
                   "Read index error");
             check(hipMemcpyAsync(select_host_, device_ids, result_bytes, hipMemcpyDeviceToHost, stream_), "Download selection");
@@ -605,6 +612,47 @@ private:
         }
     }
 
+    void drop_select_graph() noexcept {
+        if (select_exec_) {
+            hipGraphExecDestroy(select_exec_);
+        }
+        if (select_graph_) {
+            hipGraphDestroy(select_graph_);
+        }
+        select_exec_ = nullptr;
+        select_graph_ = nullptr;
+    }
+
+    // The plan followed by ``select`` (queued on the stream). With graphs on, both replay as one captured
+    // graph, kept for the selection ``key`` it was captured with (so a greedy decode step is one graph
+    // launch: the selection's kernels cost neither host-side launches nor a plain-stream gap).
+    template <class Select> void launch_all_then(const std::array<size_t, 6>& key, Select select) {
+        if (!use_graph_ || plan_.launches.empty()) {
+            launch_direct();
+            select();
+            return;
+        }
+        if (!select_exec_ || select_key_ != key) {
+            drop_select_graph();
+            check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+            try {
+                launch_direct();
+                select();
+            } catch (...) {
+                hipGraph_t broken = nullptr;
+                hipStreamEndCapture(stream_, &broken);
+                if (broken) {
+                    hipGraphDestroy(broken);
+                }
+                throw;
+            }
+            check(hipStreamEndCapture(stream_, &select_graph_), "hipStreamEndCapture");
+            check(hipGraphInstantiate(&select_exec_, select_graph_, nullptr, nullptr, 0), "hipGraphInstantiate");
+            select_key_ = key;
+        }
+        check(hipGraphLaunch(select_exec_, stream_), "hipGraphLaunch");
+    }
+
     void launch_all() {
         if (!use_graph_ || plan_.launches.empty()) {
             launch_direct();
@@ -674,6 +722,10 @@ private:
     size_t select_bytes_ = 0;
     void* select_host_ = nullptr;  // pinned landing area of run_top's ids and values
     size_t select_host_bytes_ = 0;
+    // run_top's plan and selection captured as one graph, for the selection it was captured with
+    hipGraph_t select_graph_ = nullptr;
+    hipGraphExec_t select_exec_ = nullptr;
+    std::array<size_t, 6> select_key_{};
     hipEvent_t staged_[2] = {nullptr, nullptr};
 };
 
