@@ -165,6 +165,75 @@ def test_plan_regions_are_aligned_disjoint_and_every_argument_is_inside_the_allo
             count = int(fields[7])
             offsets = list(map(int, fields[8 : 8 + count]))
             assert len(offsets) == count and all(0 <= o < arena for o in offsets)
+    # the error region (error word, router and decode-attention tickets) is 1 KiB that no region overlaps
+    error = int(next(l for l in lines if l.startswith("error")).split()[1])
+    assert all(start >= error + 1024 or end <= error for start, end in regions)
+
+
+class CachedAttention(torch.nn.Module):
+    """The workload's attention with sinks over past and new keys (gpt_oss.py sdpa, cached.py:38-48)."""
+
+    def forward(self, q, k_past, k_new, v_past, v_new, mask, sinks):
+        tokens, kv_heads, group, dim = q.shape
+        k = torch.cat((k_past, k_new))[:, :, None, :].expand(-1, -1, group, -1)
+        v = torch.cat((v_past, v_new))[:, :, None, :].expand(-1, -1, group, -1)
+        scores = torch.einsum("qhmd,khmd->hmqk", q, k) * (1 / dim**0.5) + mask[None, None, :, :]
+        s = sinks.reshape(kv_heads, group, 1, 1).expand(-1, -1, tokens, -1)
+        weights = torch.softmax(torch.cat([scores, s], dim=-1), dim=-1)[..., :-1]
+        return torch.einsum("hmqk,khmd->qhmd", weights, v)
+
+
+def cached_attention_inputs(tokens, past, kv_heads, group, dim):
+    dtype = torch.bfloat16
+    mask = torch.zeros(tokens, past + tokens, dtype=dtype)
+    return (torch.randn(tokens, kv_heads, group, dim).to(dtype), torch.randn(past, kv_heads, dim).to(dtype),
+            torch.randn(tokens, kv_heads, dim).to(dtype), torch.randn(past, kv_heads, dim).to(dtype),
+            torch.randn(tokens, kv_heads, dim).to(dtype), mask, torch.randn(kv_heads * group).to(dtype))
+
+
+class NormLinear(torch.nn.Module):
+    def __init__(self, width, columns):
+        super().__init__()
+        self.norm = RMSNorm(width)
+        self.linear = torch.nn.Linear(width, columns, bias=False)
+
+    def forward(self, x, y):
+        return self.linear(self.norm(x + y))
+
+
+def test_staging_loops_request_every_trip_before_their_arithmetic():
+    """A one-row product whose X is a norm of a sum (a decode step's QKV product at hidden size 2880):
+    the prologue's staging loops run a fixed 12 trips per thread with a clamped index, and the loop that
+    loads the sum's two operands first requests every trip's loads into per-trip arrays, then does the
+    arithmetic past a scheduling barrier."""
+    module = NormLinear(2880, 512).to(torch.bfloat16)
+    x, y = torch.randn(1, 2880).to(torch.bfloat16), torch.randn(1, 2880).to(torch.bfloat16)
+    source = lower(module, x, y).files["model.hip"]
+    assert "linear_stream" in source
+    assert "for (uint32_t trip = 0; trip < 12u; ++trip) {" in source
+    assert "const uint32_t i = slot < 2880u ? slot : 2879u;" in source
+    arrays = re.findall(r"float (pre\d+)\[12\];", source)
+    assert len(arrays) >= 2 and '__asm__ volatile("" ::: "memory");' in source
+    for array in arrays:
+        assert f"{array}[trip] = " in source  # filled in the loads-only loop ...
+        assert source.count(f"{array}[trip]") >= 2  # ... and read in the arithmetic loop
+
+
+def test_decode_attention_is_two_launches_with_tickets_inside_the_error_region():
+    """A long cache read by few (query row, head) rows: scores and statistics, then partial sums whose last
+    split adds them (no combine launch); each row's ticket word lies in the error region's decode-attention
+    words (64-127). 64 or more rows take the general split-key kernels instead."""
+    generated = lower(CachedAttention(), *cached_attention_inputs(1, 4096, 8, 8, 64))
+    kernels = [line.split()[1] for line in generated.files["model.plan"].splitlines() if line.startswith("launch ")]
+    assert [re.sub(r"_[0-9a-f]{8}$", "", name) for name in kernels] == ["chroma_attention_decode1", "chroma_attention_decode2"]
+    source = generated.files["model.hip"]
+    assert source.count("error + chroma::kAttentionTicketWord + blockIdx.x * 8u + blockIdx.y") == 2
+    header = (ROOT / "chroma_amd/csrc/include/chroma_hip/attention.h").read_text()
+    word = int(re.search(r"kAttentionTicketWord = (\d+)", header).group(1))
+    rows = int(re.search(r"kAttentionTickets = (\d+)", header).group(1))
+    assert word >= 64 and (word + rows) * 4 <= 1024  # router tickets end at word 63; the region is 1 KiB
+    wide = lower(CachedAttention(), *cached_attention_inputs(8, 1024, 8, 1, 64))  # 64 rows
+    assert "chroma_attention_decode" not in wide.files["model.hip"]
 
 
 OPERATIONS_SOURCE = """
