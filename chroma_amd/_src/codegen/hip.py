@@ -1945,6 +1945,8 @@ class HIPCodegen(Codegen):
         lanes = dim // per_chunk
         if dim % per_chunk or lanes > 64 or lanes & (lanes - 1):
             return None
+        if -(-DECODE_SPLIT_KEYS // (4 * (64 // lanes))) > 8:
+            return None  # a thread would hold more than 8 keys of a split (attention_decode's registers)
         layout = {}
         for name, value in (("k", k_past), ("v", v_past)):
             stored, strides = self._in_place(value)
@@ -1987,7 +1989,7 @@ class HIPCodegen(Codegen):
                 staged_rows = f"load_{name}_new" if name == needed else "nullptr"
                 sources.append(f"chroma::KeyRows<{ctype}>{{{base} + {offset}u + blockIdx.y * {strides[1]}u, {strides[0]}u, {past}u, {staged_rows}}}")
             k.uses_error = True  # phase 2's last split takes its ticket from the error region
-            k.line(f"chroma::attention_decode<{phase}, {dim}, {group}, {str(bf16).lower()}, {ctype}, {DECODE_SPLIT_KEYS}>(begin, end, {keys}u, {float_literal(scale)}, "
+            k.line(f"chroma::attention_decode<{phase}, {dim}, {group}, {str(bf16).lower()}, {ctype}, {DECODE_SPLIT_KEYS}>(begin, end, {float_literal(scale)}, "
                    f"load_q, {sources[0]}, {sources[1]}, load_mask, load_sink, {split}, "
                    f"{scores_slot} + (size_t(blockIdx.x) * {kv_heads}u + blockIdx.y) * {keys * group}u, store, "
                    f"error + chroma::kAttentionTicketWord + blockIdx.x * {kv_heads}u + blockIdx.y);")

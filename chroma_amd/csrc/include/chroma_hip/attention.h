@@ -420,7 +420,7 @@ constexpr uint32_t kAttentionTicketWord = 64;  // first word of the decode atten
 constexpr uint32_t kAttentionTickets = 64;     // (query row, key/value head) rows with a ticket word
 
 template <int PHASE, int D, int G, bool BF16, class T, int SPAN, class LoadQ, class LoadMask, class LoadSink, class Store>
-__device__ __forceinline__ void attention_decode(uint32_t begin, uint32_t end, uint32_t keys, float scale, LoadQ load_q, KeyRows<T> k_rows,
+__device__ __forceinline__ void attention_decode(uint32_t begin, uint32_t end, float scale, LoadQ load_q, KeyRows<T> k_rows,
                                                  KeyRows<T> v_rows, LoadMask load_mask, LoadSink load_sink, AttentionSplit split,
                                                  float* scores, Store store, unsigned int* ticket_word) {
     using C = Chunk16<T>;
@@ -437,7 +437,6 @@ __device__ __forceinline__ void attention_decode(uint32_t begin, uint32_t end, u
     const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
     const uint32_t kq = lane / LPK, c = lane % LPK;
     const float neg_inf = -__builtin_inff();
-    (void)keys;
 
     // A key's chunk: the stored row's 16 bytes, requested unconditionally (a new key requests the last
     // stored row instead, so no load waits inside a branch), widened after the barrier; a new key's

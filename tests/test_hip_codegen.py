@@ -219,6 +219,18 @@ def test_staging_loops_request_every_trip_before_their_arithmetic():
         assert source.count(f"{array}[trip]") >= 2  # ... and read in the arithmetic loop
 
 
+@pytest.mark.parametrize("dtype, dim", [(torch.float32, 128), (torch.bfloat16, 256)])
+def test_long_cache_attention_with_wide_heads_cross_compiles(tmp_path, dtype, dim):
+    """Head dimensions whose split would give a decode-attention thread more than 8 keys take the general
+    split-key kernels, and the program builds for gfx950."""
+    mask = torch.zeros(1, 1001, dtype=dtype)
+    inputs = (torch.randn(1, 2, 4, dim).to(dtype), torch.randn(1000, 2, dim).to(dtype), torch.randn(1, 2, dim).to(dtype),
+              torch.randn(1000, 2, dim).to(dtype), torch.randn(1, 2, dim).to(dtype), mask, torch.randn(8).to(dtype))
+    generated = lower(CachedAttention(), *inputs)
+    assert "attention_decode" not in generated.files["model.hip"] and generated.stats["fused_attentions"] == 1
+    build(generated, tmp_path / "program", load=False)
+
+
 def test_decode_attention_is_two_launches_with_tickets_inside_the_error_region():
     """A long cache read by few (query row, head) rows: scores and statistics, then partial sums whose last
     split adds them (no combine launch); each row's ticket word lies in the error region's decode-attention
