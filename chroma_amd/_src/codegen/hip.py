@@ -2605,7 +2605,7 @@ class HIPCodegen(Codegen):
             raise AssertionError(binding)
 
         lines = [
-            "chroma-hip-plan 1",
+            "chroma-hip-plan 2",  # 2: a 1 KiB error region
             f"arena {total}",
             f"weights {weights_size}",
             f"error {error_base}",

@@ -112,7 +112,7 @@ Plan read_plan(const std::string& path) {
     Plan plan;
     std::string line;
     std::getline(stream, line);
-    if (line != "chroma-hip-plan 1") {
+    if (line != "chroma-hip-plan 2") {  // version 2: the error region is 1 KiB (version 1 plans reserved 256 B)
         throw std::runtime_error("Unsupported launch plan version in " + path);
     }
     while (std::getline(stream, line)) {

@@ -287,7 +287,7 @@ def test_build_publishes_and_replaces_artifacts(tmp_path):
     manifest = json.loads((tmp_path / "model.json").read_text())
     assert manifest["version"] == 2 and manifest["stats"]["backend"] == "hip"
     plan = (tmp_path / "model.plan").read_text().splitlines()
-    assert plan[0] == "chroma-hip-plan 1" and any(line.startswith("signature ") for line in plan)
+    assert plan[0] == "chroma-hip-plan 2" and any(line.startswith("signature ") for line in plan)
     assert (tmp_path / manifest["library"]).stat().st_size > 0
 
 
