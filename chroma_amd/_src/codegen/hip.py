@@ -1152,7 +1152,7 @@ class HIPCodegen(Codegen):
             iterations = -(-count // threads)
             ragged = count % threads != 0
 
-            def trip_header() -> List[Node]:
+            def trip_header() -> object:
                 k.line(f"const uint32_t slot = threadIdx.x + trip * {threads}u;")
                 k.line(f"const uint32_t i = slot < {count}u ? slot : {count - 1}u;" if ragged else "const uint32_t i = slot;")
                 node = element(k.unflatten(Aff.of(Atom("i", count - 1)), shape) if shape else [])
@@ -2047,9 +2047,9 @@ class HIPCodegen(Codegen):
                 # cooperatively, into LDS; the key loops then read plain LDS values.
                 k.line(f"__shared__ float {name}_new[{fresh * dim}];")
                 with k.block(f"if ({fresh_only[1]}) {{" if fresh_only is not None else "{"):
-                    # Runs of 32 elements, one per wave (its other 32 lanes idle): each half of a head's
-                    # row (the two sides of a rotary embedding) is evaluated by whole waves, without
-                    # diverging.
+                    # Runs of 32 elements, one per wave (its other 32 lanes idle): with head dimensions of 64
+                    # or more, each half of a head's row (the two sides of a rotary embedding) is evaluated
+                    # by whole waves, without diverging.
                     runs = -(-fresh * dim // 32)
                     with k.block(f"for (uint32_t slot = threadIdx.x; slot < {runs * 64}u; slot += blockDim.x) {{"):
                         k.line("const uint32_t i = slot / 64u * 32u + slot % 64u;")

@@ -22,7 +22,7 @@ from __future__ import annotations
 import contextlib
 import itertools
 import math
-from typing import Set, Dict, Iterator, List, Optional, Sequence, Tuple, Union
+from typing import Dict, Iterator, List, Optional, Sequence, Set, Tuple, Union
 
 import torch
 
