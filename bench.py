@@ -53,6 +53,7 @@ C4_BYTES = 102_957_056 + 12 * (155_856 + 4 * (131_072 + 1_024 + 65_536 + 512)) +
 HBM_PEAK_GBS = 8000.0
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = ROOT / "profiles" / "c2_fused_softmax_traffic.txt"
+C5_DECODE_TRAFFIC_FILE = ROOT / "profiles" / "c5_decode_traffic.txt"
 VOCAB = 201088
 
 
@@ -143,12 +144,12 @@ def timed(call, warmup: int, runs: int) -> dict:
     return {"median_ms": round(statistics.median(samples), 4), "p10_ms": round(samples[len(samples) // 10], 4), "runs": runs}
 
 
-def read_traffic():
-    """HBM bytes per C2 launch from the committed rocprofv3 counter summary, or None."""
-    if not TRAFFIC_FILE.exists():
+def read_traffic(path: Path = TRAFFIC_FILE, key: str = "traffic_bytes_per_launch"):
+    """HBM bytes per launch (per step for C5 decode) from a committed rocprofv3 counter summary, or None."""
+    if not path.exists():
         return None
-    for line in TRAFFIC_FILE.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_launch"):
+    for line in path.read_text().splitlines():
+        if line.startswith(key):
             return int(float(line.split()[-1]))
     return None
 
@@ -530,7 +531,7 @@ def bench_c5(work: Path, steps: int, cpu: bool) -> dict:
         "prefill_roofline": roofline(flops["total"], prefill_ms, bound="mfma"),
         "decode_device_ms": round(decode_ms, 4),
         "decode_algorithmic_bytes": decode_bytes,
-        "decode_roofline": roofline(decode_bytes, decode_ms),
+        "decode_roofline": roofline(decode_bytes, decode_ms, traffic=read_traffic(C5_DECODE_TRAFFIC_FILE, "traffic_bytes_per_step")),
     })
     for name, program in programs.items():
         program.close()
@@ -620,25 +621,58 @@ def c5_slice(work: Path) -> dict:
 
 
 # --------------------------------------------------------------------------------------------- counters
-def counters(work: Path) -> None:
-    """For rocprofv3 --pmc: three launches of the C2 kernel and of a plain copy kernel of known size
-    (``x * 1.0`` over the same [16384, 8192] fp32 input: 512 MiB read, 512 MiB written), which calibrates
-    FETCH_SIZE / WRITE_SIZE."""
+def counters(work: Path, which: str) -> None:
+    """For rocprofv3 --pmc. ``c2``: three launches of the C2 kernel. ``c5``: three replays of the C5 decode plan
+    with all 4096 cache positions valid (two 2048-token prefills fill the cache first); its dispatches are the
+    3 x launches that precede the copy's. Both end with three launches of a plain copy kernel of known size
+    (``x * 1.0`` over a [16384, 8192] fp32 input: 512 MiB read, 512 MiB written), which calibrates FETCH_SIZE /
+    WRITE_SIZE on the same GPU."""
     import torch
 
     import chroma_amd
     from chroma_amd.models.blocks import BandwidthGraph, Copy, bandwidth_inputs
 
     x, y = bandwidth_inputs()
-    programs = [
-        (chroma_amd.compile(torch.export.export(BandwidthGraph(), (x, y)), work / "c2"), [x.numpy(), y.numpy()]),
-        (chroma_amd.compile(torch.export.export(Copy(), (x,)), work / "copy"), [x.numpy()]),
-    ]
-    for program, arrays in programs:
-        program.native.upload(arrays)
+    if which == "c2":
+        program = chroma_amd.compile(torch.export.export(BandwidthGraph(), (x, y)), work / "c2")
+        program.native.upload([x.numpy(), y.numpy()])
         program.native.execute(3)
         log(f"ran {program.stats['launches']} launch(es) x3")
         program.close()
+    else:
+        c5_decode_counters(work)
+    program = chroma_amd.compile(torch.export.export(Copy(), (x,)), work / "copy")
+    program.native.upload([x.numpy()])
+    program.native.execute(3)
+    log(f"copy: ran {program.stats['launches']} launch(es) x3")
+    program.close()
+
+
+def c5_decode_counters(work: Path) -> None:
+    """The C5 decode plan replayed three times on a full cache (the setup of ``bench_c5``)."""
+    import torch
+
+    import chroma_amd
+    from chroma_amd import Decoder
+    from chroma_amd.models.cached import export_cached
+    from chroma_amd.models.dev import make_gpt_oss_20b
+    from chroma_amd.models.variants import gpt_oss_20b
+
+    model = make_gpt_oss_20b(2, generator_device="cuda")
+    torch.cuda.empty_cache()
+    prefill = chroma_amd.compile(export_cached(model, C5_CONTEXT, C5_PREFILL), work / "c5_prefill")
+    decode = chroma_amd.compile(export_cached(model, C5_CONTEXT, 1), work / "c5_decode")
+    del model
+    tokens = torch.randint(0, VOCAB, (2 * C5_PREFILL + 1,), generator=torch.Generator().manual_seed(2)).numpy()
+    with Decoder(prefill, decode, sliding_window=gpt_oss_20b.sliding_window) as decoder:
+        decoder.append(tokens[:C5_PREFILL])
+        decoder.append(tokens[C5_PREFILL : 2 * C5_PREFILL])
+        decoder.append(tokens[2 * C5_PREFILL :])
+        torch.cuda.synchronize()
+        decode.native.execute(3)
+        log(f"C5 decode: ran {decode.stats['launches']} launch(es) x3")
+    prefill.close()
+    decode.close()
 
 
 def run_leg(name: str, leg, work: Path):
@@ -669,7 +703,8 @@ def main() -> None:
     parser.add_argument("--no-extras", action="store_true", help="only the C2 headline (and its CPU baseline)")
     parser.add_argument("--no-cpu", action="store_true", help="skip every oracle (CPU) measurement")
     parser.add_argument("--no-c5", action="store_true", help="skip the GPT-OSS-20B-shaped model (about two minutes: 42 GB of weights)")
-    parser.add_argument("--counters", action="store_true", help="only run the C2 and copy kernels (for rocprofv3 --pmc)")
+    parser.add_argument("--counters", nargs="?", const="c2", choices=["c2", "c5"],
+                        help="only run the C2 kernel (or the C5 decode plan) and a copy kernel, for rocprofv3 --pmc")
     parser.add_argument("--only", choices=["c1", "rows", "dev", "decode", "c5"], help="measure one leg and print it")
     args = parser.parse_args()
     if args.gpus != 1:
@@ -680,7 +715,7 @@ def main() -> None:
     with tempfile.TemporaryDirectory(prefix="chroma-bench-") as directory:
         work = Path(directory)
         if args.counters:
-            counters(work)
+            counters(work, args.counters)
             return
         if args.only:
             legs = {"c1": lambda: bench_c1(work, cpu), "rows": lambda: bench_rows(work, cpu), "dev": lambda: bench_dev(work, cpu),
