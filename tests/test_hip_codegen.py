@@ -43,7 +43,9 @@ def test_bandwidth_graph_is_one_single_pass_kernel():
     assert generated.stats["backend"] == "hip"
     # x and y are each read once with 128-bit loads; the softmax output is written in place (promoted).
     assert source.count("reinterpret_cast<const float4*>") == 2
-    assert "chroma::fast_tanh" in source and "chroma::block_max<4>" in source and "chroma::block_sum<4>" in source
+    # 8192-wide rows split evenly into two float4 steps of 1024 threads: 16 waves per row
+    assert "__launch_bounds__(1024)" in source
+    assert "chroma::fast_tanh" in source and "chroma::block_max<16>" in source and "chroma::block_sum<16>" in source
     plan = generated.files["model.plan"].splitlines()
     launches = [line for line in plan if line.startswith("launch ")]
     assert len(launches) == 1 and launches[0].split()[2:5] == ["64", "1", "1"]
