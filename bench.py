@@ -541,79 +541,89 @@ def bench_c5(work: Path, steps: int, cpu: bool) -> dict:
     return result
 
 
-def router_gaps(model, tokens) -> list:
-    """Per token, the smallest gap between the 4th and 5th router logit over the layers, in bfloat16 ulps
-    of the 4th value, from eager torch; and the eager logits. A token whose gap is a few ulps may be routed
-    to another expert by any other exact summation order of the router's float sums."""
-    import torch
-
-    gates = []
-    hooks = [block.mlp.gate.register_forward_hook(lambda m, i, o: gates.append(o.detach().float())) for block in model.block]
-    with torch.no_grad():
-        logits = model(tokens).float().numpy()
-    for hook in hooks:
-        hook.remove()
-    gaps = None
-    for gate in gates:
-        top = torch.sort(gate, dim=-1, descending=True).values
-        ulp = torch.exp2(torch.floor(torch.log2(top[:, 3].abs().clamp_min(1e-30))) - 7)
-        gap = (top[:, 3] - top[:, 4]).abs() / ulp
-        gaps = gap if gaps is None else torch.minimum(gaps, gap)
-    return [float(g) for g in gaps], logits
-
-
 def c5_slice(work: Path) -> dict:
     """C5 at full width on a reduced slice, hip beside the oracle: 2 layers (one sliding-window layer
     [window 16 at this context], one full layer), all 32 experts, a 64-position cache, a 32-token prefill
-    chunk and 4 single-token steps; the oracle's time per call and, per call, the logits row of its last
-    position against the oracle's, with eager torch's bfloat16 forward against the oracle on the same row
-    (the rounding noise floor) and that token's smallest router gap. A call whose token has a gap of at
-    most 4 bfloat16 ulps may route differently under any exact summation order (eager torch included), so
-    the summary holds the other calls to the bfloat16 bar and lists those apart."""
+    chunk and 4 single-token steps, both through routing probes (``export_cached(..., routing=True)``).
+    Reported: the oracle's time per call; the routing agreement over every (position, layer) decision
+    with each flip and both runs' own gate-logit gaps (oracle/routing.py); per call, the logits row of its
+    last position against the oracle's, with eager torch's bfloat16 forward against the oracle on the same
+    row (the rounding noise floor), and whether the row depends on a flip. Every call is listed; the
+    summary holds the calls that do not depend on a flip to the bfloat16 bar and names the others."""
     import numpy as np
     import torch
 
     import chroma_amd
     from chroma_amd import Decoder
+    from chroma_amd._src.dtypes import bf16_to_float32
     from chroma_amd.models.cached import export_cached
     from chroma_amd.models.dev import make_gpt_oss_20b
     from oracle import compile_cpu
+    from oracle.routing import compare_routing, downstream_of
 
-    def widen(a):
-        return (a.view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+    def gathered(runs):
+        runs = sorted(runs, key=lambda run: run[0])
+        ids = np.concatenate([arrays[1][:, :count] for _, count, arrays in runs], axis=1)
+        logits = np.concatenate([bf16_to_float32(arrays[0][:, :count]) for _, count, arrays in runs], axis=1)
+        return ids, logits
 
-    model = make_gpt_oss_20b(2, num_hidden_layers=2, num_experts=32, sliding_window=16)
+    layers = 2
+    model = make_gpt_oss_20b(2, num_hidden_layers=layers, num_experts=32, sliding_window=16)
     tokens = torch.randint(0, VOCAB, (36,), generator=torch.Generator().manual_seed(2))
-    gaps, eager = router_gaps(model, tokens)
-    graphs = [export_cached(model, 64, 32), export_cached(model, 64, 1)]
+    with torch.no_grad():
+        eager = model(tokens).float().numpy()
+    graphs = [export_cached(model, 64, 32, routing=True), export_cached(model, 64, 1, routing=True)]
     hip = [chroma_amd.compile(g, work / f"c5s_hip{i}") for i, g in enumerate(graphs)]
     cpu = [compile_cpu(g, work / f"c5s_cpu{i}") for i, g in enumerate(graphs)]
     tokens = tokens.numpy()
     times = {"hip": [], "cpu_oracle": []}
-    calls = []
-    with Decoder(*hip, sliding_window=16) as decoder, Decoder(*cpu, sliding_window=16) as reference:
+    rows = []
+    hip_runs, cpu_runs = [], []
+    with Decoder(*hip, sliding_window=16, extra_outputs=True) as decoder, Decoder(*cpu, sliding_window=16, extra_outputs=True) as reference:
         for start, end in ((0, 32), *((i, i + 1) for i in range(32, 36))):
             t0 = time.perf_counter()
-            got = widen(decoder.append(tokens[start:end]))[-1]
+            got = bf16_to_float32(decoder.append(tokens[start:end]))[-1]
             t1 = time.perf_counter()
-            want = widen(reference.append(tokens[start:end]))[-1]
+            want = bf16_to_float32(reference.append(tokens[start:end]))[-1]
             t2 = time.perf_counter()
             times["hip"].append((t1 - t0) * 1e3)
             times["cpu_oracle"].append((t2 - t1) * 1e3)
-            noise = eager[end - 1]
-            calls.append({"position": end - 1, "router_gap_ulps": round(gaps[end - 1], 1),
-                          "max_abs": round(float(np.abs(got - want).max()), 5),
-                          "rel_norm": round(float(np.linalg.norm(got - want) / np.linalg.norm(want)), 5),
-                          "argmax_equal": bool(got.argmax() == want.argmax()), "finite": bool(np.isfinite(got).all()),
-                          "eager_vs_oracle_rel_norm": round(float(np.linalg.norm(noise - want) / np.linalg.norm(want)), 5)})
+            hip_runs += decoder.extras
+            cpu_runs += reference.extras
+            rows.append((end - 1, got, want))
     for program in (*hip, *cpu):
         program.close()
-    decided = [c for c in calls if c["router_gap_ulps"] > 4]
-    summary = {"calls_held": len(decided), "near_tie_positions": [c["position"] for c in calls if c["router_gap_ulps"] <= 4],
-               "rel_norm": max(c["rel_norm"] for c in decided), "max_abs": max(c["max_abs"] for c in decided),
-               "argmax_equal": all(c["argmax_equal"] for c in decided), "all_finite": all(c["finite"] for c in calls),
-               "eager_vs_oracle_rel_norm": max(c["eager_vs_oracle_rel_norm"] for c in decided)}
-    summary["within_bf16_bar"] = summary["rel_norm"] <= 2e-2 and summary["argmax_equal"] and summary["all_finite"]
+    routing = compare_routing(*gathered(hip_runs), *gathered(cpu_runs), bound_ulps=2.0)
+    calls = []
+    for position, got, want in rows:
+        noise = eager[position]
+        calls.append({"position": position, "downstream_of_flip": downstream_of(routing["flips"], position, layers),
+                      "max_abs": round(float(np.abs(got - want).max()), 5),
+                      "rel_norm": round(float(np.linalg.norm(got - want) / np.linalg.norm(want)), 5),
+                      "argmax_equal": bool(got.argmax() == want.argmax()), "finite": bool(np.isfinite(got).all()),
+                      "eager_vs_oracle_rel_norm": round(float(np.linalg.norm(noise - want) / np.linalg.norm(want)), 5)})
+    held = [c for c in calls if not c["downstream_of_flip"]]
+    summary = {
+        "routing_agreement": routing["agreement"],
+        "routing_decisions": f"{routing['matched']}/{routing['compared']} identical, {len(routing['tie_reorders'])} exact-tie reorders "
+                             f"({routing['downstream']} downstream of a flip, {routing['downstream_matched']} of them agree)",
+        "tie_reorders": [{"position": t["position"], "layer": t["layer"], "hip_ids": t["hip_ids"], "oracle_ids": t["ref_ids"],
+                          "hip_lower_id_first": t["hip_lower_id_first"]} for t in routing["tie_reorders"]],
+        "flips": [{"position": f["position"], "layer": f["layer"], "hip_ids": f["hip_ids"], "oracle_ids": f["ref_ids"],
+                   "gaps_ulps_hip_oracle": [[p["hip_gap_ulps"], p["ref_gap_ulps"]] for p in f["pairs"]], "explained": f["explained"]}
+                  for f in routing["flips"]],
+        "unexplained_flips": routing["unexplained"],
+        "hip_ids_are_top4_of_own_logits": not routing["hip_selection_mismatches"],
+        "gate_logits_max_diff_row_ulps": routing["logit_max_diff_ulps"],
+        "flip_bound_ulps": routing["bound_ulps"],
+        "calls_held": len(held), "calls_downstream_of_flip": [c["position"] for c in calls if c["downstream_of_flip"]],
+        "held_rel_norm": max(c["rel_norm"] for c in held) if held else None,
+        "held_max_abs": max(c["max_abs"] for c in held) if held else None,
+        "held_argmax_equal": all(c["argmax_equal"] for c in held),
+        "all_finite": all(c["finite"] for c in calls),
+        "eager_vs_oracle_rel_norm": max(c["eager_vs_oracle_rel_norm"] for c in calls),
+    }
+    summary["held_within_bf16_bar"] = bool(held) and summary["held_rel_norm"] <= 2e-2 and summary["held_argmax_equal"] and summary["all_finite"]
     return {"slice": "2 layers (window 16, full), all 32 experts, hidden 2880, 64/8 heads, vocab 201088, cache 64, 32-token prefill + 4 steps, tokens seed 2",
             "hip_prefill_ms": round(times["hip"][0], 3), "cpu_prefill_ms": round(times["cpu_oracle"][0], 3),
             "hip_step_ms": round(statistics.median(times["hip"][1:]), 3), "cpu_step_ms": round(statistics.median(times["cpu_oracle"][1:]), 3),

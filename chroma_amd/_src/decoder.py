@@ -158,10 +158,12 @@ def _fill_masks(masks: Sequence[Tuple[np.ndarray, int]], key_times: np.ndarray, 
         view[:, past:] = _band(steps, window, np.dtype(bits).str)
 
 
-def _validate(prefill: Program, decode: Program) -> Tuple[dict, dict]:
+def _validate(prefill: Program, decode: Program, extra_outputs: bool = False) -> Tuple[dict, dict]:
     for name, model in (("prefill", prefill), ("decode", decode)):
-        if len(model.inputs) != 7 or len(model.outputs) != 3:
+        if len(model.inputs) != 7 or len(model.outputs) != 3 and not (extra_outputs and len(model.outputs) > 3):
             raise ValueError(f"Decoder {name} wants seven inputs and three outputs, not {len(model.inputs)} and {len(model.outputs)}")
+    if len(prefill.outputs) != len(decode.outputs):
+        raise ValueError("Decoder prefill and decode were not exported as a pair")
     cache, logits = decode.inputs[2], decode.outputs[0]
     steps = prefill.inputs[0]["shape"][0]
     if (
@@ -213,10 +215,14 @@ class _GatheredTopK:
 
 
 class Decoder:
-    def __init__(self, prefill: Program, decode: Program, *, sliding_window: int = 0) -> None:
+    def __init__(self, prefill: Program, decode: Program, *, sliding_window: int = 0, extra_outputs: bool = False) -> None:
+        """``extra_outputs`` (an addition to the reference API) accepts programs that return more than the
+        three outputs (logits, new K rows, new V rows), such as ``export_cached(..., routing=True)``
+        probes; after each ``append`` the ``extras`` property holds, per program run, the first position
+        it consumed, its token count and copies of its extra outputs."""
         if sliding_window < 0:
             raise ValueError(f"sliding_window must be nonnegative, got {sliding_window}")
-        cache, logits = _validate(prefill, decode)
+        cache, logits = _validate(prefill, decode, extra_outputs)
         self._models = (prefill, decode)
         self._shape = tuple(cache["shape"])
         self._cache_dtype = numpy_dtype(cache["dtype"])
@@ -232,14 +238,16 @@ class Decoder:
         # laid out like the program's input staging, so each run of them goes up as one copy.)
         empty = host.empty if self._on_device else np.empty
         self._empty_array = empty
-        self._buffers: List[Tuple[List[Optional[np.ndarray]], List[Optional[np.ndarray]]]] = [
+        self._buffers: List[Tuple[List[Optional[np.ndarray]], List[Optional[np.ndarray]], List[np.ndarray]]] = [
             (
                 _staging_mirror(model) if self._on_device and isinstance(model.native, NativeModel)
                 else [None if i in (2, 3) else empty(spec["shape"], numpy_dtype(spec["dtype"])) for i, spec in enumerate(model.inputs)],
-                [None if self._on_device else np.empty(spec["shape"], dtype=numpy_dtype(spec["dtype"])) for spec in model.outputs[1:]],
+                [None if self._on_device else np.empty(spec["shape"], dtype=numpy_dtype(spec["dtype"])) for spec in model.outputs[1:3]],
+                [empty(spec["shape"], numpy_dtype(spec["dtype"])) for spec in model.outputs[3:]],
             )
             for model in self._models
         ]
+        self._extras: List[Tuple[int, int, List[np.ndarray]]] = []
         self._row_bytes = int(np.prod(self._shape[2:])) * self._cache_dtype.itemsize
         self._selectors: dict = {}  # (k, gathered ids or None) -> top-k selection program (hip pairs)
         self._selector_dir: Optional[str] = None
@@ -257,7 +265,7 @@ class Decoder:
     def _commit(self, state: CacheState) -> None:
         self._state = state
         if not self._on_device:
-            for args, _ in self._buffers:
+            for args, _, _ in self._buffers:
                 args[2], args[3] = state.keys, state.values
 
     # ---------------------------------------------------------------------------- device-resident cache
@@ -297,6 +305,11 @@ class Decoder:
     @property
     def position(self) -> int:
         return self._state.position
+
+    @property
+    def extras(self) -> List[Tuple[int, int, List[np.ndarray]]]:
+        """The last ``append``'s extra outputs: (first position, tokens, arrays) per program run."""
+        return list(self._extras)
 
     @property
     def stats(self) -> dict:
@@ -409,10 +422,11 @@ class Decoder:
             logits = None
             selection = None
             which = 1
+            self._extras = []
             while offset < len(ids):
                 remaining = len(ids) - offset
                 which = 1 if remaining == 1 else 0
-                args, updates = self._buffers[which]
+                args, updates, extras = self._buffers[which]
                 steps = len(args[0])
                 count = min(steps, remaining)
                 state = self._state
@@ -441,18 +455,20 @@ class Decoder:
                 if self._on_device:
                     self._device_cache(which, args)
                     if top is not None and offset + count == len(ids):
-                        selection = self._models[which].run_top_resident(args, [logits, *updates], 0, top)
+                        selection = self._models[which].run_top_resident(args, [logits, *updates, *extras], 0, top)
                     else:
-                        self._models[which].run_resident(args, [logits, *updates])
+                        self._models[which].run_resident(args, [logits, *updates, *extras])
                     with _interrupts_deferred():
                         self._device_commit(which, state.position, count, steps)
                         self._commit(CacheState(None, None, slots, state.position + count, which))
                 else:
-                    self._models[which](*args, out=[logits, *updates])
+                    self._models[which](*args, out=[logits, *updates, *extras])
                     keys, values = state.keys.copy(), state.values.copy()
                     keys[:, rows] = updates[0][:, :count]
                     values[:, rows] = updates[1][:, :count]
                     self._commit(CacheState(keys, values, slots, state.position + count))
+                if extras:
+                    self._extras.append((state.position, count, [array.copy() for array in extras]))
                 offset += count
             return logits, which, selection
 

@@ -6,11 +6,15 @@
 window masks [steps, context + steps] (0 or -inf), and the row whose logits to return [1] int64. It
 returns the logits [1, vocab] and the new key and value rows [layers, steps, kv_heads, head_dim]
 (reference chroma/models/cached.py:9-91).
+
+``routing=True`` (an addition for parity checks, not in the reference) exports a probe of the same graph
+that also returns every layer's router decision: the gate logits [layers, steps, experts] and the chosen
+expert ids [layers, steps, k], outputs 3 and 4. The arithmetic of the other outputs is unchanged.
 """
 
 from __future__ import annotations
 
-from typing import List, Tuple
+from typing import List, Optional, Tuple
 
 import torch
 from torch import Tensor, nn
@@ -19,16 +23,21 @@ from chroma_amd.models.gpt_oss import Transformer
 
 
 class CachedTransformer(nn.Module):
-    def __init__(self, model: Transformer) -> None:
+    def __init__(self, model: Transformer, routing: bool = False, forced: Optional[Tensor] = None) -> None:
+        """``forced`` (eager use only): expert ids [layers, steps, k] every layer takes instead of its own
+        top-k, so an eager run follows another run's routing decisions."""
         super().__init__()
         self.model = model
+        self.routing = routing
+        self.forced = forced
 
     def forward(
         self, tokens: Tensor, positions: Tensor, keys: Tensor, values: Tensor, mask: Tensor, window_mask: Tensor, last: Tensor
-    ) -> Tuple[Tensor, Tensor, Tensor]:
+    ) -> Tuple[Tensor, ...]:
         x = self.model.embedding(tokens)
         new_keys: List[Tensor] = []
         new_values: List[Tensor] = []
+        routing: Optional[List[Tuple[Tensor, Tensor]]] = [] if self.routing else None
         for layer, block in enumerate(self.model.block):
             attention = block.attn
             q, k, v = attention.project(x, positions)
@@ -45,9 +54,12 @@ class CachedTransformer(nn.Module):
             sinks = attention.sinks.reshape(kv_heads, group, 1, 1).expand(-1, -1, steps, -1)
             weights = torch.cat((scores, sinks), dim=-1).softmax(-1)[..., :-1]
             attended = torch.einsum("hmqk,khmd->qhmd", weights, all_v).reshape(steps, -1)
-            x = block.mlp(x + attention.out(attended))
+            x = block.mlp(x + attention.out(attended), routing, None if self.forced is None else self.forced[layer])
         logits = self.model.unembedding(self.model.norm(x)[last])
-        return logits, torch.cat(new_keys, dim=0), torch.cat(new_values, dim=0)
+        if routing is None:
+            return logits, torch.cat(new_keys, dim=0), torch.cat(new_values, dim=0)
+        return (logits, torch.cat(new_keys, dim=0), torch.cat(new_values, dim=0),
+                *(torch.cat([layer[i].unsqueeze(0) for layer in routing], dim=0) for i in (0, 1)))
 
 
 class UncachedTransformer(nn.Module):
@@ -64,7 +76,7 @@ class UncachedTransformer(nn.Module):
         return self.model.unembedding(self.model.norm(x)[position])
 
 
-def export_cached(model: Transformer, context: int, steps: int) -> torch.export.ExportedProgram:
+def export_cached(model: Transformer, context: int, steps: int, routing: bool = False) -> torch.export.ExportedProgram:
     if context < 1 or not 1 <= steps <= context:
         raise ValueError(f"{steps} steps, context {context}")
     first = model.block[0].attn
@@ -80,7 +92,7 @@ def export_cached(model: Transformer, context: int, steps: int) -> torch.export.
         torch.tensor([steps - 1], dtype=torch.int64),
     )
     with torch.no_grad():
-        return torch.export.export(CachedTransformer(model).eval(), examples)
+        return torch.export.export(CachedTransformer(model, routing).eval(), examples)
 
 
 def export_uncached(model: Transformer, context: int) -> torch.export.ExportedProgram:

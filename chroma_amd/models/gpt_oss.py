@@ -14,7 +14,7 @@ from __future__ import annotations
 
 import math
 from dataclasses import dataclass
-from typing import Optional, Tuple
+from typing import List, Optional, Tuple
 
 import torch
 from torch import Tensor, nn
@@ -203,11 +203,22 @@ class MLPBlock(nn.Module):
         self.mlp2_weight = empty(config.num_experts, config.hidden_size, config.intermediate_size)
         self.mlp2_bias = empty(config.num_experts, config.hidden_size)
 
-    def forward(self, x: Tensor) -> Tensor:
+    def forward(self, x: Tensor, routing: Optional[List[Tuple[Tensor, Tensor]]] = None, forced: Optional[Tensor] = None) -> Tensor:
+        """Two additions, not in the reference (which has neither argument), that leave the arithmetic
+        unchanged: with a ``routing`` list the block appends its (gate logits [tokens, experts], expert
+        ids [tokens, k]) to it, so that a probe export can return every layer's routing decision; with
+        ``forced`` expert ids [tokens, k] an eager run takes those experts (and their gate logits as the
+        values) instead of its own top-k, to follow another run's routing."""
         t = self.norm(x)
-        routed = torch.topk(self.gate(t), k=self.experts_per_token, dim=-1, sorted=True)
-        expert_weights = nn.functional.softmax(routed.values, dim=1)
-        experts = routed.indices
+        gate = self.gate(t)
+        if forced is None:
+            routed = torch.topk(gate, k=self.experts_per_token, dim=-1, sorted=True)
+            values, experts = routed.values, routed.indices
+        else:
+            values, experts = torch.gather(gate, -1, forced), forced
+        if routing is not None:
+            routing.append((gate, experts))
+        expert_weights = nn.functional.softmax(values, dim=1)
         t = torch.einsum("beck,bk->bec", self.mlp1_weight[experts, ...], t) + self.mlp1_bias[experts, ...]
         t = swiglu(t, limit=self.swiglu_limit)
         t = torch.einsum("beck,bek->bec", self.mlp2_weight[experts, ...], t)
@@ -222,8 +233,8 @@ class TransformerBlock(nn.Module):
         self.attn = AttentionBlock(config, layer_idx, device)
         self.mlp = MLPBlock(config, device)
 
-    def forward(self, x: Tensor) -> Tensor:
-        return self.mlp(self.attn(x))
+    def forward(self, x: Tensor, routing: Optional[List[Tuple[Tensor, Tensor]]] = None) -> Tensor:
+        return self.mlp(self.attn(x), routing)
 
 
 class Transformer(nn.Module):

@@ -95,3 +95,13 @@ def leaves(value: Any) -> list:
     if hasattr(value, "values") and hasattr(value, "indices") and not isinstance(value, (np.ndarray, torch.Tensor)):
         return [value.values, value.indices]
     return [value]
+
+
+def gathered_routing(runs) -> tuple:
+    """(expert ids [layers, positions, k], gate logits [layers, positions, experts] as float32) over the
+    runs of ``Decoder.extras`` (first position, tokens, [gate logits, expert ids]) of routing probes, in
+    position order."""
+    runs = sorted(runs, key=lambda run: run[0])
+    ids = np.concatenate([arrays[1][:, :count] for _, count, arrays in runs], axis=1)
+    logits = np.concatenate([as_float(arrays[0][:, :count]) for _, count, arrays in runs], axis=1)
+    return ids, logits
