@@ -54,6 +54,9 @@ HBM_PEAK_GBS = 8000.0
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = ROOT / "profiles" / "c2_fused_softmax_traffic.txt"
 C5_DECODE_TRAFFIC_FILE = ROOT / "profiles" / "c5_decode_traffic.txt"
+ROWS_TRAFFIC_FILE = ROOT / "profiles" / "row_reductions_traffic.txt"
+SMALL_TRAFFIC_FILE = ROOT / "profiles" / "c1_c3_c4_traffic.txt"
+C5_PREFILL_COUNTERS_FILE = ROOT / "profiles" / "c5_prefill_mfma_counters.txt"
 VOCAB = 201088
 
 
@@ -106,6 +109,20 @@ def device_ms(program, runs: int, warmup: int = 3) -> float:
     return native.execute(runs, timed=True) / runs
 
 
+def chained_ms(program, copies: int, iterations: int) -> float:
+    """Time of one execution of ``program``'s plan from hipEvents around ``iterations`` launches of one graph
+    holding ``copies`` back-to-back executions: each kernel's own time plus the dispatch barrier in front of
+    it, without the host's per-replay graph launch (~10 us), which would otherwise set a one-kernel plan."""
+    native = program.native
+    native.execute(1)
+    return native.execute_chained(copies, iterations)
+
+
+def plan_kernels(directory: Path) -> list:
+    """Kernel names of a compiled artifact's launches, in order (from its model.plan)."""
+    return [line.split()[1] for line in (directory / "model.plan").read_text().splitlines() if line.startswith("launch ")]
+
+
 def interleaved(calls: dict, warmup: int = 10, runs: int = 100, rounds: int = 2, seed: int = 0) -> dict:
     """The reference's timing method (scripts/benchmark.py:221-230, docs/benchmarks.md:12-16): every call
     once per round in a seeded shuffled order, ``warmup`` untimed rounds, then ``runs`` timed rounds;
@@ -145,11 +162,12 @@ def timed(call, warmup: int, runs: int) -> dict:
 
 
 def read_traffic(path: Path = TRAFFIC_FILE, key: str = "traffic_bytes_per_launch"):
-    """HBM bytes per launch (per step for C5 decode) from a committed rocprofv3 counter summary, or None."""
+    """HBM bytes per launch (per step for C5 decode, per execution of a plan elsewhere) from a committed
+    rocprofv3 counter summary (the line ``<key> <bytes>``), or None."""
     if not path.exists():
         return None
     for line in path.read_text().splitlines():
-        if line.startswith(key):
+        if line.startswith(key + " ") and line[len(key) + 1 :].strip().replace(".", "", 1).isdigit():
             return int(float(line.split()[-1]))
     return None
 
@@ -248,34 +266,46 @@ ROW_CASES = [
 ]
 
 
+def row_case_module(kind: str, rows: int, width: int):
+    import torch
+
+    from chroma_amd.models.blocks import RowLogSumExp, RowNorm, RowSoftmax
+
+    x = torch.randn(rows, width, generator=torch.Generator().manual_seed(0))
+    module = RowNorm(width) if kind == "rmsnorm" else RowSoftmax() if kind == "softmax" else RowLogSumExp()
+    return module, x
+
+
 def bench_rows(work: Path, cpu: bool) -> list:
-    """Row reductions in fp32, x ~ N(0, 1) seed 0, inputs resident: device time per execution and GB/s on
-    the algorithmic bytes (read + write of R x D for RMSNorm and softmax, read + R floats for log-sum-exp),
-    checked against the oracle on the first rows; the oracle's time on a sample of at most 64 rows."""
+    """Row reductions in fp32, x ~ N(0, 1) seed 0, inputs resident: time per execution (``chained_ms``) and
+    GB/s on the algorithmic bytes (read + write of R x D for RMSNorm and softmax, read + R floats for
+    log-sum-exp), ``traffic`` from the committed counter summary, checked against the oracle on the first
+    rows; the oracle's time on a sample of at most 64 rows."""
+    import shutil
+
     import numpy as np
     import torch
 
     import chroma_amd
-    from chroma_amd.models.blocks import RowLogSumExp, RowNorm, RowSoftmax
     from oracle import compile_cpu
 
-    import shutil
-
-    modules = {"rmsnorm": RowNorm, "softmax": RowSoftmax, "logsumexp": RowLogSumExp}
     results = []
     for kind, rows, width in ROW_CASES:
-        x = torch.randn(rows, width, generator=torch.Generator().manual_seed(0))
-        module = modules[kind](width) if kind == "rmsnorm" else modules[kind]()
+        module, x = row_case_module(kind, rows, width)
         moved = rows * width * 4 + (rows * 4 if kind == "logsumexp" else rows * width * 4)
         with chroma_amd.compile(torch.export.export(module, (x,)), work / f"{kind}_{rows}_{width}") as program:
             program.native.upload([x.numpy()])
-            ms = device_ms(program, 20 if rows * width < (1 << 26) else 10)
+            small = rows * width < (1 << 26)
+            ms = chained_ms(program, 20 if small else 5, 10 if small else 3)
+            replay = device_ms(program, 20 if small else 5)
             got = program(x.numpy())
             launches = program.stats["launches"]
         sample = min(rows, 64)
         head = x[:sample].contiguous()
+        case = f"{kind} [{rows},{width}]"
         entry = {"kind": kind, "shape": [rows, width], "dtype": "f32", "launches": launches, "ms": round(ms, 4),
-                 "algorithmic_bytes": moved, "roofline": roofline(moved, ms)}
+                 "replay_ms": round(replay, 4), "algorithmic_bytes": moved,
+                 "roofline": roofline(moved, ms, traffic=read_traffic(ROWS_TRAFFIC_FILE, f"traffic_bytes_per_execution {case}"))}
         if cpu:
             oracle = compile_cpu(torch.export.export(module, (head,)), work / f"{kind}_{rows}_{width}_cpu")
             want = oracle(head.numpy())
@@ -305,10 +335,12 @@ def bench_c1(work: Path, cpu: bool) -> dict:
     array = x.numpy()
     got = program(array)
     program.native.upload([array])
-    ms = device_ms(program, 50)
+    ms = chained_ms(program, 20, 10)
     result = {"workload": "MLP block x[8,1024] fp32 seed 0: RMSNorm, SiLU(gate)*up (1024->4096), down (4096->1024), residual; weights N(0,0.02) seed 0",
-              "device_ms": round(ms, 4), "launches": program.stats["launches"], "algorithmic_bytes": C1_BYTES, "flops": C1_FLOPS,
-              "roofline": roofline(C1_BYTES, ms), "host_to_host": timed(lambda: program(array), 10, 100)}
+              "device_ms": round(ms, 4), "replay_ms": round(device_ms(program, 50), 4), "launches": program.stats["launches"],
+              "algorithmic_bytes": C1_BYTES, "flops": C1_FLOPS,
+              "roofline": roofline(C1_BYTES, ms, traffic=read_traffic(SMALL_TRAFFIC_FILE, "traffic_bytes_per_execution c1")),
+              "host_to_host": timed(lambda: program(array), 10, 100)}
     if cpu:
         oracle = compile_cpu(exported, work / "c1_cpu")
         np.testing.assert_allclose(got, oracle(array), rtol=1e-4, atol=1e-5)
@@ -352,7 +384,7 @@ def bench_dev(work: Path, cpu: bool) -> dict:
     program.native.upload([array])
     ms = device_ms(program, 100, warmup=5)
     result["hip_device_ms"] = round(ms, 4)
-    result["roofline"] = roofline(C3_BYTES, ms)
+    result["roofline"] = roofline(C3_BYTES, ms, traffic=read_traffic(SMALL_TRAFFIC_FILE, "traffic_bytes_per_execution dev"))
     result["algorithmic_bytes"] = C3_BYTES
     program.close()
     if oracle is not None:
@@ -420,7 +452,7 @@ def bench_decode(work: Path, steps: int, cpu: bool) -> dict:
             # device-only decode step: the decode plan on what its staging holds after the last step
             ms = device_ms(programs["decode"], 100, warmup=5)
             entry["decode_step_device_ms"] = round(ms, 4)
-            entry["roofline"] = roofline(C4_BYTES, ms)
+            entry["roofline"] = roofline(C4_BYTES, ms, traffic=read_traffic(SMALL_TRAFFIC_FILE, "traffic_bytes_per_execution decode"))
             entry["algorithmic_bytes_per_step"] = C4_BYTES
         decoder.close()
         results[name] = entry
@@ -632,30 +664,93 @@ def c5_slice(work: Path) -> dict:
 
 # --------------------------------------------------------------------------------------------- counters
 def counters(work: Path, which: str) -> None:
-    """For rocprofv3 --pmc. ``c2``: three launches of the C2 kernel. ``c5``: three replays of the C5 decode plan
-    with all 4096 cache positions valid (two 2048-token prefills fill the cache first); its dispatches are the
-    3 x launches that precede the copy's. Both end with three launches of a plain copy kernel of known size
-    (``x * 1.0`` over a [16384, 8192] fp32 input: 512 MiB read, 512 MiB written), which calibrates FETCH_SIZE /
-    WRITE_SIZE on the same GPU."""
+    """For rocprofv3 --pmc: the named plan replayed three times, then three launches of a plain copy kernel of
+    known size (``x * 1.0`` over a [16384, 8192] fp32 input: 512 MiB read, 512 MiB written), which calibrates
+    FETCH_SIZE / WRITE_SIZE on the same GPU. ``c2``: the C2 kernel. ``c5``: the C5 decode plan with all 4096
+    cache positions valid (two 2048-token prefills fill the cache first). ``c5prefill``: the C5 2048-token
+    prefill plan (for the matrix-core counters). ``rows``: every row-reduction case of the rows leg in turn.
+    ``c1``, ``dev``, ``decode``: the C1 block, the C3 forward and the C4 decode step (after an 8-token prefill
+    and one step). Each plan's kernel names are logged, in launch order, before it runs."""
     import torch
 
     import chroma_amd
     from chroma_amd.models.blocks import BandwidthGraph, Copy, bandwidth_inputs
 
+    def replay(program, directory: Path, label: str) -> None:
+        log(f"{label}: {program.stats['launches']} launch(es) x3: {' '.join(plan_kernels(directory))}")
+        program.native.execute(3)
+
     x, y = bandwidth_inputs()
     if which == "c2":
         program = chroma_amd.compile(torch.export.export(BandwidthGraph(), (x, y)), work / "c2")
         program.native.upload([x.numpy(), y.numpy()])
-        program.native.execute(3)
-        log(f"ran {program.stats['launches']} launch(es) x3")
+        replay(program, work / "c2", "c2")
         program.close()
-    else:
+    elif which == "c5":
         c5_decode_counters(work)
+    elif which == "c5prefill":
+        c5_prefill_counters(work)
+    elif which == "rows":
+        for kind, rows, width in ROW_CASES:
+            module, data = row_case_module(kind, rows, width)
+            directory = work / f"{kind}_{rows}_{width}"
+            with chroma_amd.compile(torch.export.export(module, (data,)), directory) as program:
+                program.native.upload([data.numpy()])
+                replay(program, directory, f"{kind} [{rows},{width}]")
+    elif which == "c1":
+        from chroma_amd.models.blocks import mlp_block, mlp_inputs
+
+        module, (data,) = mlp_block(), mlp_inputs()
+        with chroma_amd.compile(torch.export.export(module, (data,)), work / "c1") as program:
+            program.native.upload([data.numpy()])
+            replay(program, work / "c1", "c1")
+    elif which == "dev":
+        from chroma_amd.models.dev import make_dev_model
+
+        tokens = torch.randint(0, VOCAB, (8,), generator=torch.Generator().manual_seed(0))
+        with chroma_amd.compile(torch.export.export(make_dev_model(0), (tokens,)), work / "dev") as program:
+            program.native.upload([tokens.numpy()])
+            replay(program, work / "dev", "dev")
+    elif which == "decode":
+        from chroma_amd import Decoder
+        from chroma_amd.models.cached import export_cached
+        from chroma_amd.models.dev import make_dev_model
+
+        model = make_dev_model(0)
+        prefill = chroma_amd.compile(export_cached(model, 256, 256), work / "prefill")
+        decode = chroma_amd.compile(export_cached(model, 256, 1), work / "decode")
+        tokens = torch.randint(0, VOCAB, (9,), generator=torch.Generator().manual_seed(0)).numpy()
+        with Decoder(prefill, decode) as decoder:
+            decoder.append(tokens[:8])
+            decoder.append(tokens[8:])
+            replay(decode, work / "decode", "decode")
     program = chroma_amd.compile(torch.export.export(Copy(), (x,)), work / "copy")
     program.native.upload([x.numpy()])
-    program.native.execute(3)
-    log(f"copy: ran {program.stats['launches']} launch(es) x3")
+    replay(program, work / "copy", "copy")
     program.close()
+
+
+def c5_prefill_counters(work: Path) -> None:
+    """The C5 2048-token prefill plan replayed three times (after one prefill through ``Decoder``)."""
+    import torch
+
+    import chroma_amd
+    from chroma_amd import Decoder
+    from chroma_amd.models.cached import export_cached
+    from chroma_amd.models.dev import make_gpt_oss_20b
+    from chroma_amd.models.variants import gpt_oss_20b
+
+    model = make_gpt_oss_20b(2, generator_device="cuda")
+    torch.cuda.empty_cache()
+    prefill = chroma_amd.compile(export_cached(model, C5_CONTEXT, C5_PREFILL), work / "c5_prefill")
+    decode = chroma_amd.compile(export_cached(model, C5_CONTEXT, 1), work / "c5_decode")
+    del model
+    tokens = torch.randint(0, VOCAB, (C5_PREFILL,), generator=torch.Generator().manual_seed(2)).numpy()
+    with Decoder(prefill, decode, sliding_window=gpt_oss_20b.sliding_window) as decoder:
+        decoder.append(tokens)
+        torch.cuda.synchronize()
+        log(f"C5 prefill: {prefill.stats['launches']} launch(es) x3: {' '.join(plan_kernels(work / 'c5_prefill'))}")
+        prefill.native.execute(3)
 
 
 def c5_decode_counters(work: Path) -> None:
@@ -713,8 +808,8 @@ def main() -> None:
     parser.add_argument("--no-extras", action="store_true", help="only the C2 headline (and its CPU baseline)")
     parser.add_argument("--no-cpu", action="store_true", help="skip every oracle (CPU) measurement")
     parser.add_argument("--no-c5", action="store_true", help="skip the GPT-OSS-20B-shaped model (about two minutes: 42 GB of weights)")
-    parser.add_argument("--counters", nargs="?", const="c2", choices=["c2", "c5"],
-                        help="only run the C2 kernel (or the C5 decode plan) and a copy kernel, for rocprofv3 --pmc")
+    parser.add_argument("--counters", nargs="?", const="c2", choices=["c2", "c5", "c5prefill", "rows", "c1", "dev", "decode"],
+                        help="only replay one plan (C2 kernel by default; c5 = the C5 decode step) and a copy kernel, for rocprofv3 --pmc")
     parser.add_argument("--only", choices=["c1", "rows", "dev", "decode", "c5"], help="measure one leg and print it")
     args = parser.parse_args()
     if args.gpus != 1:

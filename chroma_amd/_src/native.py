@@ -90,6 +90,7 @@ def library() -> ctypes.CDLL:
         lib.chroma_hip_destroy.restype = None
         lib.chroma_hip_upload.argtypes = [c.c_void_p, c.c_void_p, c.c_char_p, c.c_size_t]
         lib.chroma_hip_execute.argtypes = [c.c_void_p, c.c_int, c.POINTER(c.c_float), c.c_char_p, c.c_size_t]
+        lib.chroma_hip_execute_chained.argtypes = [c.c_void_p, c.c_int, c.c_int, c.POINTER(c.c_float), c.c_char_p, c.c_size_t]
         lib.chroma_hip_download.argtypes = [c.c_void_p, c.c_void_p, c.c_char_p, c.c_size_t]
         lib.chroma_hip_set_graph.argtypes = [c.c_void_p, c.c_int]
         lib.chroma_hip_launch_count.argtypes = [c.c_void_p]
@@ -125,6 +126,7 @@ EXPORTED = (
     "chroma_hip_destroy",
     "chroma_hip_upload",
     "chroma_hip_execute",
+    "chroma_hip_execute_chained",
     "chroma_hip_download",
     "chroma_hip_set_graph",
     "chroma_hip_launch_count",

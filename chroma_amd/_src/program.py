@@ -165,6 +165,14 @@ class NativeModel:
         native.check(status, error)
         return elapsed.value if timed else None
 
+    def execute_chained(self, copies: int, iterations: int) -> float:
+        """Milliseconds per execution of the plan, from ``iterations`` launches of one graph holding
+        ``copies`` back-to-back executions (no per-replay host launch in the figure)."""
+        error = ctypes.create_string_buffer(1024)
+        elapsed = ctypes.c_float(0.0)
+        native.check(self._lib.chroma_hip_execute_chained(self._handle, copies, iterations, ctypes.byref(elapsed), error, len(error)), error)
+        return elapsed.value / (copies * iterations)
+
     def download(self, outputs: Sequence[np.ndarray]) -> None:
         for array, spec in zip(outputs, self._outputs):
             _checked(array, spec, True)

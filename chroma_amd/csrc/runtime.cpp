@@ -22,6 +22,7 @@
 #include <sstream>
 #include <stdexcept>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 namespace {
@@ -538,6 +539,47 @@ public:
         return milliseconds;
     }
 
+    // ``copies`` back-to-back executions of the plan captured as one graph, launched ``iterations`` times
+    // between hipEvents: the per-execution time without the host's per-replay graph launch, so a plan of
+    // one short kernel is timed by its kernel and the dispatch barrier in front of it. Returns the total.
+    float execute_chained(int copies, int iterations) {
+        DeviceGuard guard(device_);
+        if (copies < 1 || iterations < 1 || plan_.launches.empty()) {
+            throw std::runtime_error("execute_chained needs a plan and positive counts");
+        }
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+        try {
+            for (int i = 0; i < copies; ++i) {
+                launch_direct();
+            }
+        } catch (...) {
+            hipStreamEndCapture(stream_, &graph);
+            if (graph) {
+                hipGraphDestroy(graph);
+            }
+            throw;
+        }
+        check(hipStreamEndCapture(stream_, &graph), "hipStreamEndCapture");
+        std::unique_ptr<std::remove_pointer_t<hipGraph_t>, hipError_t (*)(hipGraph_t)> graph_owner(graph, hipGraphDestroy);
+        check(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+        std::unique_ptr<std::remove_pointer_t<hipGraphExec_t>, hipError_t (*)(hipGraphExec_t)> exec_owner(exec, hipGraphExecDestroy);
+        check(hipGraphLaunch(exec, stream_), "hipGraphLaunch");  // warm-up
+        check(hipEventRecord(start_, stream_), "hipEventRecord");
+        for (int i = 0; i < iterations; ++i) {
+            check(hipGraphLaunch(exec, stream_), "hipGraphLaunch");
+        }
+        check(hipEventRecord(stop_, stream_), "hipEventRecord");
+        check(hipMemcpyAsync(error_host_, static_cast<char*>(base_) + plan_.error, sizeof(unsigned), hipMemcpyDeviceToHost, stream_),
+              "Read index error");
+        check(hipStreamSynchronize(stream_), "HIP execution");
+        float milliseconds = 0.0f;
+        check(hipEventElapsedTime(&milliseconds, start_, stop_), "hipEventElapsedTime");
+        raise_index_error();
+        return milliseconds;
+    }
+
 private:
     void ensure_staging() {
         for (int slot = 0; slot < 2; ++slot) {
@@ -790,6 +832,16 @@ __attribute__((visibility("default"))) int chroma_hip_execute(void* handle, int 
                                                               size_t error_size) {
     return guarded(error, error_size, [&] {
         const float elapsed = program(handle)->execute(iterations, milliseconds != nullptr);
+        if (milliseconds) {
+            *milliseconds = elapsed;
+        }
+    });
+}
+
+__attribute__((visibility("default"))) int chroma_hip_execute_chained(void* handle, int copies, int iterations, float* milliseconds,
+                                                                      char* error, size_t error_size) {
+    return guarded(error, error_size, [&] {
+        const float elapsed = program(handle)->execute_chained(copies, iterations);
         if (milliseconds) {
             *milliseconds = elapsed;
         }

@@ -63,6 +63,12 @@ int chroma_hip_upload(void* handle, const void* const* inputs, char* error, size
  * the runtime's stream around the launches. */
 int chroma_hip_execute(void* handle, int iterations, float* milliseconds, char* error, size_t error_size);
 
+/* Capture ``copies`` back-to-back executions of the plan as one graph and launch it ``iterations``
+ * times; ``milliseconds`` (if non-null) receives the total time between hipEvents around those launches
+ * (divide by copies x iterations for one execution). Times a plan of one short kernel without the host's
+ * per-replay graph launch. */
+int chroma_hip_execute_chained(void* handle, int copies, int iterations, float* milliseconds, char* error, size_t error_size);
+
 /* Copy the output staging regions to host buffers. */
 int chroma_hip_download(void* handle, void* const* outputs, char* error, size_t error_size);
 
