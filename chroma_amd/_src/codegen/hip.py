@@ -75,6 +75,12 @@ WIDE_GEMM_TILE = (256, 192)  # chroma::kWideM, kWideN
 # the wide body takes dense products with at least this many of its tiles: below that its larger tiles
 # leave too much of the chip idle and the 128 x 128 body is faster
 WIDE_GEMM_MIN_TILES = 200
+# bfloat16 expert products whose channel count is a multiple of a tile width here take the ring body on
+# 128-slot x width tiles (chroma::grouped_expert_linear PATH 3) with that many waves side by side (each
+# wave all 128 slots of a width / waves strip). Measured on the GPT-OSS-20B shapes (2048 tokens x top-4 of
+# 32): 384 on 8 waves 465 us for the 5760-channel up product, 320 on 4 waves 237-240 us for the 2880-channel
+# down product (the 128 x 128 direct-to-LDS body: 517 and 253 us)
+RING_EXPERT_TILES = ((384, 8), (320, 4))
 REUSED_EVALUATIONS = 1 << 18  # a contraction operand is stored when (elements x reuse) reaches this
 SMALL_REDUCTION = 8  # contractions summing at most this many products are fused expressions...
 SMALL_OPERAND_COST = 8  # ...over operands that cost at most this much per element (others are stored)
@@ -2515,15 +2521,20 @@ class HIPCodegen(Codegen):
         w, xs = self._matrix_slot(k, weight), self._matrix_slot(k, x)
         table = k.slot(scratch.name, torch.int64, extent=self.extents[scratch.name])
         out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
-        path, threads = 1, 256
-        if self._direct_gemm(out.dtype, inner):
+        path, threads, width, waves = 1, 256, 128, 4
+        ring = next(((n, w) for n, w in RING_EXPERT_TILES if channels % n == 0), None)
+        if out.dtype == torch.bfloat16 and inner % 32 == 0 and ring is not None:
+            path, width, waves = 3, *ring
+            threads = 64 * waves
+            k.min_waves = 1
+        elif self._direct_gemm(out.dtype, inner):
             path, threads = 2, DIRECT_GEMM_THREADS
             k.min_waves = DIRECT_GEMM_BLOCKS
         k.line(
-            f"chroma::grouped_expert_linear<{ctype_of(out.dtype)}, {str(per_slot).lower()}, {path}>({w}, {xs}, {out_slot}, "
+            f"chroma::grouped_expert_linear<{ctype_of(out.dtype)}, {str(per_slot).lower()}, {path}, {width}, 1, {waves}>({w}, {xs}, {out_slot}, "
             f"reinterpret_cast<const int32_t*>({table}), {tokens * selected}u, {selected}u, {experts}u, {channels}u, {inner}u);"
         )
-        self.launch(k, 8 * -(-(-(-channels // 128) * tiles) // 8), threads, [weight, x, scratch], kind="experts_mfma")
+        self.launch(k, 8 * -(-(-(-channels // width) * tiles) // 8), threads, [weight, x, scratch], kind="experts_mfma")
         self.mfma_matmuls += 1
 
     def _loop_einsum(self, meta, labels, output, sizes, reduction, values) -> Value:

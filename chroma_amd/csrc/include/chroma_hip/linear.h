@@ -1053,18 +1053,26 @@ __device__ __forceinline__ uint32_t wide_swizzle(uint32_t row) { return ((row >>
 // s_waitcnt immediate waiting for at most n outstanding vector-memory operations (lgkm and exp counts free)
 constexpr int16_t vmcnt_wait(uint32_t n) { return int16_t((n & 15u) | ((n >> 4) << 14) | 0x70u | 0xF00u); }
 
-template <class T>
-__device__ __forceinline__ void mfma_gemm_wide(const uint16_t* __restrict__ a, uint32_t lda, const uint16_t* __restrict__ b,
+// ``mfma_gemm_ring`` is that body for any BM x BN tile on WM x WN waves (each wave BM / WM x BN / WN, in
+// 16 x 16 MFMA tiles) with an S-slot ring (S - 2 stages in flight): the dense linears take 256 x 192 on
+// 2 x 2 waves with 5 slots (``mfma_gemm_wide``); the expert products take 128-slot x 384- or 320-channel
+// tiles on 1 x 4 waves (each wave all 128 slots of a 96- or 80-channel strip), which keeps the 128-slot
+// tiles of the ragged per-expert slot counts while reading 0.29-0.32 KB of LDS per MFMA instead of the
+// 32 x 64 wave tiles' 0.75 (the expert body was LDS-bound at about a fifth of the matrix-core peak).
+template <class T, int BM, int BN, int WM, int WN, int S>
+__device__ __forceinline__ void mfma_gemm_ring(const uint16_t* __restrict__ a, uint32_t lda, const uint16_t* __restrict__ b,
                                                uint32_t ldb, const T* __restrict__ bias, T* __restrict__ c, uint32_t ldc,
                                                uint32_t m_total, uint32_t n_total, uint32_t k_total,
                                                const int32_t* __restrict__ a_rows, const int32_t* __restrict__ c_rows, uint32_t m0,
-                                               uint32_t n0) {
-    static_assert(sizeof(T) == 2, "the wide body takes bfloat16");
-    constexpr int BM = kWideM, BN = kWideN, WM = 2, WN = 2, WAVES = WM * WN, S = 5;
+                                               uint32_t n0, uint32_t a_div = 1) {
+    static_assert(sizeof(T) == 2, "the ring body takes bfloat16");
+    static_assert(S >= 3, "the ring needs a slot being read, one landed and one being filled");
+    constexpr int WAVES = WM * WN;
     constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
     constexpr int CA = BM / 16 / WAVES, CB = BN / 16 / WAVES, PER = CA + CB;  // 1 KB copies per wave per stage
     constexpr int SLOT = (BM + BN) * 32;                                       // bf16 elements per ring slot
     static_assert(CA * 16 * WAVES == BM && CB * 16 * WAVES == BN && PER <= TM, "one copy per MFMA row");
+    static_assert(TM * WM * 16 == BM && TN * WN * 16 == BN, "whole 16 x 16 tiles per wave");
     __shared__ __attribute__((aligned(1024))) uint16_t ring[S * SLOT];
     const uint32_t lane = threadIdx.x % 64u, wave = threadIdx.x / 64u;
     const uint32_t wm = wave / WN, wn = wave % WN;
@@ -1078,7 +1086,7 @@ __device__ __forceinline__ void mfma_gemm_wide(const uint16_t* __restrict__ a, u
         const uint32_t chunk = (lane % 4u) ^ wide_swizzle(row);
         if constexpr (i < CA) {
             const uint32_t g = m0 + row < m_total ? m0 + row : m_total - 1u;
-            src[i] = a + (a_rows ? size_t(a_rows[g]) : size_t(g)) * lda + chunk * 8u;
+            src[i] = a + (a_rows ? size_t(uint32_t(a_rows[g]) / a_div) : size_t(g)) * lda + chunk * 8u;
             dst[i] = block * 512u;
         } else {
             const uint32_t g = n0 + row < n_total ? n0 + row : n_total - 1u;
@@ -1103,7 +1111,7 @@ __device__ __forceinline__ void mfma_gemm_wide(const uint16_t* __restrict__ a, u
         __builtin_amdgcn_global_load_lds((global_void*)(src[i] + k0), (lds_void*)(ring + slot * SLOT + dst[i]), 16, 0, 0);
     };
     unroll<S - 1>([&](auto st) { unroll<PER>([&](auto i) { copy(i, uint32_t(st), k_of(st)); }); });
-    __builtin_amdgcn_s_waitcnt(vmcnt_wait(3 * PER));  // stage 0 landed
+    __builtin_amdgcn_s_waitcnt(vmcnt_wait((S - 2) * PER));  // stage 0 landed
     __builtin_amdgcn_s_barrier();
     bf16x8_t fa[TM], fb[TN];
     unroll<TM>([&](auto t) { fa[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(ring + oa[t])); });
@@ -1112,7 +1120,7 @@ __device__ __forceinline__ void mfma_gemm_wide(const uint16_t* __restrict__ a, u
     unroll<TM>([&](auto i) { unroll<TN>([&](auto j) { acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}; }); });
     for (uint32_t s = 0; s + 1u < steps; ++s) {
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(vmcnt_wait(2 * PER));  // stage s+1 landed (s+2, s+3 may be in flight)
+        __builtin_amdgcn_s_waitcnt(vmcnt_wait((S - 3) * PER));  // stage s+1 landed (s+2 .. s+S-2 may be in flight)
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         const uint16_t* next = ring + ((s + 1u) % S) * SLOT;
@@ -1183,6 +1191,15 @@ __device__ __forceinline__ void mfma_gemm_wide(const uint16_t* __restrict__ a, u
             });
         }
     });
+}
+
+template <class T>
+__device__ __forceinline__ void mfma_gemm_wide(const uint16_t* __restrict__ a, uint32_t lda, const uint16_t* __restrict__ b,
+                                               uint32_t ldb, const T* __restrict__ bias, T* __restrict__ c, uint32_t ldc,
+                                               uint32_t m_total, uint32_t n_total, uint32_t k_total,
+                                               const int32_t* __restrict__ a_rows, const int32_t* __restrict__ c_rows, uint32_t m0,
+                                               uint32_t n0) {
+    mfma_gemm_ring<T, kWideM, kWideN, 2, 2, 5>(a, lda, b, ldb, bias, c, ldc, m_total, n_total, k_total, a_rows, c_rows, m0, n0);
 }
 
 template <class T, bool B_K_CONTIGUOUS>
@@ -1566,16 +1583,24 @@ __device__ __forceinline__ void expert_tile_of(const int32_t* __restrict__ count
 // selected). ``rows`` receives the A-row of each permuted slot and is filled by each workgroup before its
 // product. One-dimensional launch of 8 * ceil(ceil(C / 128) * max tiles / 8) workgroups, mapped to tiles
 // in the expert-major, XCD-aware order above; workgroups past gx * (tile count) return at once.
-template <class T, bool PER_SLOT, int PATH = 0>
+// PATH 3 is the ring body on 128-slot x BN-channel tiles on RWM x RWN waves (64 RWM RWN threads; bfloat16,
+// K % 32 = 0, ``channels`` a multiple of BN); the other paths take 128 x 128 tiles.
+
+template <int BN>
+constexpr int ring_expert_slots() {
+    return (128 + BN) * 64 * 5 <= 150 * 1024 ? 5 : 4;
+}
+
+template <class T, bool PER_SLOT, int PATH = 0, int BN = 128, int RWM = 1, int RWN = 4, int RS = ring_expert_slots<BN>()>
 __device__ __forceinline__ void grouped_expert_linear(const T* __restrict__ w, const T* __restrict__ x, T* __restrict__ out,
                                                       const int32_t* __restrict__ scratch, uint32_t slots, uint32_t selected,
                                                       uint32_t experts, uint32_t channels, uint32_t inner) {
-    __shared__ int32_t a_rows[128], c_rows[128];
+    static_assert(PATH == 3 || BN == 128, "only the ring path takes wider channel tiles");
     const int32_t* offsets = scratch + experts;
     const uint32_t tile_count = uint32_t(scratch[2 * experts + 1]);
     const int32_t* permutation = scratch + 2 * experts + 2;
     const int32_t* tiles = permutation + slots;
-    const uint32_t gx = (channels + 127u) / 128u;
+    const uint32_t gx = (channels + BN - 1u) / BN;
     uint32_t logical;
     if (!xcd_logical_tile(gx * tile_count, logical)) {
         return;
@@ -1586,14 +1611,27 @@ __device__ __forceinline__ void grouped_expert_linear(const T* __restrict__ w, c
     const uint32_t first = uint32_t(tiles[2 * tile + 1]);
     const uint32_t count = uint32_t(offsets[expert + 1] - offsets[expert]);
     const uint32_t rows = count - first < 128u ? count - first : 128u;
-    for (uint32_t r = threadIdx.x; r < 128u; r += blockDim.x) {
-        const int32_t slot = r < rows ? permutation[offsets[expert] + first + r] : 0;
-        a_rows[r] = PER_SLOT ? slot : slot / int32_t(selected);
-        c_rows[r] = slot;
+    if constexpr (PATH == 3) {
+        // the tile's slots are read straight from the permutation in global memory (the A row of a slot is
+        // slot / selected for per-token inputs): the ring is then the kernel's only LDS array, and the
+        // compiler can tell its fragment reads from the copies in flight (with other LDS arrays in the kernel
+        // it made every fragment read wait for all outstanding copies, which serialised the pipeline)
+        static_assert(sizeof(T) == 2, "the ring body takes bfloat16");
+        const int32_t* slots_of_tile = permutation + offsets[expert] + first;
+        mfma_gemm_ring<T, 128, BN, RWM, RWN, RS>(
+            x, inner, w + size_t(expert) * channels * inner, inner, nullptr, out, channels, rows, channels, inner, slots_of_tile,
+            slots_of_tile, 0u, column * BN, PER_SLOT ? 1u : selected);
+    } else {
+        __shared__ int32_t a_rows[128], c_rows[128];
+        for (uint32_t r = threadIdx.x; r < 128u; r += blockDim.x) {
+            const int32_t slot = r < rows ? permutation[offsets[expert] + first + r] : 0;
+            a_rows[r] = PER_SLOT ? slot : slot / int32_t(selected);
+            c_rows[r] = slot;
+        }
+        __syncthreads();
+        mfma_gemm<T, true, PATH>(x, inner, w + size_t(expert) * channels * inner, inner, nullptr, out, channels, rows, channels, inner,
+                                 a_rows, c_rows, 0u, column * 128u);
     }
-    __syncthreads();
-    mfma_gemm<T, true, PATH>(x, inner, w + size_t(expert) * channels * inner, inner, nullptr, out, channels, rows, channels, inner,
-                             a_rows, c_rows, 0u, column * 128u);
 }
 
 }  // namespace chroma

@@ -339,6 +339,34 @@ def test_grouped_expert_products(tmp_path, dtype, experts):
         compare(model(*inputs), oracle(*[numpy_of(v) for v in inputs]))
 
 
+@pytest.mark.parametrize("channels, inner", [(768, 96), (640, 320), (384, 64)])
+def test_grouped_expert_products_ring_body(tmp_path, channels, inner):
+    """bfloat16 expert products whose channel count is a multiple of 384 or 320 take the ring body on
+    128-slot tiles: 6 experts with ~133 slots each (a full and a ragged tile per expert), two channel
+    tiles, K of 2-10 32-deep stages (fewer than the ring's slots included); per-token and per-slot inputs,
+    against the oracle."""
+
+    class Experts(torch.nn.Module):
+        def forward(self, weights, indices, x, per_slot):
+            selected = weights[indices]
+            return torch.einsum("beck,bk->bec", selected, x), torch.einsum("beck,bek->bec", selected, per_slot)
+
+    generator = torch.Generator().manual_seed(4)
+    experts, tokens, selected = 6, 200, 4
+    weights = (torch.randn(experts, channels, inner, generator=generator) * 0.2).to(torch.bfloat16)
+    indices = torch.stack([torch.randperm(experts, generator=generator)[:selected] for _ in range(tokens)])
+    x = torch.randn(tokens, inner, generator=generator).to(torch.bfloat16)
+    per_slot = torch.randn(tokens, selected, inner, generator=generator).to(torch.bfloat16)
+    inputs = (weights, indices, x, per_slot)
+    exported = torch.export.export(Experts(), inputs)
+    oracle = compile_cpu(exported, tmp_path / "cpu")
+    with chroma_amd.compile(exported, tmp_path / "hip") as model:
+        assert model.stats["expert_contractions"] == 2 and model.stats["mfma_matmuls"] == 2
+        source = (tmp_path / "hip" / "model.hip").read_text()
+        assert source.count(", 3, 384, 1, 8>(") + source.count(", 3, 320, 1, 4>(") == 2, "the ring path was not taken"
+        compare(model(*inputs), oracle(*[numpy_of(v) for v in inputs]))
+
+
 def test_aliases_and_live_workspace_across_linear_layers(tmp_path):
     def fn(x, w):
         first = torch.nn.functional.linear(x, w)
