@@ -903,8 +903,12 @@ __device__ __forceinline__ void mfma_gemm_direct(const uint16_t* __restrict__ a,
     constexpr int WM = 4, WN = 2, WAVES = WM * WN, BM = 128, BN = 128;
     constexpr int TM = BM / WM / 16, TN = BN / WN / 16;  // 16 x 16 tiles per wave: 2 x 4
     constexpr int BLOCKS = BM / 8 / WAVES;                // 8-row (1 KB) blocks each wave copies per operand per slice
-    __shared__ __attribute__((aligned(16))) uint16_t as[2][BM * 64];
-    __shared__ __attribute__((aligned(16))) uint16_t bs[2][BN * 64];
+    // One LDS array for both operands and both buffers: with two arrays the compiler could not tell the
+    // fragment reads from the copies in flight and made every read wait for all of them (vmcnt(0)), so the
+    // next slice's copies never overlapped the current slice's MFMAs.
+    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * (BM + BN) * 64];
+    auto as = [&](int buffer) { return lds + buffer * (BM + BN) * 64; };
+    auto bs = [&](int buffer) { return lds + buffer * (BM + BN) * 64 + BM * 64; };
     const uint32_t tid = threadIdx.x, lane = tid % 64u, wave = tid / 64u;
     const uint32_t wm = wave / WN, wn = wave % WN;
     if (m0 >= m_total) {
@@ -924,19 +928,19 @@ __device__ __forceinline__ void mfma_gemm_direct(const uint16_t* __restrict__ a,
     auto copy = [&](int buffer, uint32_t k0) {
 #pragma unroll
         for (int i = 0; i < BLOCKS; ++i) {
-            __builtin_amdgcn_global_load_lds((global_void*)(ga[i] + k0), (lds_void*)&as[buffer][(i * WAVES + wave) * 512u], 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((global_void*)(gb[i] + k0), (lds_void*)&bs[buffer][(i * WAVES + wave) * 512u], 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((global_void*)(ga[i] + k0), (lds_void*)(as(buffer) + (i * WAVES + wave) * 512u), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((global_void*)(gb[i] + k0), (lds_void*)(bs(buffer) + (i * WAVES + wave) * 512u), 16, 0, 0);
         }
     };
     auto fragments = [&](int buffer, int half, bf16x8_t (&fa)[TM], bf16x8_t (&fb)[TN]) {
         const uint32_t chunk = half * 4u + lane / 16u;
 #pragma unroll
         for (int t = 0; t < TM; ++t) {
-            fa[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(&as[buffer][deep_lds(wm * (BM / WM) + t * 16u + lane % 16u, chunk)]));
+            fa[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(as(buffer) + (deep_lds(wm * (BM / WM) + t * 16u + lane % 16u, chunk))));
         }
 #pragma unroll
         for (int t = 0; t < TN; ++t) {
-            fb[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(&bs[buffer][deep_lds(wn * (BN / WN) + t * 16u + lane % 16u, chunk)]));
+            fb[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(bs(buffer) + (deep_lds(wn * (BN / WN) + t * 16u + lane % 16u, chunk))));
         }
     };
     f32x4_t acc[TM][TN];
