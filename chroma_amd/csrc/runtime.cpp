@@ -640,7 +640,10 @@ private:
     void raise_index_error() {
         if (*error_host_) {
             *error_host_ = 0;
-            check(hipMemsetAsync(static_cast<char*>(base_) + plan_.error, 0, sizeof(unsigned), stream_), "Clear index error");
+            // the whole error region: the index word and the in-kernel handoff tickets (words 16-255), which
+            // every launch returns to zero itself; clearing them here too (outside any captured graph, after
+            // the stream has drained) leaves nothing for a later launch to inherit
+            check(hipMemsetAsync(static_cast<char*>(base_) + plan_.error, 0, kErrorRegion, stream_), "Clear index error");
             check(hipStreamSynchronize(stream_), "Clear index error");
             throw IndexError("Tensor index out of range");
         }

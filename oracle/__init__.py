@@ -4,7 +4,11 @@ CPU restatement of Chroma's CPU backend, used as the parity oracle for the ``hip
 CPU baseline in ``bench.py``. Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline
 leg may import it; the ``chroma_amd`` package never does.
 
-Parity status of each part (how it is pinned) is listed in ``oracle/PINNING.md``.
+How each part is pinned: the kernel headers by compiling the same generated program against the
+reference's own headers (oracle/ref, bit-identical results); the front end by the reference's published
+graph statistics; the numerics against eager torch at the reference's tolerances, its bf16 known answers
+and float64 closed forms; the routing checker (routing.py) against hand-built decisions with planted
+mistakes. The tests under tests/ hold each check.
 """
 
 from __future__ import annotations

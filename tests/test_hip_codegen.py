@@ -341,3 +341,28 @@ def test_dev_model_arena_lifetimes_cover_every_launch():
         for b in live[i + 1 :]:
             if a.start <= b.end and b.start <= a.end:
                 assert a.offset + a.size <= b.offset or b.offset + b.size <= a.offset
+
+
+def _function_text(source: str, marker: str) -> str:
+    """The text of the device function that contains ``marker`` (from its signature to its closing brace)."""
+    at = source.index(marker)
+    start = source.rindex("__device__ __forceinline__ void", 0, at)
+    end = source.index("\n}\n", at)
+    return source[start:end]
+
+
+def test_in_kernel_handoffs_use_device_scope_accesses():
+    """The two kernels that pass data between workgroups inside one launch (the split router's logits and
+    the decode attention's phase-2 partial sums, each handed over behind a ticket) touch that data only
+    through ``store_device`` / ``load_device`` (device-scope atomics, which the compiler keeps as such and
+    the hardware writes through / reads past the XCD's L2), and each returns its ticket word to zero."""
+    include = ROOT / "chroma_amd" / "csrc" / "include" / "chroma_hip"
+    router = _function_text((include / "linear.h").read_text(), "void router_split(")
+    uses = [line.strip() for line in router.splitlines() if "row_logits" in line and "T* row_logits =" not in line]
+    assert uses and all("store_device(row_logits" in line or "load_device(row_logits" in line for line in uses), uses
+    assert "atomicExch(counter + row, 0u)" in router and "device_stores_complete();" in router
+    decode = _function_text((include / "attention.h").read_text(), "auto finish = [&]()")
+    uses = [line.strip() for line in decode.splitlines() if "partial" in line and not line.strip().startswith("//")
+            and "float* partial = split.partial" not in line]
+    assert uses and all("store_device(" in line or "load_device(" in line for line in uses), uses
+    assert "atomicExch(ticket_word, 0u)" in decode and "device_stores_complete();" in decode
