@@ -56,6 +56,8 @@ ROW_UNROLL = 4  # vector loads per thread in flight in the one-pass row statisti
 WIDE_ROW_THREADS = 1024
 SPLIT_ROW_LIMIT = 256  # rows of a reduction below this count are split over workgroups when wide
 SPLIT_ROW_BLOCKS = 1024  # workgroups a split row reduction aims for
+COOP_THREADS = 1024  # threads of a cooperative row kernel's workgroup (one workgroup per compute unit)
+COOP_GROUPS = 64  # rows in flight at most (chroma::kCoopGroups counter words)
 STREAMING_STORES = True
 STREAMING_BYTES = 64 << 20  # smaller operands and results may stay in L2 / the last-level cache
 FUSED_CONCAT_ELEMENTS = 1 << 16  # smaller concatenations are fused into their consumers
@@ -720,7 +722,10 @@ class HIPCodegen(Codegen):
         rows = outer * inner
         if inner == 1 and width >= 64:
             splits, chunk, lanes = self._row_splits(rows, width, x.dtype)
-            if splits > 1 and not self._row_plan(width, x.dtype, softmax=True)[3]:
+            coop = self._coop_plan(rows, width, x.dtype, "softmax")
+            if coop is not None and not self._row_plan(width, x.dtype, softmax=True)[3]:
+                self._coop_rows("softmax", out, x, shape, dim, width, rows, coop)
+            elif splits > 1 and not self._row_plan(width, x.dtype, softmax=True)[3]:
                 self._split_softmax(out, x, shape, dim, width, rows, splits, chunk, lanes)
             else:
                 self._row_softmax(out, x, shape, dim, width, rows)
@@ -879,6 +884,162 @@ class HIPCodegen(Codegen):
     # ``total`` of exp(x - peak) over the elements it read (rescaled when the maximum grows) and a NaN
     # flag; the workgroup then combines its threads'. Rows too few to fill the chip are split over
     # workgroups (``_row_partials``), whose (peak, total) pairs a later launch combines in the same way.
+
+    @staticmethod
+    def _coop_plan(rows: int, width: int, dtype: torch.dtype, kind: str) -> Optional[Tuple[int, int, int]]:
+        """(parts per row, vectors per thread, lanes) of a cooperative row kernel, or None: rows too wide for
+        one workgroup's registers and many enough to fill the chip (``SPLIT_ROW_LIMIT``); each of ``parts``
+        workgroups of ``COOP_THREADS`` holds ``vectors`` vectors of ``lanes`` per thread (at most 6: three
+        rows in registers at once, and for an RMSNorm its slice of the weight), the parts covering the row
+        with at most 1/16 of it as padding."""
+        if dtype not in (torch.float32, torch.bfloat16) or rows < SPLIT_ROW_LIMIT:
+            return None
+        lanes = choose_lanes(width, dtype)
+        if width % lanes:
+            return None
+        step = COOP_THREADS * lanes
+        most = 6
+        best = None
+        for parts in range(2, 17):
+            vectors = -(-width // (parts * step))
+            if vectors > most or (parts - 1) * vectors * step >= width:
+                continue
+            waste = parts * vectors * step - width
+            if waste * 16 <= width and (best is None or waste < best[0]):
+                best = (waste, parts, vectors)
+        return None if best is None else (best[1], best[2], lanes)
+
+    def _coop_rows(self, kind: str, out: Value, x: Value, shape, dim: int, width: int, rows: int, plan: Tuple[int, int, int],
+                   weight: Optional[Value] = None, epsilon: float = 0.0) -> None:
+        """One HBM pass of a wide row softmax (gpu.py:275-298) or RMSNorm (gpu.py:339-358) over many rows: a
+        persistent grid of ``parts`` x groups co-resident workgroups (one per compute unit), group g taking
+        rows g, g + groups, ...; each part keeps its slice of a row in registers and publishes its partial
+        statistics (softmax: the slice's maximum, NaN if it holds a NaN, and sum of exp(x - max); RMSNorm:
+        its sum of squares) with ``chroma::coop_publish``; one row later (so the exchange overlaps a row of
+        work) it collects the other parts' statistics of that row (``coop_peek``, ``coop_wait``), requests
+        its slice of the row after next, combines the statistics in part order and writes its slice: exp(x - max)
+        times the reciprocal of the sum (NaN for a row holding a NaN, a +inf or only -inf, as in
+        ``_split_softmax``), or x * (1 / sqrt(sum / D + eps)) * w."""
+        parts, vectors, lanes = plan
+        threads = COOP_THREADS
+        step = threads * lanes
+        span = vectors * step
+        groups = max(1, min(MFMA_CUS // parts, rows, COOP_GROUPS))
+        floats = 2 if kind == "softmax" else 1
+        words = 4 * parts * floats  # 64-bit words per group: four slot sets of each part's floats
+        slots = self.allocate((groups * words * 2,), torch.float32)
+        neg_inf = float_literal(-math.inf)
+        k = Kernel(lanes)
+        k.streaming = STREAMING_STORES and math.prod(shape) * ITEMSIZE[out.dtype] >= STREAMING_BYTES
+        k.uses_error = True
+        k.min_waves = 1
+        slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        slot_buffer = k.slot(slots.name, torch.float32, writable=True, extent=self.extents[slots.name])
+        waves = threads // 64
+        k.line(f"const uint32_t group = blockIdx.x / {parts}u, part = blockIdx.x % {parts}u;")
+        k.line(f"const uint32_t begin = part * {span}u + threadIdx.x * {lanes}u;")
+        k.line(f"unsigned long long* const slots = reinterpret_cast<unsigned long long*>({slot_buffer}) + group * {words}u;")
+        k.line(f"float cur[{vectors}][{lanes}], nxt[{vectors}][{lanes}], ahead[{vectors}][{lanes}];")
+
+        def element_index(v: str) -> str:
+            return f"begin + {v} * {step}u"
+
+        def load(row_code: str, array: str) -> None:
+            """``array`` <- the part's slice of row ``row_code`` (padding past the row's end)."""
+            with k.block("{"):
+                row = Aff.of(k.atom(row_code, rows - 1, prefix="r"))
+                k.line("#pragma unroll")
+                with k.block(f"for (uint32_t v = 0; v < {vectors}u; ++v) {{"):
+                    k.line(f"const uint32_t at = {element_index('v')};")
+                    j = Aff.of(k.vector_atom(f"at < {width}u ? at : {width - lanes}u", width - 1))
+                    names = k.emit(self.read(k, x, self._row_coords(k, row, shape, dim, j)))
+                    names = names if isinstance(names, list) else [names] * lanes
+                    for lane, name in enumerate(names):
+                        k.line(f"{array}[v][{lane}] = {name};")  # past the row's end: a copy of its last vector
+
+        def over_slice(statement: str) -> None:
+            """``statement`` for every element of the slice; ``live`` says whether it lies inside the row
+            (the loads are unconditional, so the padding is applied where the values are used)."""
+            k.line("#pragma unroll")
+            k.line(f"for (uint32_t v = 0; v < {vectors}u; ++v) {{")
+            k.line(f"    const bool live = {element_index('v')} < {width}u;")
+            k.line("    #pragma unroll")
+            k.line(f"    for (uint32_t l = 0; l < {lanes}u; ++l) {{ {statement} }}")
+            k.line("}")
+
+        if kind == "rmsnorm":
+            k.line(f"float wv[{vectors}][{lanes}];")
+            k.line("#pragma unroll")
+            with k.block(f"for (uint32_t v = 0; v < {vectors}u; ++v) {{"):
+                k.line(f"const uint32_t at = {element_index('v')};")
+                j = Aff.of(k.vector_atom(f"at < {width}u ? at : {width - lanes}u", width - 1))
+                names = k.emit(self.read(k, weight, [j]))
+                names = names if isinstance(names, list) else [names] * lanes
+                for lane, name in enumerate(names):
+                    k.line(f"wv[v][{lane}] = {name};")
+        # rows of this group: group, group + groups, ...; round r publishes row r's statistics (``nxt``),
+        # collects round r - 1's, requests row r + 1 (``ahead``) and writes row r - 1 (``cur``): each
+        # exchange overlaps a row of work, and the next row's loads overlap the writing
+        k.line(f"const uint32_t count = ({rows}u - group + {groups - 1}u) / {groups}u;")
+        load("group", "nxt")
+        k.line("bool ok = true;")
+        with k.block("for (uint32_t round = 0; round <= count && ok; ++round) {"):
+            with k.block("if (round < count) {"):
+                if kind == "softmax":
+                    k.line(f"float peak = {neg_inf};")
+                    k.line("bool bad = false;")
+                    over_slice(f"peak = __builtin_fmaxf(peak, live ? nxt[v][l] : {neg_inf}); bad = bad | (live && __builtin_isnan(nxt[v][l]));")
+                    k.line(f"peak = chroma::block_max<{waves}>(peak, scratch);")
+                    k.line("float total = 0.0f;")
+                    with k.block(f"if (peak != {neg_inf}) {{"):
+                        over_slice("total += live ? chroma::fast_exp(nxt[v][l] - peak) : 0.0f;")
+                    k.line(f"total = chroma::block_sum<{waves}>(total, scratch);")
+                    k.line(f"const bool flagged = chroma::block_max<{waves}>(bad ? 1.0f : 0.0f, scratch) != 0.0f;")
+                    k.line('const float mine[2] = {flagged ? __builtin_nanf("") : peak, total};')
+                else:
+                    k.line("float squares = 0.0f;")
+                    over_slice("squares += live ? nxt[v][l] * nxt[v][l] : 0.0f;")
+                    k.line(f"const float mine[1] = {{chroma::block_sum<{waves}>(squares, scratch)}};")
+                k.line(f"chroma::coop_publish<{parts}, {floats}>(slots, part, round, mine);")
+            # round r - 1 was published a row ago: its words are normally there at the first look, so only
+            # the peek's round trip is exposed; the next row's loads are requested after the check (a check
+            # after them would wait for them too) and overlap the writing of row r - 1
+            k.line(f"float all[{parts}][{floats}];")
+            with k.block("if (round > 0) {"):
+                k.line(f"const unsigned long long word = chroma::coop_peek<{parts}, {floats}>(slots, round - 1u);")
+                k.line(f"ok = chroma::coop_wait<{parts}, {floats}>(slots, round - 1u, word, all, error);")
+            with k.block("if (round + 1u < count) {"):
+                load(f"group + (round + 1u) * {groups}u", "ahead")
+            with k.block("if (round > 0) {"):
+                if kind == "softmax":
+                    k.line(f"float row_peak = {neg_inf}, row_total = 0.0f;")
+                    k.line("bool row_bad = false;")
+                    k.line("#pragma unroll")
+                    k.line(f"for (uint32_t q = 0; q < {parts}u; ++q) {{ row_peak = __builtin_fmaxf(row_peak, all[q][0]); row_bad = row_bad | __builtin_isnan(all[q][0]); }}")
+                    k.line("#pragma unroll")
+                    k.line(f"for (uint32_t q = 0; q < {parts}u; ++q) row_total += all[q][0] == {neg_inf} || __builtin_isnan(all[q][0]) ? 0.0f : "
+                           "all[q][1] * chroma::fast_exp(all[q][0] - row_peak);")
+                    k.line('const float inverse = row_bad || __builtin_isinf(row_peak) ? __builtin_nanf("") : 1.0f / row_total;')
+                else:
+                    k.line("float row_squares = 0.0f;")
+                    k.line("#pragma unroll")
+                    k.line(f"for (uint32_t q = 0; q < {parts}u; ++q) row_squares += all[q][0];")
+                    k.line(f"const float scale = 1.0f / sqrtf(row_squares / {float_literal(width)} + {float_literal(epsilon)});")
+                row = Aff.of(k.atom(f"group + (round - 1u) * {groups}u", rows - 1, prefix="r"))
+                k.line("#pragma unroll")
+                with k.block(f"for (uint32_t v = 0; v < {vectors}u; ++v) {{"):
+                    k.line(f"const uint32_t at = {element_index('v')};")
+                    with k.block(f"if (at < {width}u) {{"):
+                        j = Aff.of(k.vector_atom("at", width - 1))
+                        if kind == "softmax":
+                            codes = [f"chroma::fast_exp(cur[v][{lane}] - row_peak) * inverse" for lane in range(lanes)]
+                        else:
+                            codes = [f"cur[v][{lane}] * scale * wv[v][{lane}]" for lane in range(lanes)]
+                        k.store(slot, out.dtype, Kernel.flatten(self._row_coords(k, row, shape, dim, j), shape), self._lane_values(k, codes))
+            over_slice("cur[v][l] = nxt[v][l]; nxt[v][l] = ahead[v][l];")
+        k.line(f"chroma::coop_depart<{parts}, {floats}>(slots, error + chroma::kCoopDepartWord + group);")
+        inputs = [x] + ([weight] if weight is not None else [])
+        self.launch(k, parts * groups, threads, inputs, kind=f"coop_{kind}", prologue=[f"__shared__ float scratch[{waves}];"])
 
     @staticmethod
     def _row_splits(rows: int, width: int, dtype: torch.dtype) -> Tuple[int, int, int]:
@@ -1296,6 +1457,11 @@ class HIPCodegen(Codegen):
         dim = len(shape) - 1
         threads, lanes, chunks, resident = self._row_plan(columns, x.dtype)
         splits, chunk, split_lanes = self._row_splits(rows, columns, x.dtype)
+        coop = self._coop_plan(rows, columns, x.dtype, "rmsnorm")
+        if coop is not None and not resident:
+            self._coop_rows("rmsnorm", out, x, shape, dim, columns, rows, coop, weight=weight, epsilon=epsilon)
+            self.parallel_reductions += 1
+            return out
         if splits > 1 and not resident:
             self._split_norm(out, x, weight, epsilon, shape, rows, columns, splits, chunk, split_lanes)
             self.parallel_reductions += 1

@@ -98,6 +98,114 @@ template <class T> __device__ __forceinline__ T load_device(const T* p) {
 __device__ __forceinline__ void device_stores_complete() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ---------------------------------------------------------------------------------------------
+// Cooperative row kernels (chroma_coop_*): P workgroups share each row of a wide row reduction, each
+// keeping its part of the row in registers between the row's statistics and its normalisation, so the row
+// is read from HBM once. Per row ("round") every part publishes N floats (its partial statistics) as 64-bit
+// words, the float's bits and the round's tag (round + 1) side by side, each written by one device-scope
+// atomic store, so a reader that sees the tag sees the float with it. The kernels publish round r before
+// they wait for round r - 1 (so a round's exchange overlaps a whole row of work), so a part can run ahead:
+// it publishes round r + 1 once it has read round r - 1, but round r + 2 only after it has read round r,
+// which needs every part to have published r; a part can therefore publish round r + 4 only after every
+// part has read round r (each reads round r before publishing r + 2). Rounds cycle through four slot sets,
+// and a reader never takes a word of another round: tags are unique within a launch, and the last part of
+// a group to finish the kernel returns the group's words to zero (the runtime zeroes the workspace at
+// load and after a wait that gave up). The consumer requests the words before its next row's loads
+// (vector loads complete in order, so it does not wait behind them) and checks the tags with a wave vote;
+// it polls again only while a part is behind. The waits need all of the kernel's workgroups resident at
+// once: the code generator launches at most one per compute unit, and the runtime refuses to load a
+// cooperative grid the device cannot hold. A wait is bounded: after kCoopSpinLimit polls it sets
+// kCoopTimeout in the error word and the kernel ends (the runtime then raises), so it cannot hang.
+constexpr uint32_t kCoopDepartWord = 128;   // error-region words 128..191: per-group departure counters
+constexpr uint32_t kCoopGroups = 64;
+constexpr uint32_t kCoopTimeout = 2u;       // error-word bit of a cooperative wait that gave up
+constexpr uint32_t kCoopSpinLimit = 1u << 21;
+
+// Publish this part's N floats for ``round``: lanes 0 .. N - 1 of the first wave store one word each.
+template <int P, int N>
+__device__ __forceinline__ void coop_publish(unsigned long long* slots, uint32_t part, uint32_t round, const float (&mine)[N]) {
+    static_assert(N >= 1 && N <= 2, "one or two floats per part");
+    const uint32_t lane = threadIdx.x;
+    if (lane < uint32_t(N)) {
+        const float value = (N == 1 || lane == 0) ? mine[0] : mine[N - 1];
+        const unsigned long long word = (static_cast<unsigned long long>(round + 1u) << 32) | __float_as_uint(value);
+        store_device(slots + (round & 3u) * uint32_t(P * N) + part * uint32_t(N) + lane, word);
+    }
+}
+
+// Request the words of ``round`` (lane i of the first wave: word i of the round's set), to be checked by
+// ``coop_wait``; call before the next row's loads.
+template <int P, int N>
+__device__ __forceinline__ unsigned long long coop_peek(const unsigned long long* slots, uint32_t round) {
+    static_assert(P * N <= 64, "one word per lane of a wave");
+    const uint32_t lane = threadIdx.x;
+    return lane < uint32_t(P * N) ? load_device(slots + (round & 3u) * uint32_t(P * N) + lane) : 0ull;
+}
+
+// Wait until every part's words of ``round`` carry its tag (polling again from ``word``, the lane's peeked
+// word) and give every thread the floats in part order; false (and kCoopTimeout in the error word) if the
+// wait gave up.
+template <int P, int N>
+__device__ __forceinline__ bool coop_wait(const unsigned long long* slots, uint32_t round, unsigned long long word, float (&all)[P][N],
+                                          unsigned int* error) {
+    __shared__ float shared_all[P * N];
+    __shared__ int shared_ok;
+    if (threadIdx.x < kWave) {
+        const uint32_t lane = threadIdx.x;
+        const unsigned int tag = round + 1u;
+        uint32_t polls = 0;
+        bool arrived = true;
+        while (!__all(lane >= uint32_t(P * N) || uint32_t(word >> 32) == tag)) {
+            if (++polls > kCoopSpinLimit) {
+                arrived = false;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            word = coop_peek<P, N>(slots, round);
+        }
+        if (lane < uint32_t(P * N)) {
+            shared_all[lane] = __uint_as_float(uint32_t(word));
+        }
+        if (lane == 0) {
+            shared_ok = arrived;
+            if (!arrived) {
+                atomicOr(error, kCoopTimeout);
+            }
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+#pragma unroll
+        for (int n = 0; n < N; ++n) {
+            all[q][n] = shared_all[q * N + n];
+        }
+    }
+    const bool ok = shared_ok != 0;
+    __syncthreads();  // shared_all is rewritten by the next round
+    return ok;
+}
+
+// End of a cooperative kernel for one workgroup: the last part of the group to leave (every part has read
+// every round by then) returns the group's words and its departure counter to zero for the next launch.
+template <int P, int N>
+__device__ __forceinline__ void coop_depart(unsigned long long* slots, unsigned int* depart) {
+    __shared__ int last;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        last = atomicAdd(depart, 1u) == uint32_t(P - 1);
+    }
+    __syncthreads();
+    if (last) {
+        for (uint32_t i = threadIdx.x; i < uint32_t(4 * P * N); i += blockDim.x) {
+            store_device(slots + i, 0ull);
+        }
+        if (threadIdx.x == 0) {
+            atomicExch(depart, 0u);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Streaming (non-temporal) vector stores for results no later instruction of the same kernel reads.
 typedef float float2_nt __attribute__((ext_vector_type(2)));
 typedef float float4_nt __attribute__((ext_vector_type(4)));

@@ -217,6 +217,9 @@ public:
             // tickets of split routers (chroma::router_split) and words 64-127 those of split-key decode
             // attentions (chroma::attention_decode); both return them to zero.
             check(hipMemset(static_cast<char*>(base_) + plan_.error, 0, kErrorRegion), "Clear error region");
+            // The workspace starts at zero too: cooperative kernels exchange tagged words there and return
+            // them to zero themselves (every other workspace buffer is written before it is read).
+            check(hipMemset(static_cast<char*>(base_) + plan_.weight_bytes, 0, plan_.error - plan_.weight_bytes), "Clear workspace");
             upload_weights(directory + "/" + plan_.weights_file);
             check(hipModuleLoad(&module_, (directory + "/" + plan_.code_object).c_str()), "hipModuleLoad");
             std::map<std::string, hipFunction_t> functions;
@@ -228,6 +231,9 @@ public:
                     found = functions.emplace(launch.kernel, function).first;
                 }
                 launch.function = found->second;
+                if (launch.kernel.rfind("chroma_coop_", 0) == 0) {
+                    check_co_resident(launch);
+                }
                 launch.pointers.resize(launch.offsets.size());
                 launch.arguments.resize(launch.offsets.size());
                 for (size_t i = 0; i < launch.offsets.size(); ++i) {
@@ -637,14 +643,37 @@ private:
         }
     }
 
+    // A cooperative kernel (chroma_coop_*) has its workgroups wait for each other, which needs every one of
+    // them resident at once: refuse to load a program whose cooperative grid this device cannot hold (its
+    // waits are bounded and would end in an error rather than a hang, but the result would be lost).
+    void check_co_resident(const Launch& launch) {
+        int per_cu = 0, cus = 0;
+        check(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, launch.function, int(launch.block), launch.shared),
+              "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
+        check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device_), "hipDeviceGetAttribute");
+        const size_t grid = size_t(launch.grid[0]) * launch.grid[1] * launch.grid[2];
+        if (size_t(per_cu) * size_t(cus) < grid) {
+            throw std::runtime_error("Cooperative kernel " + launch.kernel + " needs " + std::to_string(grid) +
+                                     " co-resident workgroups; this device holds " + std::to_string(per_cu * cus));
+        }
+    }
+
     void raise_index_error() {
         if (*error_host_) {
+            const unsigned word = *error_host_;
             *error_host_ = 0;
             // the whole error region: the index word and the in-kernel handoff tickets (words 16-255), which
             // every launch returns to zero itself; clearing them here too (outside any captured graph, after
             // the stream has drained) leaves nothing for a later launch to inherit
             check(hipMemsetAsync(static_cast<char*>(base_) + plan_.error, 0, kErrorRegion, stream_), "Clear index error");
             check(hipStreamSynchronize(stream_), "Clear index error");
+            if (word & 2u) {
+                // words a cooperative kernel left behind would match a later launch's tags
+                check(hipMemsetAsync(static_cast<char*>(base_) + plan_.weight_bytes, 0, plan_.error - plan_.weight_bytes, stream_),
+                      "Clear workspace");
+                check(hipStreamSynchronize(stream_), "Clear workspace");
+                throw std::runtime_error("Cooperative workgroups timed out waiting for each other");
+            }
             throw IndexError("Tensor index out of range");
         }
     }

@@ -1339,6 +1339,50 @@ def test_vocabulary_softmax_split_rows(tmp_path, rows, width, dtype):
     assert np.isnan(as_float(got)[[r for r in range(rows) if r not in ordinary]]).all()
 
 
+class WeightedRowNorm(torch.nn.Module):
+    """RMSNorm over the last axis as the explicit chain, with a weight that is not all ones."""
+
+    def __init__(self, weight: torch.Tensor) -> None:
+        super().__init__()
+        self.weight = torch.nn.Parameter(weight, requires_grad=False)
+
+    def forward(self, x):
+        return x * torch.rsqrt(torch.mean(x**2, dim=-1, keepdim=True) + 1e-5) * self.weight
+
+
+@pytest.mark.parametrize("kind, dtype", [("softmax", torch.float32), ("softmax", torch.bfloat16), ("rmsnorm", torch.float32)])
+def test_vocabulary_rows_cooperative(tmp_path, kind, dtype):
+    """Softmax and RMSNorm of many vocabulary-wide rows in one HBM pass: co-resident workgroups share each
+    row, keep their slices in registers and exchange partial statistics (chroma_coop_* kernels). 300 rows
+    (not a multiple of the rows in flight), NaN / +inf / -inf rows (softmax: NaN everywhere in them, as
+    the reference's exp(x - max) / sum gives), a weight that is not all ones (RMSNorm); three runs in a
+    row must agree bit for bit (the group counters return to zero after every launch). Against the oracle
+    on the first 40 rows and, on ordinary rows, against float64."""
+    rows, width = 300, 201088
+    x = vocabulary_rows(rows, width, dtype, 11 * rows + width)
+    if kind == "softmax":
+        module = RowSoftmax()
+    else:
+        x = torch.where(torch.isfinite(x), x, torch.zeros((), dtype=dtype))
+        module = WeightedRowNorm((torch.rand(width, generator=torch.Generator().manual_seed(5)) + 0.5).to(dtype))
+    exported = torch.export.export(module, (x,))
+    with chroma_amd.compile(exported, tmp_path / "hip") as model:
+        assert f"chroma_coop_{kind}" in (tmp_path / "hip" / "model.plan").read_text()
+        got = model(x)
+        for _ in range(2):
+            np.testing.assert_array_equal(np.asarray(model(x)).view(np.uint8), np.asarray(got).view(np.uint8))
+    head = x[:40].contiguous()
+    want = compile_cpu(torch.export.export(module, (head,)), tmp_path / "cpu")(numpy_of(head))
+    tolerance = BF16 if dtype == torch.bfloat16 else dict(rtol=1e-3, atol=1e-5)
+    assert_close(got[:40], want, **tolerance)
+    ordinary = [r for r in range(rows) if r not in (1, 2, 3)] if kind == "softmax" else list(range(rows))
+    sample = ordinary[::13]
+    exact = (torch.softmax(x[sample].double(), -1) if kind == "softmax" else module(x[sample].double()).double()).numpy()
+    np.testing.assert_allclose(as_float(got)[sample], exact, **(BF16 if dtype == torch.bfloat16 else F32))
+    if kind == "softmax":
+        assert np.isnan(as_float(got)[[1, 2, 3]]).all()
+
+
 # ------------------------------------------------------------------------------------- row selection
 def host_topk(row: np.ndarray, k: int, largest: bool) -> np.ndarray:
     """The reference GPU top-k order (gpu.py:300-337) on one row: NaN first for largest and last for
