@@ -249,6 +249,9 @@ class Decoder:
             )
             for model in self._models
         ]
+        # Multi-step hip programs build their masks on the device (NativeModel.decoder_masks).
+        self._device_masks = [self._on_device and isinstance(model.native, NativeModel) and model.inputs[0]["shape"][0] > 1
+                              for model in self._models]
         self._extras: List[Tuple[int, int, List[np.ndarray]]] = []
         self._row_bytes = int(np.prod(self._shape[2:])) * self._cache_dtype.itemsize
         self._selectors: dict = {}  # (k, gathered ids or None) -> top-k selection program (hip pairs)
@@ -272,12 +275,19 @@ class Decoder:
 
     # ---------------------------------------------------------------------------- device-resident cache
     def _device_cache(self, which: int, args: List[Any]) -> None:
-        """Make program ``which``'s device copy of the cache the committed cache: upload zeros to a fresh
-        cache, copy from the owner's staging when another program owns it, or leave it (args None)."""
+        """Make program ``which``'s device copy of the cache the committed cache: zero a fresh cache (on the
+        device for hip programs, else by uploading zeros), copy from the owner's staging when another
+        program owns it, or leave it (args None)."""
         owner = self._state.owner
         if owner is None:
-            zeros = np.zeros(self._shape, dtype=self._cache_dtype)
-            args[2], args[3] = zeros, zeros
+            native = self._models[which].native
+            if isinstance(native, NativeModel):
+                native.clear_input(2)
+                native.clear_input(3)
+                args[2] = args[3] = None
+            else:
+                zeros = np.zeros(self._shape, dtype=self._cache_dtype)
+                args[2], args[3] = zeros, zeros
             return
         args[2] = args[3] = None
         if owner != which:
@@ -446,6 +456,10 @@ class Decoder:
                         np.copyto(window_mask, full_mask)
                     else:
                         _fill_row(window_mask, state.slots > max(state.position - self._window, -1))
+                elif self._device_masks[which]:
+                    # Built on the device into the mask inputs' staging (the next run is given None for them):
+                    # two [steps, context + steps] masks never cross the host link.
+                    self._models[which].native.decoder_masks(state.slots, state.position, steps, self._window, 4, 5)
                 else:
                     _fill_masks(((full_mask, self.context), (window_mask, self._window)), np.concatenate((state.slots, times)),
                                 np.concatenate((state.slots >= 0, np.ones(steps, dtype=bool))), times)
@@ -456,10 +470,14 @@ class Decoder:
                 slots[rows] = times[:count]
                 if self._on_device:
                     self._device_cache(which, args)
+                    inputs = args
+                    if self._device_masks[which]:
+                        inputs = list(args)
+                        inputs[4] = inputs[5] = None  # the masks built on the device above
                     if top is not None and offset + count == len(ids):
-                        selection = self._models[which].run_top_resident(args, [logits, *updates, *extras], 0, top)
+                        selection = self._models[which].run_top_resident(inputs, [logits, *updates, *extras], 0, top)
                     else:
-                        self._models[which].run_resident(args, [logits, *updates, *extras])
+                        self._models[which].run_resident(inputs, [logits, *updates, *extras])
                     with _interrupts_deferred():
                         self._device_commit(which, state.position, count, steps)
                         self._commit(CacheState(None, None, slots, state.position + count, which))

@@ -70,7 +70,9 @@ def empty(shape: Sequence[int], dtype: np.dtype) -> np.ndarray:
                 _held -= size
             return np.empty(shape, dtype)
         pointer = handle.value
-    return np.asarray(_Lease(pointer, size, tuple(int(n) for n in shape), dtype.str))
+    array = np.asarray(_Lease(pointer, size, tuple(int(n) for n in shape), dtype.str))
+    # A typestr names only the item size of a dtype NumPy does not know by string (bfloat16 reads '<V2').
+    return array if array.dtype == dtype else array.view(dtype)
 
 
 def pooled_bytes() -> int:

@@ -21,6 +21,7 @@ LIBRARY = PACKAGE / "lib" / "libchroma_hip.so"
 RUNTIME_SOURCE = PACKAGE / "csrc" / "runtime.cpp"
 SELECT_SOURCE = PACKAGE / "csrc" / "select.hip"
 COPY_SOURCE = PACKAGE / "csrc" / "copy.hip"
+MASKS_SOURCE = PACKAGE / "csrc" / "masks.hip"
 DEVICE_INCLUDE = PACKAGE / "csrc" / "include"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 
@@ -43,6 +44,7 @@ def build_runtime(output: Path = LIBRARY) -> Path:
     device_flags = [flag for flag in DEVICE_FLAGS if flag != "--genco"]
     with tempfile.TemporaryDirectory(prefix="chroma-runtime-") as work:
         host_object, device_object, copy_object = Path(work) / "runtime.o", Path(work) / "select.o", Path(work) / "copy.o"
+        masks_object = Path(work) / "masks.o"
         commands = [
             [*shlex.split(os.environ.get("CXX", "g++")), "-std=c++17", "-O2", "-c", "-fPIC", "-fvisibility=hidden", "-D__HIP_PLATFORM_AMD__",
              f"-I{ROCM / 'include'}", str(RUNTIME_SOURCE), "-o", str(host_object)],
@@ -50,7 +52,10 @@ def build_runtime(output: Path = LIBRARY) -> Path:
              str(SELECT_SOURCE), "-o", str(device_object)],
             [*hipcc, f"--offload-arch={architecture()}", *device_flags, "-c", "-fPIC", "-fvisibility=hidden", f"-I{DEVICE_INCLUDE}",
              str(COPY_SOURCE), "-o", str(copy_object)],
-            [*hipcc, f"--offload-arch={architecture()}", "-shared", "-fPIC", str(host_object), str(device_object), str(copy_object), "-o", str(temporary),
+            [*hipcc, f"--offload-arch={architecture()}", *device_flags, "-c", "-fPIC", "-fvisibility=hidden", f"-I{DEVICE_INCLUDE}",
+             str(MASKS_SOURCE), "-o", str(masks_object)],
+            [*hipcc, f"--offload-arch={architecture()}", "-shared", "-fPIC", str(host_object), str(device_object), str(copy_object),
+             str(masks_object), "-o", str(temporary),
              f"-L{ROCM / 'lib'}", f"-Wl,-rpath,{ROCM / 'lib'}", "-lamdhip64"],
         ]
         for command in commands:
@@ -103,6 +108,9 @@ def library() -> ctypes.CDLL:
         lib.chroma_hip_copy_2d_queued.argtypes = lib.chroma_hip_copy_2d.argtypes
         lib.chroma_hip_copy_2d_batch_queued.argtypes = [c.c_void_p, c.POINTER(Rect), c.c_int, c.c_char_p, c.c_size_t]
         lib.chroma_hip_synchronize.argtypes = [c.c_void_p, c.c_char_p, c.c_size_t]
+        lib.chroma_hip_clear_input.argtypes = [c.c_void_p, c.c_int, c.c_char_p, c.c_size_t]
+        lib.chroma_hip_decoder_masks.argtypes = [c.c_void_p, c.c_void_p, c.c_int64, c.c_int64, c.c_int64, c.c_int64, c.c_int, c.c_int, c.c_int,
+                                                 c.c_char_p, c.c_size_t]
         lib.chroma_hip_host_alloc.argtypes = [c.c_size_t, c.POINTER(c.c_void_p), c.c_char_p, c.c_size_t]
         lib.chroma_hip_host_free.argtypes = [c.c_void_p]
         lib.chroma_hip_host_free.restype = None
@@ -127,6 +135,8 @@ EXPORTED = (
     "chroma_hip_upload",
     "chroma_hip_execute",
     "chroma_hip_execute_chained",
+    "chroma_hip_decoder_masks",
+    "chroma_hip_clear_input",
     "chroma_hip_download",
     "chroma_hip_set_graph",
     "chroma_hip_launch_count",

@@ -147,6 +147,25 @@ class NativeModel:
         error = ctypes.create_string_buffer(256)
         native.check(self._lib.chroma_hip_copy_2d_batch_queued(self._handle, array, len(rects), error, len(error)), error)
 
+    def clear_input(self, index: int) -> None:
+        """Zero input ``index``'s device staging, queued on this program's stream (see ``synchronize``)."""
+        error = ctypes.create_string_buffer(256)
+        native.check(self._lib.chroma_hip_clear_input(self._handle, index, error, len(error)), error)
+
+    def decoder_masks(self, slots: np.ndarray, position: int, steps: int, window: int, full_input: int, window_input: int) -> None:
+        """Build a multi-step decoder call's two attention masks on the device, in the staging regions of
+        inputs ``full_input`` (window = the cache's context) and ``window_input`` (``window``), queued on
+        this program's stream ahead of the next resident run, which is then given None for them.
+        ``slots`` [context] holds each cache row's time (negative when empty); query t sits at
+        ``position + t``; the masks' dtype is the program's for those inputs."""
+        table = np.ascontiguousarray(slots, dtype=np.int64)
+        dtype = self._specs[full_input][0]
+        code = native.FLOAT32 if dtype == np.dtype(np.float32) else native.BFLOAT16
+        error = ctypes.create_string_buffer(512)
+        status = self._lib.chroma_hip_decoder_masks(self._handle, table.ctypes.data, len(table), position, steps, window, code, full_input,
+                                                    window_input, error, len(error))
+        native.check(status, error)
+
     def synchronize(self) -> None:
         """Wait for everything queued on this program's stream."""
         error = ctypes.create_string_buffer(256)

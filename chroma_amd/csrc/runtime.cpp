@@ -6,6 +6,7 @@
 // the captured hipGraph), downloads the error word and the outputs, and synchronizes once.
 #include "../../include/chroma_hip.h"
 #include "copy.h"
+#include "masks.h"
 #include "select.h"
 
 #include <hip/hip_runtime_api.h>
@@ -286,6 +287,15 @@ public:
         if (error_host_) {
             hipHostFree(error_host_);
         }
+        if (slots_) {
+            hipFree(slots_);
+        }
+        if (slots_host_) {
+            hipHostFree(slots_host_);
+        }
+        if (slots_copied_) {
+            hipEventDestroy(slots_copied_);
+        }
         for (int slot = 0; slot < 2; ++slot) {
             if (staging_[slot]) {
                 hipHostFree(staging_[slot]);
@@ -315,6 +325,10 @@ public:
         select_bytes_ = 0;
         select_host_ = nullptr;
         select_host_bytes_ = 0;
+        slots_ = nullptr;
+        slots_host_ = nullptr;
+        slots_capacity_ = 0;
+        slots_copied_ = nullptr;
         error_host_ = nullptr;
         start_ = stop_ = nullptr;
         stream_ = nullptr;
@@ -496,6 +510,17 @@ public:
         }
     }
 
+    // Queued zero fill of input ``index``'s staging region (never part of a captured graph).
+    void clear_input(size_t index) {
+        DeviceGuard guard(device_);
+        if (index >= plan_.inputs.size()) {
+            throw std::runtime_error("clear_input: no such input");
+        }
+        if (plan_.inputs[index].bytes) {
+            check(hipMemsetAsync(input_pointer(index), 0, plan_.inputs[index].bytes, stream_), "hipMemsetAsync");
+        }
+    }
+
     // Queued rectangle copies in one kernel launch (copy.hip).
     void copy_2d_batch(const chroma_hip_rect* rects, int count) {
         DeviceGuard guard(device_);
@@ -514,6 +539,53 @@ public:
         }
         char message[256] = {0};
         if (chroma_copy::launch_copy_rects(copies, used, stream_, message, sizeof(message))) {
+            throw std::runtime_error(message);
+        }
+    }
+
+    // The two attention masks of a multi-step decoder call, written by a kernel queued on this program's
+    // stream straight into the staging regions of inputs ``full_input`` and ``window_input`` (so the next
+    // resident run, given None for them, uses them): the slot table goes up (through a pinned copy), and
+    // chroma_masks builds both masks from it.
+    void decoder_masks(const int64_t* slots, int64_t context, int64_t position, int64_t steps, int64_t window, bool bfloat16,
+                       size_t full_input, size_t window_input) {
+        DeviceGuard guard(device_);
+        if (full_input >= plan_.inputs.size() || window_input >= plan_.inputs.size() || context < 1 || steps < 1) {
+            throw std::runtime_error("decoder_masks: no such inputs or an empty call");
+        }
+        const size_t bytes = size_t(steps) * size_t(context + steps) * (bfloat16 ? 2u : 4u);
+        if (plan_.inputs[full_input].bytes != bytes || plan_.inputs[window_input].bytes != bytes) {
+            throw std::runtime_error("decoder_masks: the mask inputs are not [steps, context + steps] of that dtype");
+        }
+        if (slots_copied_ == nullptr) {
+            check(hipEventCreateWithFlags(&slots_copied_, hipEventDisableTiming), "decoder_masks hipEventCreate");
+        } else {
+            // the previous call's upload out of the pinned table has finished before the table is rewritten
+            // (the device table itself is only rewritten by a copy queued after the kernels that read it)
+            check(hipEventSynchronize(slots_copied_), "decoder_masks");
+        }
+        if (slots_capacity_ < size_t(context)) {
+            check(hipStreamSynchronize(stream_), "decoder_masks");  // the old device table is no longer read
+            if (slots_) {
+                hipFree(slots_);
+                slots_ = nullptr;
+            }
+            if (slots_host_) {
+                hipHostFree(slots_host_);
+                slots_host_ = nullptr;
+            }
+            slots_capacity_ = 0;
+            check(hipMalloc(reinterpret_cast<void**>(&slots_), size_t(context) * sizeof(int64_t)), "decoder_masks hipMalloc");
+            check(hipHostMalloc(reinterpret_cast<void**>(&slots_host_), size_t(context) * sizeof(int64_t), hipHostMallocDefault),
+                  "decoder_masks hipHostMalloc");
+            slots_capacity_ = size_t(context);
+        }
+        std::memcpy(slots_host_, slots, size_t(context) * sizeof(int64_t));
+        check(hipMemcpyAsync(slots_, slots_host_, size_t(context) * sizeof(int64_t), hipMemcpyHostToDevice, stream_), "decoder_masks upload");
+        check(hipEventRecord(slots_copied_, stream_), "decoder_masks hipEventRecord");
+        char message[256] = {0};
+        if (chroma_masks::launch_decoder_masks(slots_, context, position, steps, window, bfloat16, input_pointer(full_input),
+                                               input_pointer(window_input), stream_, message, sizeof(message))) {
             throw std::runtime_error(message);
         }
     }
@@ -792,6 +864,10 @@ private:
     hipGraph_t graph_ = nullptr;
     hipGraphExec_t graph_exec_ = nullptr;
     void* staging_[2] = {nullptr, nullptr};  // pinned slots for pageable host transfers (allocated on first use)
+    int64_t* slots_ = nullptr;       // decoder_masks: the cache's slot table on the device (allocated on first use)
+    int64_t* slots_host_ = nullptr;  // and its pinned copy (the caller's array may be gone before the copy ends)
+    size_t slots_capacity_ = 0;      // entries both hold
+    hipEvent_t slots_copied_ = nullptr;  // recorded after each upload out of slots_host_
     void* select_ = nullptr;  // run_top's selection scratch and device results (allocated on first use)
     size_t select_bytes_ = 0;
     void* select_host_ = nullptr;  // pinned landing area of run_top's ids and values
@@ -893,6 +969,21 @@ __attribute__((visibility("default"))) int chroma_hip_launch_count(void* handle)
 
 __attribute__((visibility("default"))) void* chroma_hip_device_base(void* handle) { return program(handle)->base(); }
 
+__attribute__((visibility("default"))) int chroma_hip_decoder_masks(void* handle, const int64_t* slots, int64_t context, int64_t position,
+                                                                    int64_t steps, int64_t window, int dtype, int full_input,
+                                                                    int window_input, char* error, size_t error_size) {
+    return guarded(error, error_size, [&] {
+        if (dtype != CHROMA_HIP_FLOAT32 && dtype != CHROMA_HIP_BFLOAT16) {
+            throw std::runtime_error("decoder_masks: float32 or bfloat16 masks");
+        }
+        if (full_input < 0 || window_input < 0) {
+            throw std::runtime_error("decoder_masks: negative input index");
+        }
+        program(handle)->decoder_masks(slots, context, position, steps, window, dtype == CHROMA_HIP_BFLOAT16, size_t(full_input),
+                                       size_t(window_input));
+    });
+}
+
 __attribute__((visibility("default"))) void* chroma_hip_input_pointer(void* handle, int index) {
     return index < 0 ? nullptr : program(handle)->input_pointer(size_t(index));
 }
@@ -934,6 +1025,15 @@ __attribute__((visibility("default"))) int chroma_hip_copy_2d_batch_queued(void*
 __attribute__((visibility("default"))) int chroma_hip_copy_2d_queued(void* handle, void* dst, size_t dst_pitch, const void* src, size_t src_pitch,
                                                                      size_t width, size_t height, char* error, size_t error_size) {
     return guarded(error, error_size, [&] { program(handle)->copy_2d(dst, dst_pitch, src, src_pitch, width, height, true); });
+}
+
+__attribute__((visibility("default"))) int chroma_hip_clear_input(void* handle, int index, char* error, size_t error_size) {
+    return guarded(error, error_size, [&] {
+        if (index < 0) {
+            throw std::runtime_error("clear_input: negative input index");
+        }
+        program(handle)->clear_input(size_t(index));
+    });
 }
 
 __attribute__((visibility("default"))) int chroma_hip_synchronize(void* handle, char* error, size_t error_size) {

@@ -69,6 +69,18 @@ int chroma_hip_execute(void* handle, int iterations, float* milliseconds, char* 
  * per-replay graph launch. */
 int chroma_hip_execute_chained(void* handle, int copies, int iterations, float* milliseconds, char* error, size_t error_size);
 
+/* The two attention masks [steps, context + steps] of a multi-step KV-cached decoder call, built on the
+ * device into the staging regions of inputs ``full_input`` and ``window_input`` (float32 or bfloat16,
+ * ``dtype`` CHROMA_HIP_FLOAT32 / CHROMA_HIP_BFLOAT16) by a kernel queued on the program's stream, so the
+ * next resident run (given NULL for those inputs) uses them. ``slots`` (host, ``context`` entries) holds
+ * the time of each cache row or a negative value for an empty row; query t sits at position + t. Element
+ * (t, j) is 0 where key j is valid, not after the query and inside the window (``context`` for the full
+ * mask, ``window`` for the other), -inf elsewhere: the reference decoder's host masks
+ * (chroma/_src/decoder.py:116-128), which this replaces for multi-step calls (no counterpart in the
+ * reference's C++: its masks are host arrays uploaded every call). */
+int chroma_hip_decoder_masks(void* handle, const int64_t* slots, int64_t context, int64_t position, int64_t steps, int64_t window,
+                             int dtype, int full_input, int window_input, char* error, size_t error_size);
+
 /* Copy the output staging regions to host buffers. */
 int chroma_hip_download(void* handle, void* const* outputs, char* error, size_t error_size);
 
@@ -99,6 +111,11 @@ int chroma_hip_copy_2d(void* handle, void* dst, size_t dst_pitch, const void* sr
 int chroma_hip_copy_2d_queued(void* handle, void* dst, size_t dst_pitch, const void* src, size_t src_pitch, size_t width,
                               size_t height, char* error, size_t error_size);
 int chroma_hip_synchronize(void* handle, char* error, size_t error_size);
+
+/* Zero input ``index``'s staging region, queued on the program's stream like
+ * ``chroma_hip_copy_2d_queued``. No counterpart in the reference (whose decoder uploads a zeroed host
+ * cache): the decoder starts a fresh device-resident KV cache with it instead of uploading zeros. */
+int chroma_hip_clear_input(void* handle, int index, char* error, size_t error_size);
 
 /* Up to four queued device-to-device rectangle copies (as ``chroma_hip_copy_2d_queued``) in one kernel
  * launch on the program's stream. No counterpart in the reference: the decoder commits a step's new key

@@ -365,3 +365,35 @@ def test_multi_step_masks_match_the_general_rule():
                 _fill_mask(as_mask(general), causal & (key_times[None] > times[:, None] - window))
                 np.testing.assert_array_equal(general.view(np.uint8), mask.view(np.uint8))
 
+
+
+def test_pinned_results_keep_their_dtype(monkeypatch):
+    """``host.empty`` hands out arrays of the asked dtype, bfloat16 included (an array interface's typestr
+    alone reads as raw two-byte items), backed by the leased block and returned to the pool when dropped."""
+    import ctypes
+    import gc
+
+    from chroma_amd._src import host, native
+    from chroma_amd._src.dtypes import BFLOAT16
+
+    blocks = []
+
+    class Library:
+        def chroma_hip_host_alloc(self, size, handle, error, error_size):
+            blocks.append(ctypes.create_string_buffer(size))
+            ctypes.cast(handle, ctypes.POINTER(ctypes.c_void_p))[0] = ctypes.addressof(blocks[-1])
+            return native.OK
+
+    monkeypatch.setattr(native, "library", lambda: Library())
+    monkeypatch.setattr(host, "_free", {})
+    monkeypatch.setattr(host, "_held", 0)
+    for dtype in (np.float32, BFLOAT16, np.int64):
+        array = host.empty((3, 5), dtype)
+        assert array.dtype == np.dtype(dtype) and array.shape == (3, 5) and array.flags.c_contiguous
+        assert array.ctypes.data == ctypes.addressof(blocks[-1])
+        array[...] = 1
+        assert float(array.astype(np.float32).sum()) == 15.0
+        del array
+        gc.collect()
+    assert host._free == {host.PAGE: [ctypes.addressof(blocks[0])]}  # one block, reused each time
+    assert len(blocks) == 1

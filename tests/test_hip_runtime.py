@@ -615,6 +615,61 @@ def test_small_transformer_and_decoder(tmp_path, dtype):
         np.testing.assert_array_equal(logits.view(np.uint8), preserved.view(np.uint8))
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decoder_masks_on_device(tmp_path, dtype):
+    """A multi-step call's two masks built by the device kernel equal the host rule (``_fill_masks``) bit
+    for bit: an empty cache, a partly filled one, a wrapped ring, and arbitrary slot tables (times after the
+    queries, negative entries), for a window inside the context and one equal to it."""
+    from chroma_amd._src.decoder import _fill_masks
+    from chroma_amd.models.cached import export_cached
+
+    context, steps = 7, 4
+    eager = random_transformer(small_config(), seed=2, std=0.1, dtype=dtype)
+    with chroma_amd.compile(export_cached(eager, context, steps), tmp_path / "prefill") as program:
+        native = program.native
+        mask_dtype = numpy_dtype_of(program.inputs[4])
+        size = steps * (context + steps) * mask_dtype.itemsize
+        readback = torch.empty(size, dtype=torch.uint8, device="cuda")
+
+        def device_mask(index):
+            native.copy_2d(readback.data_ptr(), size, native.input_pointer(index), size, size, 1)
+            return readback.cpu().numpy().copy()
+
+        wrapped = np.full(context, -1, dtype=np.int64)
+        for t in range(5, 12):
+            wrapped[t % context] = t
+        rng = np.random.default_rng(4)
+        cases = [(np.full(context, -1, dtype=np.int64), 0), (np.array([0, 1, 2, -1, -1, -1, -1], dtype=np.int64), 3), (wrapped, 12),
+                 (rng.integers(-3, 20, context).astype(np.int64), 9), (rng.integers(-1, 40, context).astype(np.int64), 30)]
+        for slots, position in cases:
+            for window in (3, context):
+                times = position + np.arange(steps, dtype=np.int64)
+                full = np.empty((steps, context + steps), mask_dtype)
+                windowed = np.empty_like(full)
+                _fill_masks(((full, context), (windowed, window)), np.concatenate((slots, times)),
+                            np.concatenate((slots >= 0, np.ones(steps, dtype=bool))), times)
+                native.decoder_masks(slots, position, steps, window, 4, 5)
+                label = f"slots {slots.tolist()} position {position} window {window}"
+                np.testing.assert_array_equal(device_mask(4), full.view(np.uint8).ravel(), err_msg=label)
+                np.testing.assert_array_equal(device_mask(5), windowed.view(np.uint8).ravel(), err_msg=label)
+        with pytest.raises(RuntimeError, match="not \\[steps, context \\+ steps\\]"):
+            native.decoder_masks(wrapped, 12, steps, 3, 0, 5)  # input 0 (the token ids) is no mask
+        # clear_input zeroes a whole staging region (the decoder's fresh device cache)
+        cache_bytes = int(np.prod(program.inputs[2]["shape"])) * numpy_dtype_of(program.inputs[2]).itemsize
+        filled = torch.full((cache_bytes,), 0x7F, dtype=torch.uint8, device="cuda")
+        torch.cuda.synchronize()
+        native.copy_2d(native.input_pointer(2), cache_bytes, filled.data_ptr(), cache_bytes, cache_bytes, 1)
+        native.clear_input(2)
+        native.copy_2d(filled.data_ptr(), cache_bytes, native.input_pointer(2), cache_bytes, cache_bytes, 1)
+        assert int(filled.count_nonzero()) == 0
+
+
+def numpy_dtype_of(spec):
+    from chroma_amd._src.dtypes import numpy_dtype
+
+    return numpy_dtype(spec["dtype"])
+
+
 def test_yarn_sliding_window_lengths(tmp_path):
     import dataclasses
 
