@@ -77,12 +77,17 @@ WIDE_GEMM_TILE = (256, 192)  # chroma::kWideM, kWideN
 # the wide body takes dense products with at least this many of its tiles: below that its larger tiles
 # leave too much of the chip idle and the 128 x 128 body is faster
 WIDE_GEMM_MIN_TILES = 200
-# bfloat16 expert products whose channel count is a multiple of a tile width here take the ring body on
-# 128-slot x width tiles (chroma::grouped_expert_linear PATH 3) with that many waves side by side (each
-# wave all 128 slots of a width / waves strip). Measured on the GPT-OSS-20B shapes (2048 tokens x top-4 of
-# 32): 384 on 8 waves 465 us for the 5760-channel up product, 320 on 4 waves 237-240 us for the 2880-channel
-# down product (the 128 x 128 direct-to-LDS body: 517 and 253 us)
-RING_EXPERT_TILES = ((384, 8), (320, 4))
+# bfloat16 expert products whose channel count is a multiple of a tile width here (the first that fits)
+# take the ring body (chroma::grouped_expert_linear PATH 3) on 128-slot x width tiles with that many waves
+# side by side (each wave all slots of a width / waves strip), and an expert's last tile holds up to the
+# third figure's slots: at 160 a remainder of up to 32 slots past a full tile joins it instead of costing
+# a whole tile of its own (chroma::kTallLastTile). Measured on the GPT-OSS-20B shapes (2048 tokens x top-4
+# of 32): with balanced routing (~256 slots per expert, half the experts with a third tile of a few slots)
+# the 5760-channel up product on 384 x 8 waves takes 466 us with 128-slot last tiles and 409 us with 160;
+# the 2880-channel down product on 320 x 4 waves 240 us and 250 us (its 585 workgroups still take three
+# rounds of the chip's 256, now with longer tiles among them), on 192 x 4 waves with 160 236 us, but 276 us
+# against 241 us on the skewed routing the seeded C5 model produces (expert counts 0-1842 at layer 19).
+RING_EXPERT_TILES = ((384, 8, 160), (320, 4, 128))
 REUSED_EVALUATIONS = 1 << 18  # a contraction operand is stored when (elements x reuse) reaches this
 SMALL_REDUCTION = 8  # contractions summing at most this many products are fused expressions...
 SMALL_OPERAND_COST = 8  # ...over operands that cost at most this much per element (others are stored)
@@ -2665,12 +2670,13 @@ class HIPCodegen(Codegen):
         return out
 
     def _route(self, indices: Value, experts: int) -> Tuple[Value, int]:
-        """Group the slots of a router output by expert once; both expert contractions of a layer share it."""
+        """Group the slots of a router output by expert once; both expert contractions of a layer share it
+        (its two tile tables serve 128-slot last tiles and taller ones)."""
         key = (indices.name, experts)
         slots = math.prod(indices.shape)
-        tiles = -(-slots // 128) + experts
+        tiles = -(-slots // 128) + experts  # chroma::expert_tile_bound
         if key not in self.routes:
-            words = 2 * experts + 2 + slots + 2 * tiles
+            words = 2 * experts + 2 + slots + 2 * tiles + 1 + 2 * tiles
             scratch = self.allocate((-(-words // 2),), torch.int64)
             k = Kernel(1)
             ids = self._matrix_slot(k, indices)
@@ -2682,23 +2688,25 @@ class HIPCodegen(Codegen):
         return self.routes[key], tiles
 
     def _grouped_experts(self, out, weight, indices, x, tokens, selected, experts, channels, inner, per_slot) -> None:
+        path, threads, width, waves, last = 1, 256, 128, 4, 128
+        ring = next(((n, w, t) for n, w, t in RING_EXPERT_TILES if channels % n == 0), None)
+        if out.dtype == torch.bfloat16 and inner % 32 == 0 and ring is not None:
+            path, (width, waves, last) = 3, ring
+            threads = 64 * waves
+        elif self._direct_gemm(out.dtype, inner):
+            path, threads = 2, DIRECT_GEMM_THREADS
         scratch, tiles = self._route(indices, experts)
         k = Kernel(1)
+        if path == 3:
+            k.min_waves = 1
+        elif path == 2:
+            k.min_waves = DIRECT_GEMM_BLOCKS
         w, xs = self._matrix_slot(k, weight), self._matrix_slot(k, x)
         table = k.slot(scratch.name, torch.int64, extent=self.extents[scratch.name])
         out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
-        path, threads, width, waves = 1, 256, 128, 4
-        ring = next(((n, w) for n, w in RING_EXPERT_TILES if channels % n == 0), None)
-        if out.dtype == torch.bfloat16 and inner % 32 == 0 and ring is not None:
-            path, width, waves = 3, *ring
-            threads = 64 * waves
-            k.min_waves = 1
-        elif self._direct_gemm(out.dtype, inner):
-            path, threads = 2, DIRECT_GEMM_THREADS
-            k.min_waves = DIRECT_GEMM_BLOCKS
         k.line(
-            f"chroma::grouped_expert_linear<{ctype_of(out.dtype)}, {str(per_slot).lower()}, {path}, {width}, 1, {waves}>({w}, {xs}, {out_slot}, "
-            f"reinterpret_cast<const int32_t*>({table}), {tokens * selected}u, {selected}u, {experts}u, {channels}u, {inner}u);"
+            f"chroma::grouped_expert_linear<{ctype_of(out.dtype)}, {str(per_slot).lower()}, {path}, {width}, 1, {waves}, {last}>({w}, {xs}, "
+            f"{out_slot}, reinterpret_cast<const int32_t*>({table}), {tokens * selected}u, {selected}u, {experts}u, {channels}u, {inner}u);"
         )
         self.launch(k, 8 * -(-(-(-channels // width) * tiles) // 8), threads, [weight, x, scratch], kind="experts_mfma")
         self.mfma_matmuls += 1

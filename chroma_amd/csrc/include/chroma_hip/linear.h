@@ -1063,21 +1063,34 @@ constexpr int16_t vmcnt_wait(uint32_t n) { return int16_t((n & 15u) | ((n >> 4) 
 // tiles on 1 x 4 waves (each wave all 128 slots of a 96- or 80-channel strip), which keeps the 128-slot
 // tiles of the ragged per-expert slot counts while reading 0.29-0.32 KB of LDS per MFMA instead of the
 // 32 x 64 wave tiles' 0.75 (the expert body was LDS-bound at about a fifth of the matrix-core peak).
-template <class T, int BM, int BN, int WM, int WN, int S>
+//
+// ``ring`` is the caller's LDS array of at least ``ring_elements<BM, BN, S>()`` bf16 elements (one array per
+// kernel, see grouped_expert_linear). When BM / 16 is not a multiple of the wave count, the A copies of the
+// last round go past the tile's row blocks: those copies repeat its last block (the same bytes to the same
+// LDS position), so every wave still issues the same number of copies per stage and the vmcnt waits hold.
+template <int BM, int BN, int S>
+constexpr int ring_elements() {
+    return S * (BM + BN) * 32;
+}
+
+template <class T, int BM, int BN, int WM, int WN, int S, int L = BM / WM / 16>
 __device__ __forceinline__ void mfma_gemm_ring(const uint16_t* __restrict__ a, uint32_t lda, const uint16_t* __restrict__ b,
                                                uint32_t ldb, const T* __restrict__ bias, T* __restrict__ c, uint32_t ldc,
                                                uint32_t m_total, uint32_t n_total, uint32_t k_total,
                                                const int32_t* __restrict__ a_rows, const int32_t* __restrict__ c_rows, uint32_t m0,
-                                               uint32_t n0, uint32_t a_div = 1) {
+                                               uint32_t n0, uint32_t a_div, uint16_t* ring) {
     static_assert(sizeof(T) == 2, "the ring body takes bfloat16");
     static_assert(S >= 3, "the ring needs a slot being read, one landed and one being filled");
     constexpr int WAVES = WM * WN;
     constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
-    constexpr int CA = BM / 16 / WAVES, CB = BN / 16 / WAVES, PER = CA + CB;  // 1 KB copies per wave per stage
-    constexpr int SLOT = (BM + BN) * 32;                                       // bf16 elements per ring slot
-    static_assert(CA * 16 * WAVES == BM && CB * 16 * WAVES == BN && PER <= TM, "one copy per MFMA row");
+    constexpr int A_BLOCKS = BM / 16;
+    constexpr int CA = (A_BLOCKS + WAVES - 1) / WAVES, CB = BN / 16 / WAVES, PER = CA + CB;  // 1 KB copies per wave per stage
+    constexpr int SLOT = (BM + BN) * 32;                                                    // bf16 elements per ring slot
+    static_assert(CB * 16 * WAVES == BN, "whole B row blocks per wave");
     static_assert(TM * WM * 16 == BM && TN * WN * 16 == BN, "whole 16 x 16 tiles per wave");
-    __shared__ __attribute__((aligned(1024))) uint16_t ring[S * SLOT];
+    // L live 16-row tiles per wave (the others hold no row of the tile: no MFMA, fragment read or store);
+    // the stage's copies are spread over the live rows' MFMA sequences, copy c in row c % L
+    static_assert(L >= 1 && L <= TM && (L == TM || WM == 1), "live row tiles of a one-row-group tile");
     const uint32_t lane = threadIdx.x % 64u, wave = threadIdx.x / 64u;
     const uint32_t wm = wave / WN, wn = wave % WN;
     // copy i moves 16 rows x 64 B: lane -> row block * 16 + lane / 4, LDS position lane % 4
@@ -1085,7 +1098,8 @@ __device__ __forceinline__ void mfma_gemm_ring(const uint16_t* __restrict__ a, u
     uint32_t dst[PER];
     unroll<PER>([&](auto ic) {
         constexpr int i = ic;
-        const uint32_t block = (i < CA ? i : i - CA) * WAVES + wave;
+        const uint32_t spread = (i < CA ? i : i - CA) * WAVES + wave;
+        const uint32_t block = i < CA && spread >= uint32_t(A_BLOCKS) ? uint32_t(A_BLOCKS - 1) : spread;
         const uint32_t row = block * 16u + lane / 4u;
         const uint32_t chunk = (lane % 4u) ^ wide_swizzle(row);
         if constexpr (i < CA) {
@@ -1098,8 +1112,8 @@ __device__ __forceinline__ void mfma_gemm_ring(const uint16_t* __restrict__ a, u
             dst[i] = BM * 32u + block * 512u;
         }
     });
-    uint32_t oa[TM], ob[TN];
-    unroll<TM>([&](auto t) {
+    uint32_t oa[L], ob[TN];
+    unroll<L>([&](auto t) {
         const uint32_t row = wm * (BM / WM) + t * 16u + lane % 16u;
         oa[t] = row * 32u + (((lane / 16u) ^ wide_swizzle(row)) * 8u);
     });
@@ -1114,14 +1128,21 @@ __device__ __forceinline__ void mfma_gemm_ring(const uint16_t* __restrict__ a, u
         constexpr int i = ic;
         __builtin_amdgcn_global_load_lds((global_void*)(src[i] + k0), (lds_void*)(ring + slot * SLOT + dst[i]), 16, 0, 0);
     };
+    // the copies of live row r (c = r, r + L, ...) and how many there are
+    auto copies_of_row = [&](auto rc, uint32_t slot, uint32_t k0) {
+        unroll<PER>([&](auto cc) {
+            if constexpr (int(cc) % L == int(rc)) copy(cc, slot, k0);
+        });
+    };
+    constexpr auto row_copies = [](int r) { return (PER - r + L - 1) / L; };
     unroll<S - 1>([&](auto st) { unroll<PER>([&](auto i) { copy(i, uint32_t(st), k_of(st)); }); });
     __builtin_amdgcn_s_waitcnt(vmcnt_wait((S - 2) * PER));  // stage 0 landed
     __builtin_amdgcn_s_barrier();
-    bf16x8_t fa[TM], fb[TN];
-    unroll<TM>([&](auto t) { fa[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(ring + oa[t])); });
+    bf16x8_t fa[L], fb[TN];
+    unroll<L>([&](auto t) { fa[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(ring + oa[t])); });
     unroll<TN>([&](auto t) { fb[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(ring + ob[t])); });
-    f32x4_t acc[TM][TN];
-    unroll<TM>([&](auto i) { unroll<TN>([&](auto j) { acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}; }); });
+    f32x4_t acc[L][TN];
+    unroll<L>([&](auto i) { unroll<TN>([&](auto j) { acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}; }); });
     for (uint32_t s = 0; s + 1u < steps; ++s) {
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(vmcnt_wait((S - 3) * PER));  // stage s+1 landed (s+2 .. s+S-2 may be in flight)
@@ -1129,47 +1150,47 @@ __device__ __forceinline__ void mfma_gemm_ring(const uint16_t* __restrict__ a, u
         __builtin_amdgcn_sched_barrier(0);
         const uint16_t* next = ring + ((s + 1u) % S) * SLOT;
         const uint32_t fill = (s + S - 1u) % S, k_fill = k_of(s + S - 1u);
-        unroll<TM - 1>([&](auto ic) {
+        unroll<L - 1>([&](auto ic) {
             constexpr int i = ic;
             unroll<TN>([&](auto jc) {
                 constexpr int j = jc;
                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
-                if constexpr (j == TN / 2 && i < PER) copy(ic, fill, k_fill);
+                if constexpr (j == TN / 2) copies_of_row(ic, fill, k_fill);
             });
             fa[i] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(next + oa[i]));
         });
         unroll<TN>([&](auto jc) {
             constexpr int j = jc;
-            acc[TM - 1][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[TM - 1], acc[TM - 1][j], 0, 0, 0);
-            if constexpr (j == TN / 2 && TM - 1 < PER) copy(std::integral_constant<int, TM - 1>{}, fill, k_fill);
+            acc[L - 1][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[L - 1], acc[L - 1][j], 0, 0, 0);
+            if constexpr (j == TN / 2) copies_of_row(std::integral_constant<int, L - 1>{}, fill, k_fill);
             fb[j] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(next + ob[j]));
         });
-        fa[TM - 1] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(next + oa[TM - 1]));
-        // issue order: per row, half its MFMAs, its copy, the rest, one fragment read
-        unroll<TM - 1>([&](auto ic) {
+        fa[L - 1] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(next + oa[L - 1]));
+        // issue order: per row, half its MFMAs, its copies, the rest, one fragment read
+        unroll<L - 1>([&](auto ic) {
             __builtin_amdgcn_sched_group_barrier(0x008, TN / 2 + 1, 0);
-            if constexpr (int(ic) < PER) {
-                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            if constexpr (row_copies(int(ic)) > 0) {
+                __builtin_amdgcn_sched_group_barrier(0x020, row_copies(int(ic)), 0);
             }
             __builtin_amdgcn_sched_group_barrier(0x008, TN - TN / 2 - 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         });
         unroll<TN>([&](auto jc) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            if constexpr (int(jc) == TN / 2 && TM - 1 < PER) {
-                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            if constexpr (int(jc) == TN / 2 && row_copies(L - 1) > 0) {
+                __builtin_amdgcn_sched_group_barrier(0x020, row_copies(L - 1), 0);
             }
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         });
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
-    unroll<TM>([&](auto i) {
+    unroll<L>([&](auto i) {
         unroll<TN>([&](auto j) { acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0); });
     });
     __builtin_amdgcn_s_waitcnt(vmcnt_wait(0));  // re-copies of the last stage land before the workgroup ends
     // lane holds row lane % 16 and columns 4 (lane / 16) .. + 3 of each 16 x 16 tile
     const bool vector_rows = (ldc & 3u) == 0;
-    unroll<TM>([&](auto i) {
+    unroll<L>([&](auto i) {
         const uint32_t gm = m0 + wm * (BM / WM) + i * 16u + lane % 16u;
         if (gm < m_total) {
             T* row = c + (c_rows ? size_t(c_rows[gm]) : size_t(gm)) * ldc;
@@ -1203,7 +1224,8 @@ __device__ __forceinline__ void mfma_gemm_wide(const uint16_t* __restrict__ a, u
                                                uint32_t m_total, uint32_t n_total, uint32_t k_total,
                                                const int32_t* __restrict__ a_rows, const int32_t* __restrict__ c_rows, uint32_t m0,
                                                uint32_t n0) {
-    mfma_gemm_ring<T, kWideM, kWideN, 2, 2, 5>(a, lda, b, ldb, bias, c, ldc, m_total, n_total, k_total, a_rows, c_rows, m0, n0);
+    __shared__ __attribute__((aligned(1024))) uint16_t ring[ring_elements<kWideM, kWideN, 5>()];
+    mfma_gemm_ring<T, kWideM, kWideN, 2, 2, 5>(a, lda, b, ldb, bias, c, ldc, m_total, n_total, k_total, a_rows, c_rows, m0, n0, 1u, ring);
 }
 
 template <class T, bool B_K_CONTIGUOUS>
@@ -1495,13 +1517,37 @@ __device__ __forceinline__ void narrow_linear(const T* __restrict__ x, const T* 
 // Expert-grouped mixture-of-experts products.
 //
 // ``route_slots`` (one workgroup) turns the [tokens x selected] expert ids into a slot permutation grouped
-// by expert and a table of 128-slot tiles; ids are checked like every gather (negative ids wrap, an id
+// by expert and a table of row tiles; ids are checked like every gather (negative ids wrap, an id
 // outside [-experts, experts) raises the error word and counts as expert 0). Layout of ``scratch``
 // (int32): [0, E) per-expert counts, [E, 2E+1) offsets, [2E+1] tile count, then ``slots`` permutation
-// entries, then the tile table as (expert, first row) pairs.
+// entries, then the tile table as (expert, first row) pairs, ``expert_tile_bound`` of them; then a second
+// table, [tile count, (expert, first row) pairs], for taller last tiles. An expert's tiles hold 128 slots
+// each while more than ``last`` of its slots remain, then one tile takes the rest: the first table has
+// ``last`` = 128 (ceil(count / 128) tiles), the second 160 (a remainder of at most 32 slots rides on the
+// expert's last full tile, a 160-slot tile, instead of costing a whole tile of its own).
 // ``grouped_expert_linear`` then computes, for every tile, Y[slot, :] = W[e] . X[row(slot)]^T on the
 // matrix cores: each expert's [C, K] slab is read once per tile instead of once per slot. Every output
 // row is an independent dot product, so the order of slots inside a group changes no result bit.
+constexpr uint32_t kTallLastTile = 160;
+
+// Tiles a table can hold: ceil(slots / 128) + experts covers every rule above.
+__host__ __device__ constexpr uint32_t expert_tile_bound(uint32_t slots, uint32_t experts) { return (slots + 127u) / 128u + experts; }
+
+// The tile count word of the table for ``last`` (its (expert, first row) pairs follow it, except in the
+// first table, whose pairs follow the permutation).
+__device__ __forceinline__ uint32_t expert_table_word(uint32_t slots, uint32_t experts, uint32_t last) {
+    return last == 128u ? 2u * experts + 1u : 2u * experts + 2u + slots + 2u * expert_tile_bound(slots, experts);
+}
+
+__device__ __forceinline__ uint32_t expert_row_tiles(uint32_t count, uint32_t last) {
+    return count == 0u ? 0u : 1u + (count > last ? (count - last + 127u) / 128u : 0u);
+}
+
+// Slots in the tile of an expert with ``count`` slots that starts at slot ``first`` (a multiple of 128).
+__device__ __forceinline__ uint32_t expert_tile_rows(uint32_t count, uint32_t first, uint32_t last) {
+    return count - first <= last ? count - first : 128u;
+}
+
 __device__ __forceinline__ void route_slots(const int64_t* __restrict__ indices, uint32_t slots, uint32_t experts,
                                             int32_t* __restrict__ scratch, unsigned int* error) {
     extern __shared__ int32_t shared_counts[];
@@ -1520,20 +1566,29 @@ __device__ __forceinline__ void route_slots(const int64_t* __restrict__ indices,
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        int32_t running = 0, tile = 0;
+        int32_t* tall_count = scratch + expert_table_word(slots, experts, kTallLastTile);
+        int32_t* tall = tall_count + 1;
+        int32_t running = 0, tile = 0, tall_tile = 0;
         for (uint32_t e = 0; e < experts; ++e) {
             const int32_t count = shared_counts[e];
             counts[e] = count;
             offsets[e] = running;
-            for (int32_t first = 0; first < count; first += 128) {
+            const uint32_t n = expert_row_tiles(uint32_t(count), 128u), m = expert_row_tiles(uint32_t(count), kTallLastTile);
+            for (uint32_t t = 0; t < n; ++t) {
                 tiles[2 * tile] = int32_t(e);
-                tiles[2 * tile + 1] = first;
+                tiles[2 * tile + 1] = int32_t(128u * t);
                 ++tile;
+                if (t < m) {
+                    tall[2 * tall_tile] = int32_t(e);
+                    tall[2 * tall_tile + 1] = int32_t(128u * t);
+                    ++tall_tile;
+                }
             }
             running += count;
         }
         offsets[experts] = running;
         *tile_count = tile;
+        *tall_count = tall_tile;
     }
     __syncthreads();
     for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) {
@@ -1552,17 +1607,18 @@ __device__ __forceinline__ void route_slots(const int64_t* __restrict__ indices,
 // tile with that expert's row tiles adjacent, so the row tiles that share a slab of W[e] run together and
 // an XCD's run of logical tiles reads each slab once. Expert e owns logical tiles
 // [gx * first_e, gx * (first_e + n_e)), n_e = ceil(count_e / 128) row tiles starting at tile first_e of the
-// routing table. Every wave finds (row tile, column tile) of ``logical`` with a wave-wide scan of the
-// per-expert counts; ``logical`` < gx * (tile count) always has one.
+// routing table (n_e by ``expert_row_tiles`` with the routing's ``last``). Every wave finds (row tile,
+// column tile) of ``logical`` with a wave-wide scan of the per-expert counts; ``logical`` < gx * (tile
+// count) always has one.
 __device__ __forceinline__ void expert_tile_of(const int32_t* __restrict__ counts, uint32_t experts, uint32_t gx,
-                                               uint32_t logical, uint32_t& tile, uint32_t& column) {
+                                               uint32_t logical, uint32_t& tile, uint32_t& column, uint32_t last) {
     const uint32_t lane = threadIdx.x % kWave;
     uint32_t carry = 0;
     tile = 0;
     column = 0;
     for (uint32_t e0 = 0; e0 < experts; e0 += kWave) {
         const uint32_t e = e0 + lane;
-        const uint32_t n = e < experts ? (uint32_t(counts[e]) + 127u) / 128u : 0u;
+        const uint32_t n = e < experts ? expert_row_tiles(uint32_t(counts[e]), last) : 0u;
         uint32_t inclusive = n;
 #pragma unroll
         for (int d = 1; d < kWave; d <<= 1) {
@@ -1588,33 +1644,38 @@ __device__ __forceinline__ void expert_tile_of(const int32_t* __restrict__ count
 // product. One-dimensional launch of 8 * ceil(ceil(C / 128) * max tiles / 8) workgroups, mapped to tiles
 // in the expert-major, XCD-aware order above; workgroups past gx * (tile count) return at once.
 // PATH 3 is the ring body on 128-slot x BN-channel tiles on RWM x RWN waves (64 RWM RWN threads; bfloat16,
-// K % 32 = 0, ``channels`` a multiple of BN); the other paths take 128 x 128 tiles.
+// K % 32 = 0, ``channels`` a multiple of BN), and on LAST-slot tiles (LAST = 160, RWM = 1: 10 row blocks of
+// 16) for an expert's last tile when the routing was built with ``last`` = LAST; the two bodies share the
+// kernel's one LDS array. The other paths take 128 x 128 tiles (LAST = 128).
 
-template <int BN>
+template <int BN, int LAST = 128>
 constexpr int ring_expert_slots() {
-    return (128 + BN) * 64 * 5 <= 150 * 1024 ? 5 : 4;
+    return (LAST + BN) * 64 * 5 <= 150 * 1024 ? 5 : 4;
 }
 
-template <class T, bool PER_SLOT, int PATH = 0, int BN = 128, int RWM = 1, int RWN = 4, int RS = ring_expert_slots<BN>()>
+template <class T, bool PER_SLOT, int PATH = 0, int BN = 128, int RWM = 1, int RWN = 4, int LAST = 128,
+          int RS = ring_expert_slots<BN, LAST>()>
 __device__ __forceinline__ void grouped_expert_linear(const T* __restrict__ w, const T* __restrict__ x, T* __restrict__ out,
                                                       const int32_t* __restrict__ scratch, uint32_t slots, uint32_t selected,
                                                       uint32_t experts, uint32_t channels, uint32_t inner) {
     static_assert(PATH == 3 || BN == 128, "only the ring path takes wider channel tiles");
+    static_assert(LAST == 128 || (PATH == 3 && LAST == int(kTallLastTile) && RWM == 1), "taller last tiles on the ring path only");
     const int32_t* offsets = scratch + experts;
-    const uint32_t tile_count = uint32_t(scratch[2 * experts + 1]);
+    const uint32_t table = expert_table_word(slots, experts, LAST);
+    const uint32_t tile_count = uint32_t(scratch[table]);
     const int32_t* permutation = scratch + 2 * experts + 2;
-    const int32_t* tiles = permutation + slots;
+    const int32_t* tiles = LAST == 128 ? permutation + slots : scratch + table + 1;
     const uint32_t gx = (channels + BN - 1u) / BN;
     uint32_t logical;
     if (!xcd_logical_tile(gx * tile_count, logical)) {
         return;
     }
     uint32_t tile, column;
-    expert_tile_of(scratch, experts, gx, logical, tile, column);
+    expert_tile_of(scratch, experts, gx, logical, tile, column, LAST);
     const uint32_t expert = uint32_t(tiles[2 * tile]);
     const uint32_t first = uint32_t(tiles[2 * tile + 1]);
     const uint32_t count = uint32_t(offsets[expert + 1] - offsets[expert]);
-    const uint32_t rows = count - first < 128u ? count - first : 128u;
+    const uint32_t rows = expert_tile_rows(count, first, LAST);
     if constexpr (PATH == 3) {
         // the tile's slots are read straight from the permutation in global memory (the A row of a slot is
         // slot / selected for per-token inputs): the ring is then the kernel's only LDS array, and the
@@ -1622,9 +1683,34 @@ __device__ __forceinline__ void grouped_expert_linear(const T* __restrict__ w, c
         // it made every fragment read wait for all outstanding copies, which serialised the pipeline)
         static_assert(sizeof(T) == 2, "the ring body takes bfloat16");
         const int32_t* slots_of_tile = permutation + offsets[expert] + first;
-        mfma_gemm_ring<T, 128, BN, RWM, RWN, RS>(
-            x, inner, w + size_t(expert) * channels * inner, inner, nullptr, out, channels, rows, channels, inner, slots_of_tile,
-            slots_of_tile, 0u, column * BN, PER_SLOT ? 1u : selected);
+        __shared__ __attribute__((aligned(1024))) uint16_t ring[ring_elements<LAST, BN, RS>()];
+        const T* slab = w + size_t(expert) * channels * inner;
+        // the body for the tile's live 16-row blocks: 1, 2, 4 or 8 of a 128-slot tile, all of a taller last tile
+        auto body = [&](auto bm, auto live) {
+            mfma_gemm_ring<T, int(bm), BN, RWM, RWN, RS, int(live)>(x, inner, slab, inner, nullptr, out, channels, rows, channels, inner,
+                                                                     slots_of_tile, slots_of_tile, 0u, column * BN,
+                                                                     PER_SLOT ? 1u : selected, ring);
+        };
+        using I = std::integral_constant<int, 128>;
+        if constexpr (LAST > 128) {
+            if (rows > 128u) {
+                body(std::integral_constant<int, LAST>{}, std::integral_constant<int, LAST / 16>{});
+                return;
+            }
+        }
+        if constexpr (RWM == 1) {
+            if (rows <= 16u) {
+                body(I{}, std::integral_constant<int, 1>{});
+            } else if (rows <= 32u) {
+                body(I{}, std::integral_constant<int, 2>{});
+            } else if (rows <= 64u) {
+                body(I{}, std::integral_constant<int, 4>{});
+            } else {
+                body(I{}, std::integral_constant<int, 8>{});
+            }
+        } else {
+            body(I{}, std::integral_constant<int, 128 / RWM / 16>{});
+        }
     } else {
         __shared__ int32_t a_rows[128], c_rows[128];
         for (uint32_t r = threadIdx.x; r < 128u; r += blockDim.x) {

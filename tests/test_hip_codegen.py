@@ -250,6 +250,29 @@ def test_decode_attention_is_two_launches_with_tickets_inside_the_error_region()
     assert "chroma_attention_decode" not in wide.files["model.hip"]
 
 
+class GroupedExperts(torch.nn.Module):
+    def forward(self, weights, indices, x, per_slot):
+        selected = weights[indices]
+        return torch.einsum("beck,bk->bec", selected, x), torch.einsum("beck,bek->bec", selected, per_slot)
+
+
+def test_expert_ring_bodies_cross_compile_with_tall_last_tiles(tmp_path):
+    """Every ring tile width builds for gfx950 with its bodies in one kernel (the live-row variants of the
+    128-slot tile, and the 160-slot last tile where its rule takes it), and both products of a layer share
+    one routing."""
+    from chroma_amd._src.codegen.hip import RING_EXPERT_TILES
+
+    for width, waves, last in RING_EXPERT_TILES:
+        experts, tokens, selected, inner = 4, 160, 2, 64
+        inputs = (torch.randn(experts, width, inner).to(torch.bfloat16), torch.randint(0, experts, (tokens, selected)),
+                  torch.randn(tokens, inner).to(torch.bfloat16), torch.randn(tokens, selected, inner).to(torch.bfloat16))
+        generated = lower(GroupedExperts(), *inputs)
+        source = generated.files["model.hip"]
+        assert source.count(f", 3, {width}, 1, {waves}, {last}>(") == 2
+        assert source.count("chroma::route_slots(") == 1
+        build(generated, tmp_path / f"ring{width}", load=False)
+
+
 OPERATIONS_SOURCE = """
 def fn(x, y, ids):
     selected = x[ids]

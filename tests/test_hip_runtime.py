@@ -20,6 +20,7 @@ import torch
 
 import chroma_amd
 from chroma_amd import Decoder, Program
+from chroma_amd._src.codegen.hip import RING_EXPERT_TILES
 from chroma_amd._src.dtypes import BFLOAT16
 from oracle import compile_cpu
 from tests.helpers import Function, as_float, assert_close, export, leaves, numpy_of, random_transformer, small_config
@@ -339,10 +340,12 @@ def test_grouped_expert_products(tmp_path, dtype, experts):
         compare(model(*inputs), oracle(*[numpy_of(v) for v in inputs]))
 
 
-@pytest.mark.parametrize("channels, inner", [(768, 96), (640, 320), (384, 64)])
+@pytest.mark.parametrize("channels, inner", [(768, 96), (640, 320), (1152, 64), (384, 64)])
 def test_grouped_expert_products_ring_body(tmp_path, channels, inner):
-    """bfloat16 expert products whose channel count is a multiple of 384 or 320 take the ring body on
-    128-slot tiles: 6 experts with ~133 slots each (a full and a ragged tile per expert), two channel
+    """bfloat16 expert products whose channel count is a multiple of 384 or 320 take the ring body: 6
+    experts whose slot counts give every tile kind of both routing tables (300: two full tiles and a
+    44-slot one; 280: a full tile and a 152-slot last tile, or two; 160, 150 and 130: one tall tile, or a
+    full one and a 2-32-slot one; 60: a 64-row tile), so every live-row body runs; one to three channel
     tiles, K of 2-10 32-deep stages (fewer than the ring's slots included); per-token and per-slot inputs,
     against the oracle."""
 
@@ -352,9 +355,15 @@ def test_grouped_expert_products_ring_body(tmp_path, channels, inner):
             return torch.einsum("beck,bk->bec", selected, x), torch.einsum("beck,bek->bec", selected, per_slot)
 
     generator = torch.Generator().manual_seed(4)
-    experts, tokens, selected = 6, 200, 4
+    experts, tokens, selected = 6, 360, 3
+    counts = [300, 280, 160, 150, 130, 60]
+    # expert runs laid over (slot, token) in token-fastest order: a run of <= tokens ids meets each token once
+    order = torch.cat([torch.full((count,), e, dtype=torch.int64) for e, count in enumerate(counts)])
+    indices = order.reshape(selected, tokens).t().contiguous()
+    indices = torch.stack([row[torch.randperm(selected, generator=generator)] for row in indices])
+    assert torch.bincount(indices.flatten(), minlength=experts).tolist() == counts
+    assert all(len(set(row.tolist())) == selected for row in indices)
     weights = (torch.randn(experts, channels, inner, generator=generator) * 0.2).to(torch.bfloat16)
-    indices = torch.stack([torch.randperm(experts, generator=generator)[:selected] for _ in range(tokens)])
     x = torch.randn(tokens, inner, generator=generator).to(torch.bfloat16)
     per_slot = torch.randn(tokens, selected, inner, generator=generator).to(torch.bfloat16)
     inputs = (weights, indices, x, per_slot)
@@ -363,7 +372,9 @@ def test_grouped_expert_products_ring_body(tmp_path, channels, inner):
     with chroma_amd.compile(exported, tmp_path / "hip") as model:
         assert model.stats["expert_contractions"] == 2 and model.stats["mfma_matmuls"] == 2
         source = (tmp_path / "hip" / "model.hip").read_text()
-        assert source.count(", 3, 384, 1, 8>(") + source.count(", 3, 320, 1, 4>(") == 2, "the ring path was not taken"
+        width, waves, last = next(tile for tile in RING_EXPERT_TILES if channels % tile[0] == 0)
+        assert source.count(f", 3, {width}, 1, {waves}, {last}>(") == 2, "the ring path was not taken"
+        assert source.count("chroma::route_slots(") == 1, "both products share one routing"
         compare(model(*inputs), oracle(*[numpy_of(v) for v in inputs]))
 
 
