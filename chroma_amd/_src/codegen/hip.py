@@ -88,6 +88,9 @@ WIDE_GEMM_MIN_TILES = 200
 # rounds of the chip's 256, now with longer tiles among them), on 192 x 4 waves with 160 236 us, but 276 us
 # against 241 us on the skewed routing the seeded C5 model produces (expert counts 0-1842 at layer 19).
 RING_EXPERT_TILES = ((384, 8, 160), (320, 4, 128))
+# A gated activation between two expert products is computed in the first product's epilogue (no map
+# launch; the first product is not stored when nothing else reads it). False keeps the separate launch.
+ACTIVATION_EPILOGUES = True
 REUSED_EVALUATIONS = 1 << 18  # a contraction operand is stored when (elements x reuse) reaches this
 SMALL_REDUCTION = 8  # contractions summing at most this many products are fused expressions...
 SMALL_OPERAND_COST = 8  # ...over operands that cost at most this much per element (others are stored)
@@ -144,6 +147,7 @@ class Launch:
     block: int
     bindings: List[Binding]
     shared: int = 0
+    buffers: List[str] = field(default_factory=list)  # the buffers behind ``bindings``
 
 
 def _align(value: int) -> int:
@@ -152,6 +156,10 @@ def _align(value: int) -> int:
 
 def _shape(value_shape: Sequence[int]) -> Tuple[int, ...]:
     return tuple(value_shape) if value_shape else (1,)
+
+
+class _NotFusible(Exception):
+    """An epilogue fusion does not apply to this expression (the plain launches are kept)."""
 
 
 class HIPCodegen(Codegen):
@@ -198,6 +206,15 @@ class HIPCodegen(Codegen):
         self.write_through_stores: Set[str] = set()  # buffers written by the first kernel that stages them
         self.folded_norms = 0
         self.fused_routers = 0
+        # Gated activations computed in the epilogue of the expert product they read: the last grouped ring
+        # launch (to re-emit with an epilogue), the activations' stored copies (expression -> buffer), and
+        # per fused launch (launch index, product buffer, the variant that does not store the product),
+        # swapped in at the end when nothing else reads the product.
+        self.last_grouped: Optional[dict] = None
+        self.epilogue_values: Dict[str, Value] = {}
+        self.product_stores: List[Tuple[int, str, Kernel, Tuple[int, int, int], int]] = []
+        self.expert_epilogues = 0
+        self.unstored_products = 0
 
     # ===================================================================================== storage
     def extern(self, tensor: torch.Tensor, kind: str, offset: int) -> Value:
@@ -249,12 +266,18 @@ class HIPCodegen(Codegen):
         staged = k.staged_values.get(value.name)
         if staged is not None:
             return ("lds", staged, Kernel.flatten(coords, _shape(value.shape)) if value.shape else ZERO)
+        stored_copy = self.epilogue_values.get(value.name)
+        if stored_copy is not None:
+            return self.read(k, stored_copy, coords)
         if value.stored:
             root, view = value.root, value.view
             address = Aff((), view.offset)
             for coord, stride, size in zip(coords, view.strides, value.shape):
                 if size != 1 and stride:
                     address = address + coord.scale(stride)
+            hook = k.register_reads.get(root.name)
+            if hook is not None:
+                return hook(address)
             if root.name in k.staged_values:
                 return ("lds", k.staged_values[root.name], address)
             expression = k.unstored.get(root.name)
@@ -271,7 +294,8 @@ class HIPCodegen(Codegen):
         return node
 
     def read_flat(self, k: Kernel, value: Value, flat: Aff) -> tuple:
-        if value.stored and value.view.base is None and value.name not in k.unstored and value.name not in k.staged_values:
+        if (value.stored and value.view.base is None and value.name not in k.unstored and value.name not in k.staged_values
+                and value.name not in k.register_reads):
             return ("ld", k.slot(value.name, value.dtype, extent=self.extents[value.name]), value.dtype, flat)
         return self.read(k, value, k.unflatten(flat, value.shape))
 
@@ -482,7 +506,7 @@ class HIPCodegen(Codegen):
                 allocation.start = min(allocation.start, self.kernels)
                 allocation.end = max(allocation.end, self.kernels)
         self.record_usage(inputs)
-        self.launches.append(Launch(name, grid3, block, bindings, shared))
+        self.launches.append(Launch(name, grid3, block, bindings, shared, list(k.slots)))
         if k.resolved_stores:
             self.resolved_by_launch[len(self.launches) - 1] = list(k.resolved_stores)
         self.kernels += 1
@@ -2533,6 +2557,8 @@ class HIPCodegen(Codegen):
             self.launch(k, (blocks_per_slot, tokens * selected, 1), threads, [weight, indices, x], kind="expert_stream")
             self.expert_contractions += 1
             return out
+        if per_slot and not x.stored:
+            x = self._activation_epilogue(x) or x
         x = self.contiguous(x)
         if tokens * selected >= GROUPED_SLOTS and inner % (8 if meta.dtype == torch.bfloat16 else 4) == 0 and experts <= 4096:
             self._grouped_experts(out, weight, indices, x, tokens, selected, experts, channels, inner, per_slot)
@@ -2688,6 +2714,17 @@ class HIPCodegen(Codegen):
         return self.routes[key], tiles
 
     def _grouped_experts(self, out, weight, indices, x, tokens, selected, experts, channels, inner, per_slot) -> None:
+        args = (out, weight, indices, x, tokens, selected, experts, channels, inner, per_slot)
+        k, grid, threads, path, scratch = self._grouped_kernel(*args)
+        self.launch(k, grid, threads, [weight, x, scratch], kind="experts_mfma")
+        self.mfma_matmuls += 1
+        self.last_grouped = {"index": len(self.launches) - 1, "args": args, "path": path, "scratch": scratch}
+
+    def _grouped_kernel(self, out, weight, indices, x, tokens, selected, experts, channels, inner, per_slot, activation=None,
+                        store_product: bool = True):
+        """The grouped expert product's kernel, grid, threads, body path and routing; with ``activation``
+        = (value, buffer) the ring body's epilogue writes ``value`` (which reads this product's output)
+        into ``buffer``, and the product too unless ``store_product`` is false (``_activation_epilogue``)."""
         path, threads, width, waves, last = 1, 256, 128, 4, 128
         ring = next(((n, w, t) for n, w, t in RING_EXPERT_TILES if channels % n == 0), None)
         if out.dtype == torch.bfloat16 and inner % 32 == 0 and ring is not None:
@@ -2703,13 +2740,123 @@ class HIPCodegen(Codegen):
             k.min_waves = DIRECT_GEMM_BLOCKS
         w, xs = self._matrix_slot(k, weight), self._matrix_slot(k, x)
         table = k.slot(scratch.name, torch.int64, extent=self.extents[scratch.name])
-        out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        if activation is None:
+            destination, epilogue = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name]), ""
+        else:
+            assert path == 3, "activation epilogues take the ring body"
+            self._emit_activation_epilogue(k, out, indices, *activation, tokens, selected, channels, store_product)
+            destination, epilogue = f"static_cast<{ctype_of(out.dtype)}*>(nullptr)", ", epilogue"
         k.line(
             f"chroma::grouped_expert_linear<{ctype_of(out.dtype)}, {str(per_slot).lower()}, {path}, {width}, 1, {waves}, {last}>({w}, {xs}, "
-            f"{out_slot}, reinterpret_cast<const int32_t*>({table}), {tokens * selected}u, {selected}u, {experts}u, {channels}u, {inner}u);"
+            f"{destination}, reinterpret_cast<const int32_t*>({table}), {tokens * selected}u, {selected}u, {experts}u, {channels}u, "
+            f"{inner}u{epilogue});"
         )
-        self.launch(k, 8 * -(-(-(-channels // width) * tiles) // 8), threads, [weight, x, scratch], kind="experts_mfma")
-        self.mfma_matmuls += 1
+        return k, 8 * -(-(-(-channels // width) * tiles) // 8), threads, path, scratch
+
+    def _emit_activation_epilogue(self, k: Kernel, product: Value, indices: Value, value: Value, buffer: Value, tokens: int,
+                                  selected: int, channels: int, store_product: bool) -> None:
+        """The lambda the ring body calls per (slot, 4 consecutive channels c .. c + 3) of ``product``
+        [tokens, selected, channels]: it rounds the four sums as the product's store would (and stores
+        them when ``store_product``), then evaluates ``value`` [tokens, selected, channels / 2] at channels
+        c / 2 and c / 2 + 1 (a gated activation reads channels 2i and 2i + 1 of the product for its channel
+        i) and writes both to ``buffer``. The expression is the one a map kernel would evaluate, with every
+        read of the product replaced by the lane's rounded sums, and the slot's own expert id (a gather of
+        the experts' biases) by the tile's expert, which every slot of the tile is routed to (an id outside
+        the experts has already raised the error word in the routing); a read of any other product element
+        raises ``_NotFusible``."""
+        half = channels // 2
+        slot = k.slot(buffer.name, buffer.dtype, writable=True, extent=self.extents[buffer.name])
+        with k.block("auto epilogue = [&](uint32_t slot, uint32_t column, const float* sums, uint32_t expert) {", "};"):
+            k.line("uint16_t bits[4];")
+            k.line("float u[4];")
+            k.line("for (int r = 0; r < 4; ++r) {")
+            k.line("    bits[r] = chroma::f32_to_bf16(sums[r]);")
+            k.line("    u[r] = chroma::bf16_to_f32(bits[r]);  // the product as stored")
+            k.line("}")
+            b = Aff.of(k.atom(f"slot / {selected}u", tokens - 1, prefix="t"))
+            e = Aff.of(k.atom(f"slot % {selected}u", selected - 1, prefix="t"))
+            h = k.atom("column / 2u", half - 2, prefix="h")
+            row = b.scale(selected * channels) + e.scale(channels)
+            if store_product:
+                target = k.slot(product.root.name, product.dtype, writable=True, extent=self.extents[product.root.name])
+                at = row + Aff.of(h, 2) + product.view.offset
+                k.check_bounds(target, at + 3)
+                k.line(f"*reinterpret_cast<uint2*>({target} + {at.code()}) = uint2{{uint32_t(bits[0]) | (uint32_t(bits[1]) << 16), "
+                       "uint32_t(bits[2]) | (uint32_t(bits[3]) << 16)};")
+
+            def lane_value(address: Aff) -> tuple:
+                rest = address.without(h)
+                if address.coefficient(h) != 2 or Aff(rest.terms) != row or not 0 <= rest.const < 4:
+                    raise _NotFusible(f"the activation reads {product.name}[{address.code()}] outside the lane's four channels")
+                return ("lds", "u", Aff((), rest.const))
+
+            slot_id = b.scale(selected) + e + indices.view.offset
+
+            def tile_expert(address: Aff) -> tuple:
+                if address != slot_id:
+                    raise _NotFusible(f"the activation reads {indices.name}[{address.code()}], not its slot's expert id")
+                return ("reg", torch.int64, "int64_t(expert)")
+
+            k.register_reads[product.root.name] = lane_value
+            k.register_reads[indices.root.name] = tile_expert
+            try:
+                names = [k.emit(self.read(k, value, [b, e, Aff.of(h) + p])) for p in (0, 1)]
+            finally:
+                del k.register_reads[product.root.name]
+                del k.register_reads[indices.root.name]
+            at = b.scale(selected * half) + e.scale(half) + Aff.of(h)
+            k.check_bounds(slot, at + 1)
+            k.line(f"*reinterpret_cast<uint32_t*>({slot} + {at.code()}) = uint32_t(chroma::f32_to_bf16({names[0]})) | "
+                   f"(uint32_t(chroma::f32_to_bf16({names[1]})) << 16);")
+
+    def _activation_epilogue(self, x: Value) -> Optional[Value]:
+        """Store the per-slot operand ``x`` of a second expert product from the epilogue of the first when
+        ``x`` is an elementwise expression of that product's output (the gated activation) and the first
+        product is the last launch, on the ring body, with ``x`` taking channels 2i and 2i + 1 for its
+        channel i (bfloat16). The first product's launch is re-emitted with the epilogue, its output is
+        never written (any other read of it fails the compile), and ``x``'s readers read the stored copy.
+        Removes the activation's map launch and the round trip of the product through HBM."""
+        last = self.last_grouped
+        if not ACTIVATION_EPILOGUES or last is None or last["index"] != len(self.launches) - 1 or last["path"] != 3:
+            return None
+        out, weight, indices, xin, tokens, selected, experts, channels, inner, per_slot = last["args"]
+        if (out.name not in self.sources.get(x.name, ()) or x.dtype != torch.bfloat16 or out.dtype != torch.bfloat16
+                or tuple(x.shape) != (tokens, selected, channels // 2) or channels % 4):
+            return None
+        buffer = self.allocate(tuple(x.shape), x.dtype)
+        try:
+            k, grid, threads, _, scratch = self._grouped_kernel(*last["args"], activation=(x, buffer))
+            lean, *_ = self._grouped_kernel(*last["args"], activation=(x, buffer), store_product=False)
+        except _NotFusible:
+            return None
+        self._retract_last_launch()
+        self.launch(k, grid, threads, [weight, xin, scratch, x], kind="experts_mfma")
+        self.product_stores.append((len(self.launches) - 1, out.root.name, lean, self.launches[-1].grid, threads))
+        self.epilogue_values[x.name] = buffer
+        self.materialized[x.name] = buffer
+        self.last_grouped = None
+        self.expert_epilogues += 1
+        return buffer
+
+    def _drop_unread_product_stores(self) -> None:
+        """After lowering: a fused expert launch whose product no later launch binds and no output holds
+        takes the variant that does not store the product."""
+        for index, product, lean, grid, threads in self.product_stores:
+            if product in self.output_buffers or any(product in launch.buffers for launch in self.launches[index + 1 :]):
+                continue
+            source = lean.render("KERNEL_NAME", threads)
+            name = self.kernel_names.get(source)
+            if name is None:
+                name = f"chroma_experts_mfma_{hashlib.sha256(source.encode()).hexdigest()[:8]}"
+                self.kernel_names[source] = name
+                self.kernel_sources.append(source.replace("KERNEL_NAME", name, 1))
+            old = self.launches[index]
+            self.launches[index] = Launch(name, grid, threads, [self.binding_of(buffer) for buffer in lean.slots], old.shared, list(lean.slots))
+            if all(launch.kernel != old.kernel for launch in self.launches):
+                text = next(src for src, kernel in self.kernel_names.items() if kernel == old.kernel)
+                del self.kernel_names[text]
+                self.kernel_sources = [text for text in self.kernel_sources if f" {old.kernel}(" not in text]
+            self.unstored_products += 1
 
     def _loop_einsum(self, meta, labels, output, sizes, reduction, values) -> Value:
         out = self.allocate(tuple(meta.shape), meta.dtype)
@@ -2763,6 +2910,7 @@ class HIPCodegen(Codegen):
 
     # ================================================================================== finish
     def generate(self, inputs: List[TensorSpec], outputs: List[TensorSpec], stats: Stats) -> GeneratedCode:
+        self._drop_unread_product_stores()
         weights_size = len(self.weights)
         workspace_base = _align(weights_size)
         error_base = workspace_base + _align(stats["workspace_bytes"])
@@ -2819,6 +2967,8 @@ class HIPCodegen(Codegen):
             fused_attentions=self.fused_attentions,
             fused_routers=self.fused_routers,
             routed_experts=self.routed_experts,
+            expert_epilogues=self.expert_epilogues,
+            unstored_products=self.unstored_products,
             small_contractions=self.small_contractions,
             attention_epilogues=self.attention_epilogues,
             write_through_stores=len(self.write_through_stores),

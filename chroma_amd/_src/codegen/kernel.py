@@ -129,6 +129,7 @@ def is_int(dtype: torch.dtype) -> bool:
 # Expression nodes are tuples (hash-consed through the kernel's memo):
 #   ("ld", slot, dtype, aff)   ("f", value)   ("i", value)   ("un", op, x)   ("bin", op, x, y)
 #   ("rnd", x)   ("sel", cond, x, y)   ("cmp", op, aff_a, aff_b, constant)   ("cases", tests, parts)
+#   ("reg", dtype, code): a value the surrounding code already holds (C expression ``code``)
 Node = tuple
 
 UNARY_CODE = {
@@ -205,6 +206,9 @@ class Kernel:
         # Values whose elements this kernel has evaluated into a __shared__ float array (value -> array),
         # in row-major order; reads of them become LDS reads ("lds" nodes).
         self.staged_values: Dict[str, str] = {}
+        # Stored buffers whose reads resolve to nodes the kernel already holds (buffer -> address -> node),
+        # e.g. an epilogue reading the product it is storing.
+        self.register_reads: Dict[str, object] = {}
 
     # -- parameters ------------------------------------------------------------------------------
     def slot(self, buffer: str, dtype: torch.dtype, writable: bool = False, extent: Optional[int] = None) -> str:
@@ -366,6 +370,8 @@ class Kernel:
             return is_int(node[2])
         if tag == "i":
             return True
+        if tag == "reg":
+            return is_int(node[1])
         if tag == "sel":
             return Kernel.node_is_int(node[2])
         if tag == "cases":
@@ -388,6 +394,8 @@ class Kernel:
             result: Union[str, List[str]] = float_literal(node[1])
         elif tag == "i":
             result = f"int64_t({int(node[1])}ll)"
+        elif tag == "reg":
+            result = node[2]
         elif tag == "ld":
             result = self._emit_load(node)
         elif tag == "lds":

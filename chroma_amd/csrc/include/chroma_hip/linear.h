@@ -1073,12 +1073,18 @@ constexpr int ring_elements() {
     return S * (BM + BN) * 32;
 }
 
-template <class T, int BM, int BN, int WM, int WN, int S, int L = BM / WM / 16>
+//
+// With an ``epilogue`` (any callable but nullptr) the tile stores nothing itself: for every output row gm of
+// the tile (c_rows[gm], or gm) and every 4 consecutive columns n .. n + 3 a lane holds, it calls
+// epilogue(row, n, v, tag) with v[r] the float value the plain store would round to bfloat16 (acc + bias)
+// and ``tag`` the caller's (the grouped expert products pass the tile's expert).
+template <class T, int BM, int BN, int WM, int WN, int S, int L = BM / WM / 16, class Epilogue = std::nullptr_t>
 __device__ __forceinline__ void mfma_gemm_ring(const uint16_t* __restrict__ a, uint32_t lda, const uint16_t* __restrict__ b,
                                                uint32_t ldb, const T* __restrict__ bias, T* __restrict__ c, uint32_t ldc,
                                                uint32_t m_total, uint32_t n_total, uint32_t k_total,
                                                const int32_t* __restrict__ a_rows, const int32_t* __restrict__ c_rows, uint32_t m0,
-                                               uint32_t n0, uint32_t a_div, uint16_t* ring) {
+                                               uint32_t n0, uint32_t a_div, uint16_t* ring, Epilogue epilogue = nullptr,
+                                               uint32_t tag = 0) {
     static_assert(sizeof(T) == 2, "the ring body takes bfloat16");
     static_assert(S >= 3, "the ring needs a slot being read, one landed and one being filled");
     constexpr int WAVES = WM * WN;
@@ -1193,7 +1199,8 @@ __device__ __forceinline__ void mfma_gemm_ring(const uint16_t* __restrict__ a, u
     unroll<L>([&](auto i) {
         const uint32_t gm = m0 + wm * (BM / WM) + i * 16u + lane % 16u;
         if (gm < m_total) {
-            T* row = c + (c_rows ? size_t(c_rows[gm]) : size_t(gm)) * ldc;
+            const uint32_t c_row = c_rows ? uint32_t(c_rows[gm]) : gm;
+            T* row = c + size_t(c_row) * ldc;
             unroll<TN>([&](auto j) {
                 const uint32_t gn = n0 + wn * (BN / WN) + j * 16u + (lane / 16u) * 4u;
                 float v[4];
@@ -1201,7 +1208,11 @@ __device__ __forceinline__ void mfma_gemm_ring(const uint16_t* __restrict__ a, u
                 for (int r = 0; r < 4; ++r) {
                     v[r] = acc[i][j][r] + (bias && gn + r < n_total ? load1<T>(bias + gn + r) : 0.0f);
                 }
-                if (vector_rows && gn + 3u < n_total) {
+                if constexpr (!std::is_same_v<Epilogue, std::nullptr_t>) {
+                    if (gn + 3u < n_total) {
+                        epilogue(c_row, gn, v, tag);
+                    }
+                } else if (vector_rows && gn + 3u < n_total) {
                     const uint32_t lo = uint32_t(f32_to_bf16(v[0])) | (uint32_t(f32_to_bf16(v[1])) << 16);
                     const uint32_t hi = uint32_t(f32_to_bf16(v[2])) | (uint32_t(f32_to_bf16(v[3])) << 16);
                     *reinterpret_cast<uint2*>(row + gn) = uint2{lo, hi};
@@ -1653,11 +1664,16 @@ constexpr int ring_expert_slots() {
     return (LAST + BN) * 64 * 5 <= 150 * 1024 ? 5 : 4;
 }
 
+//
+// An ``epilogue`` (ring path only) replaces the stores of Y: it is called for every slot of a tile and every
+// 4 consecutive channels a lane holds, as mfma_gemm_ring describes, with the tile's expert as its tag (every
+// slot of a tile is routed to that expert); ``out`` is then not written.
 template <class T, bool PER_SLOT, int PATH = 0, int BN = 128, int RWM = 1, int RWN = 4, int LAST = 128,
-          int RS = ring_expert_slots<BN, LAST>()>
+          int RS = ring_expert_slots<BN, LAST>(), class Epilogue = std::nullptr_t>
 __device__ __forceinline__ void grouped_expert_linear(const T* __restrict__ w, const T* __restrict__ x, T* __restrict__ out,
                                                       const int32_t* __restrict__ scratch, uint32_t slots, uint32_t selected,
-                                                      uint32_t experts, uint32_t channels, uint32_t inner) {
+                                                      uint32_t experts, uint32_t channels, uint32_t inner, Epilogue epilogue = nullptr) {
+    static_assert(PATH == 3 || std::is_same_v<Epilogue, std::nullptr_t>, "epilogues on the ring path only");
     static_assert(PATH == 3 || BN == 128, "only the ring path takes wider channel tiles");
     static_assert(LAST == 128 || (PATH == 3 && LAST == int(kTallLastTile) && RWM == 1), "taller last tiles on the ring path only");
     const int32_t* offsets = scratch + experts;
@@ -1689,7 +1705,7 @@ __device__ __forceinline__ void grouped_expert_linear(const T* __restrict__ w, c
         auto body = [&](auto bm, auto live) {
             mfma_gemm_ring<T, int(bm), BN, RWM, RWN, RS, int(live)>(x, inner, slab, inner, nullptr, out, channels, rows, channels, inner,
                                                                      slots_of_tile, slots_of_tile, 0u, column * BN,
-                                                                     PER_SLOT ? 1u : selected, ring);
+                                                                     PER_SLOT ? 1u : selected, ring, epilogue, expert);
         };
         using I = std::integral_constant<int, 128>;
         if constexpr (LAST > 128) {

@@ -105,3 +105,44 @@ def gathered_routing(runs) -> tuple:
     ids = np.concatenate([arrays[1][:, :count] for _, count, arrays in runs], axis=1)
     logits = np.concatenate([as_float(arrays[0][:, :count]) for _, count, arrays in runs], axis=1)
     return ids, logits
+
+
+class ExpertMLP(torch.nn.Module):
+    """The workload's mixture-of-experts MLP (gpt_oss.py MLPBlock) at a chosen size, bfloat16, weights
+    N(0, ``std``) from ``seed``; with ``product`` the first expert product is returned as well."""
+
+    def __init__(self, hidden: int = 64, intermediate: int = 192, experts: int = 8, selected: int = 4, *, seed: int = 0,
+                 std: float = 0.1, product: bool = False) -> None:
+        super().__init__()
+        import dataclasses
+
+        from chroma_amd.models.gpt_oss import MLPBlock
+        from chroma_amd.models.variants import gpt_oss_20b
+
+        config = dataclasses.replace(gpt_oss_20b, hidden_size=hidden, intermediate_size=intermediate, num_experts=experts,
+                                     experts_per_token=selected)
+        with torch.device("meta"):
+            self.block = MLPBlock(config)
+        self.block = self.block.to_empty(device="cpu")
+        generator = torch.Generator().manual_seed(seed)
+        with torch.no_grad():
+            for name, parameter in self.block.named_parameters():
+                if name.endswith("scale"):
+                    parameter.fill_(1.0)
+                else:
+                    parameter.copy_(torch.randn(parameter.shape, generator=generator) * std)
+        self.product = product
+
+    def forward(self, x):
+        if not self.product:
+            return self.block(x)
+        from chroma_amd.models.gpt_oss import swiglu
+
+        b = self.block
+        t = b.norm(x)
+        experts = torch.topk(b.gate(t), k=b.experts_per_token, dim=-1, sorted=True)
+        weights = torch.nn.functional.softmax(experts.values, dim=1)
+        up = torch.einsum("beck,bk->bec", b.mlp1_weight[experts.indices, ...], t)
+        t = swiglu(up + b.mlp1_bias[experts.indices, ...], limit=b.swiglu_limit)
+        t = torch.einsum("beck,bek->bec", b.mlp2_weight[experts.indices, ...], t) + b.mlp2_bias[experts.indices, ...]
+        return x + torch.einsum("bec,be->bc", t, weights), up

@@ -273,6 +273,31 @@ def test_expert_ring_bodies_cross_compile_with_tall_last_tiles(tmp_path):
         build(generated, tmp_path / f"ring{width}", load=False)
 
 
+def test_gated_activation_is_the_first_expert_products_epilogue(tmp_path, monkeypatch):
+    """The MoE MLP's clamped SwiGLU (and the first product's bias) between its two expert products is
+    computed in the first product's epilogue: one launch fewer, and the first product is not stored when
+    nothing else reads it; when the graph also returns it, the fused kernel stores it too. Both build for
+    gfx950."""
+    from chroma_amd._src.codegen import hip as codegen
+    from tests.helpers import ExpertMLP
+
+    x = torch.randn(256, 64).to(torch.bfloat16)
+    monkeypatch.setattr(codegen, "ACTIVATION_EPILOGUES", False)
+    plain = lower(ExpertMLP(), x)
+    assert plain.stats["expert_epilogues"] == 0
+    monkeypatch.setattr(codegen, "ACTIVATION_EPILOGUES", True)
+    fused = lower(ExpertMLP(), x)
+    assert fused.stats["expert_epilogues"] == 1 and fused.stats["unstored_products"] == 1
+    assert fused.stats["launches"] == plain.stats["launches"] - 1
+    source = fused.files["model.hip"]
+    assert "auto epilogue = [&]" in source and ", epilogue);" in source and "uint2{" not in source
+    build(fused, tmp_path / "fused", load=False)
+    both = lower(ExpertMLP(product=True), x)
+    assert both.stats["expert_epilogues"] == 1 and both.stats["unstored_products"] == 0
+    assert "uint2{" in both.files["model.hip"]  # the epilogue stores the product as well
+    build(both, tmp_path / "both", load=False)
+
+
 OPERATIONS_SOURCE = """
 def fn(x, y, ids):
     selected = x[ids]

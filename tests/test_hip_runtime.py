@@ -378,6 +378,29 @@ def test_grouped_expert_products_ring_body(tmp_path, channels, inner):
         compare(model(*inputs), oracle(*[numpy_of(v) for v in inputs]))
 
 
+def test_gated_activation_epilogue_is_bit_identical(tmp_path, monkeypatch):
+    """The MoE MLP (hidden 128, 8 experts top-4, intermediate 384: a two-column-tile ring up product over
+    ~256 slots per expert) with its clamped SwiGLU computed in the up product's epilogue equals the build
+    with a separate activation launch bit for bit; so does the up product itself when the graph also
+    returns it (the fused kernel then stores it). (The C5 block and decoder tests hold the fused path
+    against the oracle.)"""
+    from chroma_amd._src.codegen import hip as codegen
+    from tests.helpers import ExpertMLP
+
+    x = (torch.randn(512, 128, generator=torch.Generator().manual_seed(3)) * 2).to(torch.bfloat16)
+    for product in (False, True):
+        exported = torch.export.export(ExpertMLP(128, 384, seed=1, std=0.08, product=product).eval(), (x,))
+        runs = []
+        for fused in (False, True):
+            monkeypatch.setattr(codegen, "ACTIVATION_EPILOGUES", fused)
+            with chroma_amd.compile(exported, tmp_path / f"{product}{fused}") as program:
+                assert program.stats["expert_epilogues"] == int(fused)
+                assert program.stats["unstored_products"] == int(fused and not product)
+                runs.append([np.asarray(a).copy() for a in leaves(program(x))])
+        for plain, fused in zip(*runs):
+            np.testing.assert_array_equal(fused.view(np.uint16), plain.view(np.uint16))
+
+
 def test_aliases_and_live_workspace_across_linear_layers(tmp_path):
     def fn(x, w):
         first = torch.nn.functional.linear(x, w)
