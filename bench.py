@@ -578,7 +578,8 @@ def c5_slice(work: Path) -> dict:
     [window 16 at this context], one full layer), all 32 experts, a 64-position cache, a 32-token prefill
     chunk and 4 single-token steps, both through routing probes (``export_cached(..., routing=True)``).
     Reported: the oracle's time per call; the routing agreement over every (position, layer) decision
-    with each flip and both runs' own gate-logit gaps (oracle/routing.py); per call, the logits row of its
+    with each flip and both runs' own gate-logit gaps (oracle/routing.py), and the same comparison of eager
+    torch's bfloat16 forward (its own gate logits) with the oracle, the noise floor; per call, the logits row of its
     last position against the oracle's, with eager torch's bfloat16 forward against the oracle on the same
     row (the rounding noise floor), and whether the row depends on a flip. Every call is listed; the
     summary holds the calls that do not depend on a flip to the bfloat16 bar and names the others."""
@@ -602,8 +603,14 @@ def c5_slice(work: Path) -> dict:
     layers = 2
     model = make_gpt_oss_20b(2, num_hidden_layers=layers, num_experts=32, sliding_window=16)
     tokens = torch.randint(0, VOCAB, (36,), generator=torch.Generator().manual_seed(2))
+    gates = []
+    hooks = [block.mlp.gate.register_forward_hook(lambda module, args, out: gates.append(out.float().numpy())) for block in model.block]
     with torch.no_grad():
         eager = model(tokens).float().numpy()
+    for hook in hooks:
+        hook.remove()
+    eager_logits = np.stack(gates)  # [layers, positions, experts]: eager torch's own bfloat16 gate logits
+    eager_ids = torch.topk(torch.from_numpy(eager_logits), 4, dim=-1, sorted=True).indices.numpy()
     graphs = [export_cached(model, 64, 32, routing=True), export_cached(model, 64, 1, routing=True)]
     hip = [chroma_amd.compile(g, work / f"c5s_hip{i}") for i, g in enumerate(graphs)]
     cpu = [compile_cpu(g, work / f"c5s_cpu{i}") for i, g in enumerate(graphs)]
@@ -625,7 +632,16 @@ def c5_slice(work: Path) -> dict:
             rows.append((end - 1, got, want))
     for program in (*hip, *cpu):
         program.close()
-    routing = compare_routing(*gathered(hip_runs), *gathered(cpu_runs), bound_ulps=2.0)
+    oracle_routing = gathered(cpu_runs)
+    routing = compare_routing(*gathered(hip_runs), *oracle_routing, bound_ulps=2.0)
+    # the same comparison for eager torch's bfloat16 forward: how far another exact bfloat16 evaluation of
+    # the model drifts from the oracle on the same decisions (the noise floor hip's flips sit against)
+    eager_routing = compare_routing(eager_ids, eager_logits, *oracle_routing, bound_ulps=2.0)
+
+    def flip_list(result, name):
+        return [{"position": f["position"], "layer": f["layer"], f"{name}_ids": f["hip_ids"], "oracle_ids": f["ref_ids"],
+                 f"gaps_ulps_{name}_oracle": [[p["hip_gap_ulps"], p["ref_gap_ulps"]] for p in f["pairs"]], "explained": f["explained"]}
+                for f in result["flips"]]
     calls = []
     for position, got, want in rows:
         noise = eager[position]
@@ -641,13 +657,19 @@ def c5_slice(work: Path) -> dict:
                              f"({routing['downstream']} downstream of a flip, {routing['downstream_matched']} of them agree)",
         "tie_reorders": [{"position": t["position"], "layer": t["layer"], "hip_ids": t["hip_ids"], "oracle_ids": t["ref_ids"],
                           "hip_lower_id_first": t["hip_lower_id_first"]} for t in routing["tie_reorders"]],
-        "flips": [{"position": f["position"], "layer": f["layer"], "hip_ids": f["hip_ids"], "oracle_ids": f["ref_ids"],
-                   "gaps_ulps_hip_oracle": [[p["hip_gap_ulps"], p["ref_gap_ulps"]] for p in f["pairs"]], "explained": f["explained"]}
-                  for f in routing["flips"]],
+        "flips": flip_list(routing, "hip"),
         "unexplained_flips": routing["unexplained"],
+        # flips beyond the bound whose gaps are still within how far eager torch's own gate logits drift
+        # from the oracle's (another exact bfloat16 evaluation)
+        "unexplained_within_eager_logit_drift": sum(
+            1 for f in routing["flips"] if not f["explained"]
+            and all(max(p["hip_gap_ulps"], p["ref_gap_ulps"]) <= eager_routing["logit_max_diff_ulps"] for p in f["pairs"])),
         "hip_ids_are_top4_of_own_logits": not routing["hip_selection_mismatches"],
         "gate_logits_max_diff_row_ulps": routing["logit_max_diff_ulps"],
         "flip_bound_ulps": routing["bound_ulps"],
+        "eager_vs_oracle_routing": {"agreement": eager_routing["agreement"], "flips": flip_list(eager_routing, "eager"),
+                                    "unexplained_flips": eager_routing["unexplained"],
+                                    "gate_logits_max_diff_row_ulps": eager_routing["logit_max_diff_ulps"]},
         "calls_held": len(held), "calls_downstream_of_flip": [c["position"] for c in calls if c["downstream_of_flip"]],
         "held_rel_norm": max(c["rel_norm"] for c in held) if held else None,
         "held_max_abs": max(c["max_abs"] for c in held) if held else None,

@@ -1056,7 +1056,13 @@ __device__ __forceinline__ void attention_live_tiles(const uint16_t* __restrict_
 template <int D, int G, bool POW2> __device__ __forceinline__ void attention_heads_mfma_bf16(const AttentionOperands& a) {
     static_assert(D % 32 == 0 && D <= 128 && G >= 1 && G <= 8, "head dimension and group");
     constexpr int QT = 16, KB = 64, THREADS = 64 * G;
-    constexpr int KPAD = D + 8, VPAD = KB + 8, MPAD = KB + 4;
+    // K rows unpadded, their 16-byte chunk c stored at c ^ ((row / 2) & KSWZ) (KSWZ keeps it inside the
+    // row): the 16-byte K fragment reads then hit no bank twice (with 144-byte padded rows they accounted
+    // for every SQ_LDS_BANK_CONFLICT cycle of the kernel, 1.1x its LDS-active cycles). V^T rows of 136
+    // bytes: a fragment read's 16 lanes (one V^T row each, 8 bytes) land on distinct bank pairs. Full C5
+    // layer 196 -> 182 us.
+    constexpr int KPAD = D, VPAD = KB + 4, MPAD = KB + 4;
+    constexpr uint32_t KSWZ = ((D / 8) & 7) == 0 ? 7u : ((D / 8) & 3) == 0 ? 3u : 1u;
     constexpr int CHUNKS = (KB * D / 8 + THREADS - 1) / THREADS;  // 16-byte K (and V) chunks per thread per block
     constexpr int MASKS = (QT * KB + THREADS - 1) / THREADS;      // mask entries per thread per block
     constexpr uint32_t MASKED = 0x8000u;                           // list entry flag: the block reads its mask
@@ -1151,7 +1157,7 @@ template <int D, int G, bool POW2> __device__ __forceinline__ void attention_hea
             if (c < uint32_t(KB * D / 8)) {
                 const uint32_t r = c / (D / 8), dc = (c % (D / 8)) * 8u;
                 const bool ok = kb * KB + r < a.keys;
-                *reinterpret_cast<uint4*>(&k_s[buffer][r * KPAD + dc]) = ok ? rk[i] : uint4{0, 0, 0, 0};
+                *reinterpret_cast<uint4*>(&k_s[buffer][r * KPAD + (((dc / 8u) ^ ((r >> 1) & KSWZ)) * 8u)]) = ok ? rk[i] : uint4{0, 0, 0, 0};
                 if (values) {
                     // lanes hold consecutive keys vr of one chunk: each 2-byte store of a wave covers 128
                     // contiguous bytes of a V^T row (no two lanes in one bank at different addresses)
@@ -1186,7 +1192,7 @@ template <int D, int G, bool POW2> __device__ __forceinline__ void attention_hea
             acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int ks = 0; ks < D / 32; ++ks) {
-                const bf16x8_t kf = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(&k_s[buffer][(t * 16u + col) * KPAD + ks * 32u + quad * 8u]));
+                const bf16x8_t kf = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(&k_s[buffer][(t * 16u + col) * KPAD + (((ks * 4u + quad) ^ (((t * 16u + col) >> 1) & KSWZ)) * 8u)]));
                 acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ks], acc[t], 0, 0, 0);
             }
         }
