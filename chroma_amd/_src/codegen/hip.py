@@ -52,7 +52,8 @@ ROW_THREADS = 256
 ROW_RESIDENT = 32
 ROW_UNROLL = 4  # vector loads per thread in flight in the one-pass row statistics
 # a row softmax whose row splits evenly into at least two vector steps of this many threads takes them: fewer
-# values per thread leave more waves resident (C2's [16384, 8192] fp32 rows: 0.269 ms against 0.274 at 256)
+# values per thread leave more waves resident (C2's [16384, 8192] fp32 rows: 2-3% faster than 256 threads,
+# measured in one process)
 WIDE_ROW_THREADS = 1024
 SPLIT_ROW_LIMIT = 256  # rows of a reduction below this count are split over workgroups when wide
 SPLIT_ROW_BLOCKS = 1024  # workgroups a split row reduction aims for
