@@ -92,6 +92,12 @@ RING_EXPERT_TILES = ((384, 8, 160), (320, 4, 128))
 # A gated activation between two expert products is computed in the first product's epilogue (no map
 # launch; the first product is not stored when nothing else reads it). False keeps the separate launch.
 ACTIVATION_EPILOGUES = True
+# An elementwise expression of a row-per-workgroup RMSNorm's output (the workloads' cast to bfloat16) is
+# written by the norm kernel itself. False keeps the separate map launch.
+NORM_EPILOGUES = True
+# A stored map reading only weights and graph inputs is launched once per distinct kernel and bindings
+# (``_constant_map``). False launches every one.
+CONSTANT_MAPS = True
 REUSED_EVALUATIONS = 1 << 18  # a contraction operand is stored when (elements x reuse) reaches this
 SMALL_REDUCTION = 8  # contractions summing at most this many products are fused expressions...
 SMALL_OPERAND_COST = 8  # ...over operands that cost at most this much per element (others are stored)
@@ -213,9 +219,13 @@ class HIPCodegen(Codegen):
         # swapped in at the end when nothing else reads the product.
         self.last_grouped: Optional[dict] = None
         self.epilogue_values: Dict[str, Value] = {}
-        self.product_stores: List[Tuple[int, str, Kernel, Tuple[int, int, int], int]] = []
+        self.product_stores: List[Tuple[int, str, Kernel, Tuple[int, int, int], int, Sequence[str], str]] = []
         self.expert_epilogues = 0
         self.unstored_products = 0
+        self.constant_maps: Dict[tuple, Value] = {}  # (kernel, read bindings, grid) -> buffer it wrote
+        self.reused_maps = 0
+        self.last_norm: Optional[dict] = None  # the last one-workgroup-per-row RMSNorm launch
+        self.norm_epilogues = 0
 
     # ===================================================================================== storage
     def extern(self, tensor: torch.Tensor, kind: str, offset: int) -> Value:
@@ -354,10 +364,60 @@ class HIPCodegen(Codegen):
         if value.name in self.pending_norms:
             return self._force_norm(value.name)
         if value.name not in self.materialized:
-            out = self.allocate(value.shape, value.dtype)
-            self.map_kernel(out, value)
-            self.materialized[value.name] = out
+            fused = self._norm_epilogue(value)
+            self.materialized[value.name] = fused if fused is not None else self._constant_map(self.allocate(value.shape, value.dtype), value)
         return self.materialized[value.name]
+
+    def _norm_epilogue(self, value: Value) -> Optional[Value]:
+        """Store ``value`` from the RMSNorm kernel that is the last launch when ``value`` is an elementwise
+        expression of that norm's output (same shape; any other buffer it reads is a weight or graph
+        input): the norm launch is re-emitted writing ``value`` too, and, unless some later launch reads
+        the norm itself, finally without the norm's store. The workloads' norms end with a cast to
+        bfloat16, which then costs no map launch and no float round trip."""
+        last = self.last_norm
+        if not NORM_EPILOGUES or last is None or last["index"] != len(self.launches) - 1 or value.stored or value.name not in self.closures:
+            return None
+        out, x, weight, epsilon = last["args"]
+        sources = self.sources.get(value.name, frozenset())
+        if (out.name not in sources or tuple(value.shape) != tuple(out.shape)
+                or any(self.binding_of(b).kind not in ("weight", "input") for b in sources if b != out.name)):
+            return None
+        buffer = self.allocate(tuple(value.shape), value.dtype)
+        try:
+            k, prologue = self._rmsnorm_rows(out, x, weight, epsilon, epilogue=(value, buffer))
+            lean, _ = self._rmsnorm_rows(out, x, weight, epsilon, epilogue=(value, buffer), store_norm=False)
+        except _NotFusible:
+            return None
+        self._retract_last_launch()
+        self.launch(k, last["rows"], last["threads"], [x, weight, value], kind="rmsnorm", prologue=prologue)
+        self.product_stores.append((len(self.launches) - 1, out.root.name, lean, self.launches[-1].grid, last["threads"], prologue, "rmsnorm"))
+        self.epilogue_values[value.name] = buffer
+        self.last_norm = None
+        self.norm_epilogues += 1
+        return buffer
+
+    def _constant_map(self, out: Value, value: Value) -> Value:
+        """``map_kernel(out, value)``, except that a map reading only weights and graph inputs (which no
+        launch writes) whose kernel and bindings equal an earlier one's is not launched again: the earlier
+        buffer already holds the same values and is returned instead (the per-layer rotary cos/sin
+        tables of a prefill are computed once)."""
+        shape = _shape(value.shape)
+        lanes = choose_lanes(shape[-1], value.dtype, 8 if value.dtype == torch.bfloat16 else 4)
+        k, grid = self._map_kernel(out, value, None, lanes)
+        if lanes == 8 and k.scalar_lane_loads:
+            k, grid = self._map_kernel(out, value, None, 4)
+        reads = [buffer for buffer in k.slots if buffer != out.name]
+        key = None
+        if CONSTANT_MAPS and all(self.binding_of(buffer).kind in ("weight", "input") for buffer in reads):
+            key = (k.render("KERNEL_NAME", MAP_THREADS), tuple(self.binding_of(buffer) for buffer in reads), grid)
+            earlier = self.constant_maps.get(key)
+            if earlier is not None:
+                self.reused_maps += 1
+                return earlier
+        self.launch(k, grid, MAP_THREADS, [value], kind="map")
+        if key is not None:
+            self.constant_maps[key] = out
+        return out
 
     @staticmethod
     def is_contiguous(value: Value) -> bool:
@@ -372,8 +432,10 @@ class HIPCodegen(Codegen):
             return value
         key = value.name + "#contiguous"
         if key not in self.materialized:
-            out = self.allocate(value.shape, value.dtype)
-            self.map_kernel(out, value)
+            out = self._norm_epilogue(value)
+            if out is None:
+                out = self.allocate(value.shape, value.dtype)
+                self.map_kernel(out, value)
             self.materialized[key] = out
         return self.materialized[key]
 
@@ -490,6 +552,10 @@ class HIPCodegen(Codegen):
         for buffer in list(k.slots):
             if buffer in self.pending_stores and buffer not in k.unstored:
                 self._flush_store(buffer)
+        for buffer, (_, _, writable) in k.slots.items():
+            # weights and graph inputs are never written by a launch (``_constant_map`` relies on it)
+            if writable and self.binding_of(buffer).kind in ("weight", "input"):
+                raise AssertionError(f"a launch writes {buffer}, a weight or graph input")
         source = k.render("KERNEL_NAME", block, prologue)
         name = self.kernel_names.get(source)
         if name is None:
@@ -1496,9 +1562,28 @@ class HIPCodegen(Codegen):
             self._split_norm(out, x, weight, epsilon, shape, rows, columns, splits, chunk, split_lanes)
             self.parallel_reductions += 1
             return out
+        k, prologue = self._rmsnorm_rows(out, x, weight, epsilon)
+        self.launch(k, rows, threads, [x, weight], kind="rmsnorm", prologue=prologue)
+        self.parallel_reductions += 1
+        self.last_norm = {"index": len(self.launches) - 1, "args": (out, x, weight, epsilon), "rows": rows, "threads": threads}
+        return out
+
+    def _rmsnorm_rows(self, out: Value, x: Value, weight: Value, epsilon: float, epilogue: Optional[Tuple[Value, Value]] = None,
+                      store_norm: bool = True) -> Tuple[Kernel, List[str]]:
+        """The one-workgroup-per-row RMSNorm kernel writing ``out`` (and its shared-memory prologue). With
+        ``epilogue`` = (value, buffer) it also writes ``value``, an elementwise expression of ``out`` (the
+        bfloat16 cast the workloads' norm ends with), into ``buffer`` from the normalised lanes it holds,
+        and writes ``out`` itself only if ``store_norm``; a read of ``out`` at any other element raises
+        ``_NotFusible``."""
+        shape = _shape(x.shape)
+        columns = shape[-1]
+        rows = math.prod(shape) // columns
+        dim = len(shape) - 1
+        threads, lanes, chunks, resident = self._row_plan(columns, x.dtype)
         waves = threads // 64
         k = Kernel(lanes)
-        slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name]) if store_norm else None
+        extra = None if epilogue is None else k.slot(epilogue[1].name, epilogue[1].dtype, writable=True, extent=self.extents[epilogue[1].name])
         row = Aff.of(k.atom("blockIdx.x", rows - 1, prefix="r"))
         step = threads * lanes
         ragged = columns % step != 0
@@ -1540,13 +1625,27 @@ class HIPCodegen(Codegen):
             xs = [f"vals[c][{lane}]" for lane in range(lanes)] if resident else names_of(self.read(k, x, coords(j)))
             ws = names_of(self.read(k, weight, [j]))
             result = self._lane_values(k, [f"{xv} * scale * {wv}" for xv, wv in zip(xs, ws)])
-            k.store(slot, out.dtype, Kernel.flatten(coords(j), shape), result)
+            at = Kernel.flatten(coords(j), shape)
+            if store_norm:
+                k.store(slot, out.dtype, at, result)
+            if epilogue is not None:
+                value, buffer = epilogue
+                here = at + out.view.offset
+
+                def normalised(address: Aff) -> tuple:
+                    if address != here:
+                        raise _NotFusible(f"the expression reads {out.name}[{address.code()}], not the element it stores")
+                    return result
+
+                k.register_reads[out.root.name] = normalised
+                try:
+                    k.store(extra, buffer.dtype, at, self.read(k, value, coords(j)))
+                finally:
+                    del k.register_reads[out.root.name]
             if ragged and resident:
                 k.indent -= 1
                 k.line("}")
-        self.launch(k, rows, threads, [x, weight], kind="rmsnorm", prologue=[f"__shared__ float scratch[{waves}];"])
-        self.parallel_reductions += 1
-        return out
+        return k, [f"__shared__ float scratch[{waves}];"]
 
     def _split_norm(self, out: Value, x: Value, weight: Value, epsilon: float, shape, rows: int, columns: int, splits: int, chunk: int,
                     lanes: int) -> None:
@@ -2832,7 +2931,7 @@ class HIPCodegen(Codegen):
             return None
         self._retract_last_launch()
         self.launch(k, grid, threads, [weight, xin, scratch, x], kind="experts_mfma")
-        self.product_stores.append((len(self.launches) - 1, out.root.name, lean, self.launches[-1].grid, threads))
+        self.product_stores.append((len(self.launches) - 1, out.root.name, lean, self.launches[-1].grid, threads, (), "experts_mfma"))
         self.epilogue_values[x.name] = buffer
         self.materialized[x.name] = buffer
         self.last_grouped = None
@@ -2842,13 +2941,13 @@ class HIPCodegen(Codegen):
     def _drop_unread_product_stores(self) -> None:
         """After lowering: a fused expert launch whose product no later launch binds and no output holds
         takes the variant that does not store the product."""
-        for index, product, lean, grid, threads in self.product_stores:
+        for index, product, lean, grid, threads, prologue, kind in self.product_stores:
             if product in self.output_buffers or any(product in launch.buffers for launch in self.launches[index + 1 :]):
                 continue
-            source = lean.render("KERNEL_NAME", threads)
+            source = lean.render("KERNEL_NAME", threads, prologue)
             name = self.kernel_names.get(source)
             if name is None:
-                name = f"chroma_experts_mfma_{hashlib.sha256(source.encode()).hexdigest()[:8]}"
+                name = f"chroma_{kind}_{hashlib.sha256(source.encode()).hexdigest()[:8]}"
                 self.kernel_names[source] = name
                 self.kernel_sources.append(source.replace("KERNEL_NAME", name, 1))
             old = self.launches[index]
@@ -2970,6 +3069,8 @@ class HIPCodegen(Codegen):
             routed_experts=self.routed_experts,
             expert_epilogues=self.expert_epilogues,
             unstored_products=self.unstored_products,
+            reused_maps=self.reused_maps,
+            norm_epilogues=self.norm_epilogues,
             small_contractions=self.small_contractions,
             attention_epilogues=self.attention_epilogues,
             write_through_stores=len(self.write_through_stores),

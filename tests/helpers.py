@@ -146,3 +146,21 @@ class ExpertMLP(torch.nn.Module):
         t = swiglu(up + b.mlp1_bias[experts.indices, ...], limit=b.swiglu_limit)
         t = torch.einsum("beck,bek->bec", b.mlp2_weight[experts.indices, ...], t) + b.mlp2_bias[experts.indices, ...]
         return x + torch.einsum("bec,be->bc", t, weights), up
+
+
+class NormThenLinear(torch.nn.Module):
+    """The workloads' RMSNorm (float32 chain, cast back to bfloat16) feeding a linear; with ``both`` the
+    float32 normalised rows are returned as well."""
+
+    def __init__(self, width: int = 256, columns: int = 384, *, both: bool = False, seed: int = 0) -> None:
+        super().__init__()
+        generator = torch.Generator().manual_seed(seed)
+        self.scale = torch.nn.Parameter(torch.rand(width, generator=generator) + 0.5)
+        self.weight = torch.nn.Parameter((torch.randn(columns, width, generator=generator) * 0.05).to(torch.bfloat16))
+        self.both = both
+
+    def forward(self, x):
+        h = x.float()
+        y = h * torch.rsqrt(torch.mean(h**2, dim=-1, keepdim=True) + 1e-5) * self.scale
+        out = torch.nn.functional.linear(y.to(torch.bfloat16), self.weight)
+        return (out, y) if self.both else out

@@ -282,6 +282,7 @@ def test_gated_activation_is_the_first_expert_products_epilogue(tmp_path, monkey
     from tests.helpers import ExpertMLP
 
     x = torch.randn(256, 64).to(torch.bfloat16)
+    monkeypatch.setattr(codegen, "NORM_EPILOGUES", False)  # counted on their own below
     monkeypatch.setattr(codegen, "ACTIVATION_EPILOGUES", False)
     plain = lower(ExpertMLP(), x)
     assert plain.stats["expert_epilogues"] == 0
@@ -296,6 +297,41 @@ def test_gated_activation_is_the_first_expert_products_epilogue(tmp_path, monkey
     assert both.stats["expert_epilogues"] == 1 and both.stats["unstored_products"] == 0
     assert "uint2{" in both.files["model.hip"]  # the epilogue stores the product as well
     build(both, tmp_path / "both", load=False)
+
+
+def test_norm_cast_is_the_norm_kernels_epilogue(tmp_path, monkeypatch):
+    """The bfloat16 cast a workload's RMSNorm ends with is written by the norm kernel itself (one launch
+    fewer, no float round trip); when the graph also returns the float rows, the fused kernel keeps
+    writing them. Both build for gfx950."""
+    from chroma_amd._src.codegen import hip as codegen
+    from tests.helpers import NormThenLinear
+
+    x = torch.randn(256, 256).to(torch.bfloat16)
+    monkeypatch.setattr(codegen, "NORM_EPILOGUES", False)
+    plain = lower(NormThenLinear(), x)
+    monkeypatch.setattr(codegen, "NORM_EPILOGUES", True)
+    fused = lower(NormThenLinear(), x)
+    assert plain.stats["norm_epilogues"] == 0 and fused.stats["norm_epilogues"] == 1
+    assert fused.stats["launches"] == plain.stats["launches"] - 1 and fused.stats["unstored_products"] == 1
+    build(fused, tmp_path / "fused", load=False)
+    both = lower(NormThenLinear(both=True), x)
+    assert both.stats["norm_epilogues"] == 1 and both.stats["unstored_products"] == 0
+    build(both, tmp_path / "both", load=False)
+
+
+def test_constant_tables_are_computed_once():
+    """A stored map that reads only weights and graph inputs is launched once per distinct kernel and
+    bindings: the prefill's per-layer rotary cos/sin tables (a transcendental table stored for its many
+    readers) are computed by the first layer and read by the others."""
+    from chroma_amd.models.cached import export_cached
+
+    # tables of 512 steps x 16 frequencies: large enough to be stored, in each of 3 layers
+    model = random_transformer(small_config(num_hidden_layers=3, head_dim=32, num_attention_heads=2, num_key_value_heads=1),
+                               seed=1, std=0.1)
+    generated = lower_program(export_cached(model, 512, 512), HIPCodegen())
+    assert generated.stats["reused_maps"] == 4, generated.stats["reused_maps"]  # cos and sin of layers 1 and 2
+    plan = [line.split()[1] for line in generated.files["model.plan"].splitlines() if line.startswith("launch ")]
+    assert len(plan) == generated.stats["launches"]
 
 
 OPERATIONS_SOURCE = """

@@ -388,6 +388,7 @@ def test_gated_activation_epilogue_is_bit_identical(tmp_path, monkeypatch):
     from tests.helpers import ExpertMLP
 
     x = (torch.randn(512, 128, generator=torch.Generator().manual_seed(3)) * 2).to(torch.bfloat16)
+    monkeypatch.setattr(codegen, "NORM_EPILOGUES", False)  # the norm's own epilogue is tested on its own
     for product in (False, True):
         exported = torch.export.export(ExpertMLP(128, 384, seed=1, std=0.08, product=product).eval(), (x,))
         runs = []
@@ -399,6 +400,36 @@ def test_gated_activation_epilogue_is_bit_identical(tmp_path, monkeypatch):
                 runs.append([np.asarray(a).copy() for a in leaves(program(x))])
         for plain, fused in zip(*runs):
             np.testing.assert_array_equal(fused.view(np.uint16), plain.view(np.uint16))
+
+
+def test_norm_epilogue_and_table_reuse_are_bit_identical(tmp_path, monkeypatch):
+    """The RMSNorm kernel writing its bfloat16 cast itself, and rotary tables computed once for all layers,
+    give the same bits as the separate launches: a norm feeding a linear (with and without the float rows
+    also returned), and a 3-layer bfloat16 KV-cached prefill whose layers share their tables."""
+    from chroma_amd._src.codegen import hip as codegen
+    from chroma_amd.models.cached import export_cached
+    from tests.helpers import NormThenLinear
+
+    x = (torch.randn(256, 256, generator=torch.Generator().manual_seed(2)) * 3).to(torch.bfloat16)
+    cases = [(torch.export.export(NormThenLinear(both=both).eval(), (x,)), [x]) for both in (False, True)]
+    model = random_transformer(small_config(num_hidden_layers=3, head_dim=32, num_attention_heads=2, num_key_value_heads=1),
+                               seed=1, std=0.1, dtype=torch.bfloat16)
+    tokens = (torch.arange(512) * 7 + 3) % 17
+    cached = export_cached(model, 512, 512)
+    cases.append((cached, None))
+    for n, (exported, inputs) in enumerate(cases):
+        runs = []
+        for fused in (False, True):
+            monkeypatch.setattr(codegen, "NORM_EPILOGUES", fused)
+            monkeypatch.setattr(codegen, "CONSTANT_MAPS", fused)
+            with chroma_amd.compile(exported, tmp_path / f"{n}{fused}") as program:
+                if inputs is None:
+                    with Decoder(program, chroma_amd.compile(export_cached(model, 512, 1), tmp_path / f"{n}{fused}d")) as decoder:
+                        runs.append([np.asarray(decoder.append(tokens.numpy())).copy()])
+                    continue
+                runs.append([np.asarray(a).copy() for a in leaves(program(*inputs))])
+        for plain, fused in zip(*runs):
+            np.testing.assert_array_equal(fused.view(np.uint8), plain.view(np.uint8))
 
 
 def test_aliases_and_live_workspace_across_linear_layers(tmp_path):
