@@ -643,10 +643,21 @@ class HIPCodegen(Codegen):
         out = self.allocate(tuple(meta.shape), meta.dtype)
         shape = _shape(out.shape)
         innermost = dim == len(shape) - 1
-        lanes = choose_lanes(shape[-1], meta.dtype)
+        # bfloat16 parts take 8 lanes (16-byte accesses) like the map kernels, unless some operand could not
+        # be read that wide; then 4
+        lanes = choose_lanes(shape[-1], meta.dtype, 8 if meta.dtype == torch.bfloat16 else 4)
         if innermost:
             while lanes > 1 and any(v.shape[dim] % lanes for v in values):
                 lanes //= 2
+        k, grid = self._concat_kernel(out, values, dim, lanes)
+        if lanes == 8 and k.scalar_lane_loads:
+            k, grid = self._concat_kernel(out, values, dim, 4)
+        self.launch(k, grid, MAP_THREADS, values, kind="concat")
+        return out
+
+    def _concat_kernel(self, out: Value, values: Sequence[Value], dim: int, lanes: int) -> Tuple[Kernel, int]:
+        shape = _shape(out.shape)
+        innermost = dim == len(shape) - 1
         count = math.prod(shape)
         k = Kernel(lanes)
         slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
@@ -681,9 +692,7 @@ class HIPCodegen(Codegen):
                 k.indent -= 1
                 start = end
             k.line("}")
-        grid = max(1, min(-(-vectors // MAP_THREADS), MAP_GRID))
-        self.launch(k, grid, MAP_THREADS, values, kind="concat")
-        return out
+        return k, max(1, min(-(-vectors // MAP_THREADS), MAP_GRID))
 
     def _concat_expression(self, meta, values: Sequence[Value], dim: int) -> Value:
         """Concatenation folded into its consumer: a case split over the parts along ``dim`` (only the

@@ -316,7 +316,32 @@ class Kernel:
         low = Aff(remainder, aff.const % divisor)
         if low.hi() < divisor:
             return Aff(quotient, aff.const // divisor)
+        split = self._split_terms(low, divisor)
+        if split is not None:
+            return Aff(quotient + split[0], aff.const // divisor)
         return self._opaque(("div", aff, divisor), aff, f"({{}}) / {divisor}u", aff.hi() // divisor)
+
+    def _split_terms(self, low: Aff, divisor: int) -> Optional[Tuple[List[Tuple[Atom, int]], Aff]]:
+        """``low`` (every coefficient below ``divisor``) as divisor * q + r with 0 <= r < divisor, by
+        writing each uniform term c * a whose coefficient divides the divisor as
+        divisor * (a / m) + c * (a % m), m = divisor / c: returns (q's terms, r), or None when the rest
+        still reaches the divisor. (a / m and a % m are uniform: computed once, shifts for powers of two.)
+        Folds the head-major addresses views produce, e.g. (64 * head + j) / 512 = head / 8 for j < 64."""
+        quotient: List[Tuple[Atom, int]] = []
+        rest = Aff((), low.const)
+        changed = False
+        for atom, coef in low.terms:
+            if coef > 1 and divisor % coef == 0 and not atom.varying and atom.hi >= divisor // coef:
+                m = divisor // coef
+                whole = Aff.of(atom)
+                quotient += self._opaque(("div", whole, m), whole, f"({{}}) / {m}u", atom.hi // m).terms
+                rest = rest + self._opaque(("mod", whole, m), whole, f"({{}}) % {m}u", m - 1).scale(coef)
+                changed = True
+            else:
+                rest = rest + Aff(((atom, coef),))
+        if not changed or rest.hi() >= divisor:
+            return None
+        return quotient, rest
 
     def mod(self, aff: Aff, modulus: int) -> Aff:
         if modulus == 1:
@@ -326,7 +351,12 @@ class Kernel:
         reduced = Aff([(a, c % modulus) for a, c in aff.terms], aff.const % modulus)
         if reduced.hi() < modulus:
             return reduced
-        return self._opaque(("mod", aff, modulus), aff, f"({{}}) % {modulus}u", min(modulus - 1, aff.hi()))
+        split = self._split_terms(reduced, modulus)
+        if split is not None:
+            return split[1]
+        # aff and its reduced form differ by a multiple of the modulus: the remainder of the reduced form
+        # (fewer terms, and shared with any other address that reduces to it)
+        return self._opaque(("mod", reduced, modulus), reduced, f"({{}}) % {modulus}u", min(modulus - 1, reduced.hi()))
 
     def unflatten(self, flat: Aff, shape: Sequence[int]) -> List[Aff]:
         coords = []

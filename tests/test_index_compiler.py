@@ -47,6 +47,24 @@ def test_div_mod_of_random_affine_forms(seed):
             assert 0 <= evaluate(kernel, remainder, dict(env)) <= remainder.hi()
 
 
+def test_head_major_addresses_fold_without_an_opaque_division():
+    """(4096 * token + 64 * head + j) / 512 and % 512 for j < 32 (a rotary half of a head of 64 inside a
+    [tokens, 8, 8, 64] view): the head term is split as 512 * (head / 8) + 64 * (head % 8), so the
+    quotient is 8 * token + head / 8 and no division of the whole address is declared; correct for every
+    value."""
+    kernel = Kernel()
+    token, head, j = Atom("t", 3), Atom("h", 63), Atom("j", 31)
+    aff = Aff(((token, 4096), (head, 64), (j, 1)), 0)
+    quotient, remainder = kernel.div(aff, 512), kernel.mod(aff, 512)
+    declared = [kernel.definitions[a.name] for a, _ in quotient.terms + remainder.terms if a.name in kernel.definitions]
+    assert declared and all(operand != aff for _, operand, _ in declared)  # only head / 8 and head % 8
+    assert quotient.coefficient(token) == 8 and quotient.coefficient(j) == 0
+    for env in all_values([token, head, j]):
+        value = evaluate(kernel, aff, dict(env))
+        assert evaluate(kernel, quotient, dict(env)) == value // 512
+        assert evaluate(kernel, remainder, dict(env)) == value % 512
+
+
 @pytest.mark.parametrize("seed", range(30))
 def test_view_addresses_decode_to_the_right_coordinates(seed):
     """A permuted / sliced / broadcast view of a contiguous source, read through flat-index decoding."""
