@@ -1961,8 +1961,9 @@ class HIPCodegen(Codegen):
     def _stream_plan(rows: int, inner: int, dtype: torch.dtype, weight_bytes: int) -> Optional[Tuple[int, int]]:
         """(lanes per row, rows per step) for ``stream_rows``: 64 lanes per row when a row has at least 64
         16-byte chunks, wastes at most 1/8 of its lanes' chunks on a ragged end and the launch stays within
-        ``FOLDED_STAGING_BLOCKS`` workgroups; otherwise the widest power-of-two lane group that gives each lane
-        4 or more whole chunks (or a whole short row). Products streaming at most ``SPREAD_BYTES`` of
+        ``FOLDED_STAGING_BLOCKS`` workgroups (or the narrower layout would exceed them too); otherwise the
+        widest power-of-two lane group that gives each lane 4 or more whole chunks (or a whole short row).
+        Products streaming at most ``SPREAD_BYTES`` of
         weights take one row step per wave; larger ones take more only as far as needed to stay within
         ``FOLDED_STAGING_BLOCKS`` workgroups (up to ~32 chunks per lane in flight). A workgroup's stream is
         bounded by its compute unit's outstanding requests, so products go fastest spread over as many
@@ -1986,17 +1987,27 @@ class HIPCodegen(Codegen):
             steps = 1
             while steps < most and -(-rows_of_w // (64 // lanes * steps * 4)) > FOLDED_STAGING_BLOCKS:
                 steps += 1
+            if rows > 1 and -(-rows_of_w // (64 // lanes * steps * 4)) > FOLDED_STAGING_BLOCKS:
+                # out of reach: a product of several X rows then streams fastest one row step per wave over
+                # the most workgroups (C3's 8-row vocabulary product, 8 x 4 -> 8 x 1: forward 335.8 -> 318.7 us)
+                steps = 1
             return lanes, steps, -(-rows_of_w // (64 // lanes * steps * 4))
 
         wide = -(-chunks // 64)
+        whole_rows = None
         if chunks >= 64 and (wide * 64 - chunks) * 8 <= wide * 64:
             # 64 lanes per row (a ragged last chunk costs at most 1/8 of a lane's chunks): a wave covers one
             # row per step, so the product spreads over as many workgroups as its rows allow
-            chosen = plan(64)
-            if chosen is not None and chosen[2] <= FOLDED_STAGING_BLOCKS:
-                return chosen[0], chosen[1]
+            whole_rows = plan(64)
+            if whole_rows is not None and whole_rows[2] <= FOLDED_STAGING_BLOCKS:
+                return whole_rows[0], whole_rows[1]
         lanes = next((l for l in (64, 32, 16, 8, 4, 2) if chunks % l == 0 and chunks // l >= 4), 1)
         chosen = plan(lanes)
+        if whole_rows is not None and (chosen is None or chosen[2] > FOLDED_STAGING_BLOCKS):
+            # neither stays within FOLDED_STAGING_BLOCKS (a vocabulary-sized W): whole rows per load, 1 KiB
+            # of one row per wave instruction, stream faster than 8 rows x 128 B (GPT-OSS-20B unembedding,
+            # 1.16 GB: the decode step 40 us shorter)
+            return whole_rows[0], whole_rows[1]
         return None if chosen is None else (chosen[0], chosen[1])
 
     def _stream_blocks(self, columns: int, lanes: int, steps: int) -> int:
@@ -2178,7 +2189,7 @@ class HIPCodegen(Codegen):
     def _waves_attention(self, out, q, k_past, k_new, v_past, v_new, mask, sinks, scale, epilogue=None) -> Kernel:
         """The one-wave-per-query-head attention kernel. ``epilogue`` = (weight, bias, linear output, lanes,
         steps): the workgroup also multiplies its finished row (all heads, rounded as stored) by W^T from
-        LDS, with W requested once the attention is done."""
+        LDS (W requested before the attention when small, else once it is done)."""
         tokens, kv_heads, group, dim = q.shape
         keys = (k_past.shape[0] if k_past is not None else 0) + k_new.shape[0]
         bf16 = out.dtype == torch.bfloat16
@@ -2190,15 +2201,25 @@ class HIPCodegen(Codegen):
             prelude.append(lambda k: f"__shared__ float attention_row[{inner}];")
             store_extra = [f"attention_row[g * {dim}u + d] = chroma::storage_round<{str(bf16).lower()}>(value);"]
         k, _, _ = self._attention_kernel(out, q, k_past, k_new, v_past, v_new, mask, sinks, None, prelude=prelude, store_extra=store_extra)
+        # A small W is requested before the attention, so its round trip overlaps the attention's own loads;
+        # a large one once the attention is done (loads complete in order, see _stream_linear)
+        early = epilogue is not None and columns * inner * ITEMSIZE[weight.dtype] <= EARLY_FETCH_BYTES
+        fetch = []
+        if epilogue is not None:
+            fetch = [f"chroma::StreamStep<{inner}, {lanes}, {steps}, {ctype}> prefetched;",
+                     f"chroma::stream_block_fetch(prefetched, {self._matrix_slot(k, weight)}, {columns}u);"]
+        if early:
+            for line in fetch:
+                k.line(line)
         k.line(f"chroma::attention_waves<{dim}, {group}, {str(bf16).lower()}>({keys}u, {float_literal(scale)}, "
                "load_q, load_k, load_v, load_mask, load_sink, store);")
         if epilogue is not None:
             b_arg = self._matrix_slot(k, bias) if bias is not None else "nullptr"
             out_slot = k.slot(linear_out.name, linear_out.dtype, writable=True, extent=self.extents[linear_out.name])
             k.line("__syncthreads();")
-            # W is requested once the attention is done (see _stream_linear)
-            k.line(f"chroma::StreamStep<{inner}, {lanes}, {steps}, {ctype}> prefetched;")
-            k.line(f"chroma::stream_block_fetch(prefetched, {self._matrix_slot(k, weight)}, {columns}u);")
+            if not early:
+                for line in fetch:
+                    k.line(line)
             k.line(f"chroma::stream_block_linear<1, {inner}, {lanes}, {steps}, true, {ctype}>(nullptr, attention_row, "
                    f"{self._matrix_slot(k, weight)}, {b_arg}, {out_slot} + size_t(blockIdx.x) * {columns}u, {columns}u, prefetched);")
         return k
