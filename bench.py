@@ -21,6 +21,9 @@ Beside it the same line reports:
   prefill (matrix-core fraction on the work actually performed) and its decode step at a full
   4096-position cache (HBM fraction), with the oracle's time and parity on a reduced slice;
 * ``host``: CPU model, core counts, ROCm version and GPU name.
+
+``--only experts`` (not in the default line) times the C5 expert products alone against the vendor
+library's dense, grouped and per-expert GEMMs of the same FLOPs.
 """
 
 from __future__ import annotations
@@ -573,6 +576,94 @@ def bench_c5(work: Path, steps: int, cpu: bool) -> dict:
     return result
 
 
+# Expert slot counts of one layer of the C5 bench prefill (2048 tokens x top-4 over 32 experts), sorted:
+# the skewed routing the random-weight model actually produces in its later layers.
+C5_SKEWED_COUNTS = (0, 0, 0, 2, 4, 4, 9, 12, 13, 21, 21, 38, 46, 59, 90, 109, 144, 147, 148, 159, 164, 176, 210, 220,
+                    241, 269, 385, 427, 535, 1285, 1412, 1842)
+
+
+def bench_experts(work: Path) -> dict:
+    """The C5 expert products alone (up: [5760, 2880] per expert over the token rows; down: [2880, 2880] per
+    expert over the slot rows; bf16, 2048 tokens x top-4 of 32) on the hip backend (routing launch plus
+    the grouped matrix-core product), against the vendor library on the same work: one dense torch.mm of
+    the same FLOPs (hipBLASLt; it reads one expert's weights instead of all 32), torch._grouped_mm over
+    the experts' row groups, and one torch.mm per expert. Uniform routing (each token's 4 of 32 experts
+    drawn at random) and C5's measured skew."""
+    import numpy as np
+    import torch
+
+    import chroma_amd
+    from tests.helpers import numpy_of
+
+    experts, tokens, selected, inner = 32, 2048, 4, 2880
+
+    class Up(torch.nn.Module):
+        def __init__(self, w):
+            super().__init__()
+            self.w = torch.nn.Parameter(w, requires_grad=False)
+
+        def forward(self, indices, x):
+            return torch.einsum("beck,bk->bec", self.w[indices], x)
+
+    class Down(Up):
+        def forward(self, indices, x):
+            return torch.einsum("beck,bek->bec", self.w[indices], x)
+
+    def cuda_us(fn, runs: int = 20) -> float:
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(runs):
+            fn()
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / runs * 1e3
+
+    generator = torch.Generator().manual_seed(0)
+    uniform = torch.stack([torch.randperm(experts, generator=generator)[:selected] for _ in range(tokens)])
+    order = torch.repeat_interleave(torch.arange(experts), torch.tensor(C5_SKEWED_COUNTS))
+    skewed = torch.empty(tokens * selected, dtype=torch.int64)
+    # expert runs laid over (slot, token) in token-fastest order, so a run of at most 2048 ids meets each token once
+    skewed[(torch.arange(tokens * selected) % tokens) * selected + torch.arange(tokens * selected) // tokens] = order
+    routings = {"uniform": uniform, "c5_skewed": skewed.reshape(tokens, selected)}
+    result = {"workload": "C5 expert products, bf16, 2048 tokens x top-4 of 32 experts, K = 2880", "products": {}}
+    for name, channels, per_slot in (("up", 5760, False), ("down", 2880, True)):
+        w = (torch.randn(experts, channels, inner, generator=generator) * 0.02).to(torch.bfloat16)
+        x = torch.randn(*((tokens, selected, inner) if per_slot else (tokens, inner)), generator=generator).to(torch.bfloat16)
+        flops = 2 * tokens * selected * channels * inner
+        entry = {"flops": flops, "hip": {}}
+        for label, indices in routings.items():
+            module = (Down if per_slot else Up)(w)
+            with chroma_amd.compile(torch.export.export(module, (indices, x)), work / f"{name}_{label}") as program:
+                program.native.upload([indices.numpy(), numpy_of(x)])
+                us = device_ms(program, 20) * 1e3
+            counts = np.bincount(indices.numpy().ravel(), minlength=experts)
+            entry["hip"][label] = {"us": round(us, 1), "frac": round(flops / (us * 1e-6) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4),
+                                   "slots_per_expert_min_max": [int(counts.min()), int(counts.max())]}
+        wd = w.cuda()
+        rows = tokens * selected
+        xd = torch.randn(rows, inner, device="cuda", dtype=torch.bfloat16)
+        dense = wd[0].contiguous()
+        library = {"dense_mm_same_flops": cuda_us(lambda: torch.mm(xd, dense.t()))}
+        offsets = torch.arange(1, experts + 1, device="cuda", dtype=torch.int32) * (rows // experts)
+        if hasattr(torch, "_grouped_mm"):
+            try:
+                library["grouped_mm_uniform_groups"] = cuda_us(lambda: torch._grouped_mm(xd, wd.transpose(-2, -1), offs=offsets))
+            except Exception as error:  # noqa: BLE001 - reported in the JSON line
+                library["grouped_mm_uniform_groups"] = f"{type(error).__name__}: {str(error)[:120]}"
+        parts = xd.view(experts, rows // experts, inner)
+        library["mm_per_expert_uniform_groups"] = cuda_us(lambda: [torch.mm(parts[e], wd[e].t()) for e in range(experts)])
+        entry["library_us"] = {key: round(value, 1) if isinstance(value, float) else value for key, value in library.items()}
+        entry["library_frac"] = {key: round(flops / (value * 1e-6) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4)
+                                 for key, value in library.items() if isinstance(value, float)}
+        result["products"][name] = entry
+        del wd, xd, dense
+        torch.cuda.empty_cache()
+    return result
+
+
 def c5_slice(work: Path) -> dict:
     """C5 at full width on a reduced slice, hip beside the oracle: 2 layers (one sliding-window layer
     [window 16 at this context], one full layer), all 32 experts, a 64-position cache, a 32-token prefill
@@ -832,7 +923,8 @@ def main() -> None:
     parser.add_argument("--no-c5", action="store_true", help="skip the GPT-OSS-20B-shaped model (about two minutes: 42 GB of weights)")
     parser.add_argument("--counters", nargs="?", const="c2", choices=["c2", "c5", "c5prefill", "rows", "c1", "dev", "decode"],
                         help="only replay one plan (C2 kernel by default; c5 = the C5 decode step) and a copy kernel, for rocprofv3 --pmc")
-    parser.add_argument("--only", choices=["c1", "rows", "dev", "decode", "c5"], help="measure one leg and print it")
+    parser.add_argument("--only", choices=["c1", "rows", "dev", "decode", "c5", "experts"],
+                        help="measure one leg and print it (experts: the C5 expert products against the vendor library)")
     args = parser.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the hip backend is single-device (every GPU box here has one GPU)", file=sys.stderr)
@@ -846,7 +938,8 @@ def main() -> None:
             return
         if args.only:
             legs = {"c1": lambda: bench_c1(work, cpu), "rows": lambda: bench_rows(work, cpu), "dev": lambda: bench_dev(work, cpu),
-                    "decode": lambda: bench_decode(work, 32, cpu), "c5": lambda: bench_c5(work, 16, cpu)}
+                    "decode": lambda: bench_decode(work, 32, cpu), "c5": lambda: bench_c5(work, 16, cpu),
+                    "experts": lambda: bench_experts(work)}
             print(json.dumps({args.only: legs[args.only]()}), flush=True)
             return
         c2 = bench_c2(args, work)
