@@ -98,6 +98,9 @@ NORM_EPILOGUES = True
 # A stored map reading only weights and graph inputs is launched once per distinct kernel and bindings
 # (``_constant_map``). False launches every one.
 CONSTANT_MAPS = True
+# A concatenation of equal parts along the innermost dimension writes every part's element at one position from
+# one thread (``_concat_kernel``). False keeps one part per thread.
+PAIRED_CONCAT = True
 REUSED_EVALUATIONS = 1 << 18  # a contraction operand is stored when (elements x reuse) reaches this
 SMALL_REDUCTION = 8  # contractions summing at most this many products are fused expressions...
 SMALL_OPERAND_COST = 8  # ...over operands that cost at most this much per element (others are stored)
@@ -661,6 +664,21 @@ class HIPCodegen(Codegen):
         count = math.prod(shape)
         k = Kernel(lanes)
         slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
+        size = values[0].shape[dim]
+        if (PAIRED_CONCAT and innermost and lanes > 1 and len(values) > 1 and size % lanes == 0
+                and all(value.shape[dim] == size for value in values)):
+            # Equal parts along the innermost dimension (the two halves of a rotary embedding): a thread
+            # writes the same position of every part, so what the parts read in common (x1, x2, cos, sin)
+            # is loaded once.
+            vectors = count // lanes // len(values)
+            with k.block(f"for (uint32_t v = blockIdx.x * {MAP_THREADS}u + threadIdx.x; v < {vectors}u; v += gridDim.x * {MAP_THREADS}u) {{"):
+                v = Atom("v", vectors - 1)
+                coords = k.unflatten(Aff.of(v), shape[:-1] + (size // lanes,))
+                coords[-1] = Aff.of(k.vector_atom(f"({coords[-1].code()}) * {lanes}u", size - 1))
+                for i, value in enumerate(values):
+                    node = self.read(k, value, coords)
+                    k.store(slot, out.dtype, Kernel.flatten(coords[:-1] + [coords[-1] + i * size], shape), node)
+            return k, max(1, min(-(-vectors // MAP_THREADS), MAP_GRID))
         vectors = count // lanes
         with k.block(f"for (uint32_t v = blockIdx.x * {MAP_THREADS}u + threadIdx.x; v < {vectors}u; v += gridDim.x * {MAP_THREADS}u) {{"):
             v = Atom("v", vectors - 1)

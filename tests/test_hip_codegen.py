@@ -221,6 +221,27 @@ def test_staging_loops_request_every_trip_before_their_arithmetic():
         assert source.count(f"{array}[trip]") >= 2  # ... and read in the arithmetic loop
 
 
+def test_rotary_halves_are_written_by_one_thread():
+    """A rotary embedding's concatenation of two equal halves along the last dimension: one thread writes
+    both halves of a position (half as many vectors, two 16-byte stores, no branch on the part), and the
+    loads the halves share (x1, x2, cos, sin) appear once."""
+
+    def rotary(x, cos, sin):
+        x1, x2 = x[..., :32], x[..., 32:]
+        return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1)
+
+    x = torch.randn(256, 8, 64).to(torch.bfloat16)
+    cos, sin = torch.randn(256, 1, 32).to(torch.bfloat16), torch.randn(256, 1, 32).to(torch.bfloat16)
+    source = lower(Function(rotary), x, cos, sin).files["model.hip"]
+    kernel = source[source.index("chroma_concat_"):]
+    kernel = kernel[: kernel.index("\n}\n")]
+    assert f"v < {256 * 8 * 64 // 8 // 2}u" in kernel
+    assert kernel.count("*reinterpret_cast<uint4*>(b0 + ") == 2
+    assert "if (j" not in kernel
+    loads = re.findall(r"reinterpret_cast<const uint4\*>\((b\d+ \+ [^)]*)\)", kernel)
+    assert len(loads) == len(set(loads)) == 4  # x1, x2, cos, sin: 16 bytes each, once
+
+
 @pytest.mark.parametrize("dtype, dim", [(torch.float32, 128), (torch.bfloat16, 256)])
 def test_long_cache_attention_with_wide_heads_cross_compiles(tmp_path, dtype, dim):
     """Head dimensions whose split would give a decode-attention thread more than 8 keys take the general

@@ -468,6 +468,36 @@ def test_reductions_softmax_gather_cat_triangular_norm_and_einsum(tmp_path, dtyp
     check(tmp_path / "norm", RMSNorm(17).to(dtype).eval(), torch.randn(5, 17).to(dtype))
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rotary_concatenation_of_equal_parts(tmp_path, dtype):
+    """A rotary embedding's cat(x1 cos - x2 sin, x2 cos + x1 sin) along the last dimension, large enough for
+    the concatenation kernel: the equal-parts form (one thread writes both halves of a position) against the
+    oracle and eager torch, bit-identical to one part per thread; a cat of unequal parts takes the
+    per-part form."""
+    from chroma_amd._src.codegen import hip as hipgen
+
+    def rotary(x, cos, sin):
+        x1, x2 = x[..., :32], x[..., 32:]
+        return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1), torch.cat((x1 * cos, x), dim=-1)
+
+    generator = torch.Generator().manual_seed(12)
+    x = torch.randn(256, 8, 64, generator=generator).to(dtype)
+    angles = torch.arange(256, dtype=torch.float32)[:, None, None] * torch.rand(1, 1, 32, generator=generator)
+    cos, sin = torch.cos(angles).to(dtype), torch.sin(angles).to(dtype)
+    check(tmp_path / "rotary", Function(rotary), x, cos, sin)
+    exported = torch.export.export(Function(rotary), (x, cos, sin))
+    results = []
+    try:
+        for paired in (True, False):
+            hipgen.PAIRED_CONCAT = paired
+            with chroma_amd.compile(exported, tmp_path / f"paired_{paired}") as model:
+                results.append([np.array(a, copy=True) for a in leaves(model(x, cos, sin))])
+    finally:
+        hipgen.PAIRED_CONCAT = True
+    for got, want in zip(*results):
+        np.testing.assert_array_equal(got.view(np.uint8), want.view(np.uint8))
+
+
 def test_int64_gather_cat_masks_bounds_and_recovery(tmp_path):
     def fn(x, ids):
         selected = x[ids]
