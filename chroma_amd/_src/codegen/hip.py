@@ -78,6 +78,12 @@ WIDE_GEMM_TILE = (256, 192)  # chroma::kWideM, kWideN
 # the wide body takes dense products with at least this many of its tiles: below that its larger tiles
 # leave too much of the chip idle and the 128 x 128 body is faster
 WIDE_GEMM_MIN_TILES = 200
+# below that, products with at least this many 128 x 192 tiles take the mid ring body (chroma::kMidThreads
+# 4 waves, one 100 KiB-LDS workgroup per CU); smaller ones the 128 x 128 direct body
+MID_GEMM_TILE = (128, 192)  # chroma::kMidM, kMidN
+MID_GEMM_THREADS = 256
+MID_GEMM_MIN_TILES = 160
+MID_GEMMS = True
 # bfloat16 expert products whose channel count is a multiple of a tile width here (the first that fits)
 # take the ring body (chroma::grouped_expert_linear PATH 3) on 128-slot x width tiles with that many waves
 # side by side (each wave all slots of a width / waves strip), and an expert's last tile holds up to the
@@ -2103,6 +2109,12 @@ class HIPCodegen(Codegen):
             k.min_waves = 1
             k.line(f"chroma::mfma_linear_wide<{ctype_of(out.dtype)}>({args[0]}, {args[1]}, {args[2]}, {out_slot}, {rows}u, {columns}u, {inner}u);")
             self.launch(k, 8 * -(-wide_tiles // 8), WIDE_GEMM_THREADS, [x, weight] + ([bias] if bias is not None else []), kind="linear_wide")
+            return
+        mid_tiles = -(-rows // MID_GEMM_TILE[0]) * -(-columns // MID_GEMM_TILE[1])
+        if MID_GEMMS and out.dtype == torch.bfloat16 and inner % 32 == 0 and mid_tiles >= MID_GEMM_MIN_TILES:
+            k.min_waves = 1
+            k.line(f"chroma::mfma_linear_mid<{ctype_of(out.dtype)}>({args[0]}, {args[1]}, {args[2]}, {out_slot}, {rows}u, {columns}u, {inner}u);")
+            self.launch(k, 8 * -(-mid_tiles // 8), MID_GEMM_THREADS, [x, weight] + ([bias] if bias is not None else []), kind="linear_mid")
             return
         if self._direct_gemm(out.dtype, inner):
             path, threads = 2, DIRECT_GEMM_THREADS

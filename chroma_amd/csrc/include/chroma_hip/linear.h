@@ -1430,6 +1430,31 @@ __device__ __forceinline__ void mfma_linear_wide(const T* __restrict__ x, const 
                       tx * kWideN);
 }
 
+// A linear layer on the ring body in kMidM x kMidN (128 x 192) tiles on 2 x 2 waves (each a 64 x 96 part,
+// 24 accumulator tiles) with a 5-slot ring (100 KiB of LDS): the products whose 256 x 192 tiles would leave
+// much of the chip idle (C5's output projection, 2048 x 2880 x 4096: 120 wide tiles against 240 of these,
+// 78.2 -> 58.2 us in isolation, the 128 x 128 direct body 63.0 us). Launched as 8 * ceil(tiles / 8)
+// workgroups of kMidThreads; logical tiles run down groups of 8 row tiles before the next column tile.
+constexpr uint32_t kMidThreads = 256, kMidM = 128, kMidN = 192;
+
+template <class T>
+__device__ __forceinline__ void mfma_linear_mid(const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias,
+                                                T* __restrict__ out, uint32_t m_total, uint32_t n_total, uint32_t k_total) {
+    const uint32_t gx = (n_total + kMidN - 1u) / kMidN, gy = (m_total + kMidM - 1u) / kMidM;
+    uint32_t logical;
+    if (!xcd_logical_tile(gx * gy, logical)) {
+        return;
+    }
+    constexpr uint32_t G = 8;
+    const uint32_t group = logical / (G * gx), first = group * G;
+    const uint32_t height = gy - first < G ? gy - first : G;
+    const uint32_t within = logical - group * G * gx;
+    const uint32_t ty = first + within % height, tx = within / height;
+    __shared__ __attribute__((aligned(1024))) uint16_t ring[ring_elements<kMidM, kMidN, 5>()];
+    mfma_gemm_ring<T, kMidM, kMidN, 2, 2, 5>(x, k_total, w, k_total, bias, out, n_total, m_total, n_total, k_total, nullptr, nullptr,
+                                             ty * kMidM, tx * kMidN, 1u, ring);
+}
+
 // Y[M, N] = X[M, K] . W[N, K]^T (+ bias[N]) for few columns (N <= 64: a router's gate) and many rows: one
 // workgroup of 4 waves per 16 rows of X, the waves splitting K into quarters; the matrix-core operands are
 // read straight from global memory (each X row once, W - N x K, small - from L2), 8 k-steps of loads in

@@ -106,11 +106,13 @@ def test_linear_kernel_selection():
     assert "mfma_linear<uint16_t, 2>" in direct and "__launch_bounds__(512, 2)" in direct
     assert "mfma_linear<uint16_t, 0>" in lower(torch.nn.Linear(40, 7).bfloat16().eval(), torch.ones(40, 40, dtype=torch.bfloat16)).files["model.hip"]
     # products with at least 200 of the wide body's 256 x 192 tiles take it (4 waves, one workgroup per CU);
-    # one tile row fewer keeps the 128 x 128 body
+    # one tile row fewer takes the mid ring body (at least 160 tiles of 128 x 192), fewer tiles the 128 x 128 body
     wide = lower(torch.nn.Linear(32, 4800).bfloat16().eval(), torch.ones(2048, 32, dtype=torch.bfloat16)).files["model.hip"]
     assert "chroma::mfma_linear_wide<uint16_t>" in wide and "__launch_bounds__(256, 1)" in wide
     narrow = lower(torch.nn.Linear(32, 4800).bfloat16().eval(), torch.ones(1792, 32, dtype=torch.bfloat16)).files["model.hip"]
-    assert "mfma_linear_wide" not in narrow
+    assert "mfma_linear_wide" not in narrow and "chroma::mfma_linear_mid<uint16_t>" in narrow
+    small = lower(torch.nn.Linear(32, 4800).bfloat16().eval(), torch.ones(640, 32, dtype=torch.bfloat16)).files["model.hip"]
+    assert "mfma_linear_mid" not in small and "mfma_linear<uint16_t, 0>" in small
     # bfloat16 keeps float accumulation in both paths
     generated = lower(torch.nn.Linear(17, 7).bfloat16().eval(), torch.ones(3, 5, 17, dtype=torch.bfloat16))
     assert generated.inputs[0]["dtype"] == "bfloat16" and generated.outputs[0]["dtype"] == "bfloat16"

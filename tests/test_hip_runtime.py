@@ -247,6 +247,26 @@ def test_wide_matrix_core_linear(tmp_path, rows, inner, columns):
     assert_close(got, want, **tolerance(want))
 
 
+@pytest.mark.parametrize("rows, inner, columns", [(2048, 256, 2880), (1700, 96, 4003), (2000, 32, 1999)])
+def test_mid_matrix_core_linear(tmp_path, rows, inner, columns):
+    """bfloat16 products too small for 200 wide tiles on the mid ring body (128 x 192 tiles, 4 waves, 5-slot
+    ring) against the oracle: C5's output-projection shape in whole tiles; ragged rows with an odd column
+    count; and K = 32, a single stage."""
+    generator = torch.Generator().manual_seed(rows + inner + columns)
+    layer = torch.nn.Linear(inner, columns).eval()
+    with torch.no_grad():
+        layer.weight.copy_(torch.randn(columns, inner, generator=generator) * 0.05)
+        layer.bias.copy_(torch.randn(columns, generator=generator))
+    layer = layer.to(torch.bfloat16)
+    x = torch.randn(rows, inner, generator=generator).to(torch.bfloat16)
+    exported = torch.export.export(layer, (x,))
+    with chroma_amd.compile(exported, tmp_path / "hip") as model:
+        assert "chroma::mfma_linear_mid<uint16_t>" in (tmp_path / "hip" / "model.hip").read_text()
+        got = model(x)
+    want = compile_cpu(exported, tmp_path / "cpu")(numpy_of(x))
+    assert_close(got, want, **tolerance(want))
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_matrix_core_contractions(tmp_path, dtype):
     """Attention-shaped einsums on the batched MFMA path: k-contiguous and n-contiguous right operands,
