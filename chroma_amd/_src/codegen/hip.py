@@ -84,6 +84,12 @@ MID_GEMM_TILE = (128, 192)  # chroma::kMidM, kMidN
 MID_GEMM_THREADS = 256
 MID_GEMM_MIN_TILES = 160
 MID_GEMMS = True
+# A matrix-core linear whose weights (a constant) take this many bytes or more, up to a quarter of the 256 MB
+# memory-side cache, is preceded by a launch that reads them (chroma::prefetch_bytes): its copy ring then
+# finds them in that cache instead of waiting an HBM round trip per stage
+PREFETCH_WEIGHT_BYTES = (4 << 20, 64 << 20)
+PREFETCH_BLOCKS = 2048
+WEIGHT_PREFETCH = True
 # bfloat16 expert products whose channel count is a multiple of a tile width here (the first that fits)
 # take the ring body (chroma::grouped_expert_linear PATH 3) on 128-slot x width tiles with that many waves
 # side by side (each wave all slots of a width / waves strip), and an expert's last tile holds up to the
@@ -239,6 +245,7 @@ class HIPCodegen(Codegen):
         self.reused_maps = 0
         self.last_norm: Optional[dict] = None  # the last one-workgroup-per-row RMSNorm launch
         self.norm_epilogues = 0
+        self.weight_prefetches = 0
 
     # ===================================================================================== storage
     def extern(self, tensor: torch.Tensor, kind: str, offset: int) -> Value:
@@ -2095,7 +2102,21 @@ class HIPCodegen(Codegen):
         )
         self.launch(k, blocks, 256, [x, weight] + ([bias] if bias is not None else []), kind="linear_skinny")
 
+    def _prefetch_weight(self, weight: Value) -> None:
+        """Launch ``prefetch_bytes`` over a constant weight of PREFETCH_WEIGHT_BYTES (see there)."""
+        size = math.prod(weight.shape) * ITEMSIZE[weight.dtype]
+        offset = weight.view.offset * ITEMSIZE[weight.dtype] if weight.view is not None else 0
+        low, high = PREFETCH_WEIGHT_BYTES
+        if (not WEIGHT_PREFETCH or not low <= size <= high or offset % 16 or not weight.stored
+                or self.binding_of(weight.root.name).kind != "weight"):
+            return
+        k = Kernel(1)
+        k.line(f"chroma::prefetch_bytes({self._matrix_slot(k, weight)}, {size - size % 16}ull);")
+        self.launch(k, min(-(-size // (16 * 256)), PREFETCH_BLOCKS), 256, [weight], kind="prefetch")
+        self.weight_prefetches += 1
+
     def _mfma_linear(self, out, x, weight, bias, rows, columns, inner) -> None:
+        self._prefetch_weight(weight)
         k = Kernel(1)
         args = [self._matrix_slot(k, x), self._matrix_slot(k, weight), self._matrix_slot(k, bias) if bias is not None else "nullptr"]
         out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
@@ -3135,6 +3156,7 @@ class HIPCodegen(Codegen):
             unstored_products=self.unstored_products,
             reused_maps=self.reused_maps,
             norm_epilogues=self.norm_epilogues,
+            weight_prefetches=self.weight_prefetches,
             small_contractions=self.small_contractions,
             attention_epilogues=self.attention_epilogues,
             write_through_stores=len(self.write_through_stores),

@@ -206,6 +206,20 @@ __device__ __forceinline__ void coop_depart(unsigned long long* slots, unsigned 
 }
 
 // ---------------------------------------------------------------------------------------------
+// Reads ``bytes`` (a multiple of 16) at ``p`` and discards them: a weight stream of the next launch is then
+// served from the memory-side cache (MALL) instead of HBM. A matrix-core product's copy ring has a few
+// stages in flight, so with cold weights every stage waits for an HBM round trip (C5's QKV product: 81 us
+// cold, 66 us warm); the read-ahead itself streams at HBM rate. Grid-stride, 16 bytes per thread per trip.
+__device__ __forceinline__ void prefetch_bytes(const void* __restrict__ p, size_t bytes) {
+    const uint4* v = static_cast<const uint4*>(p);
+    const size_t count = bytes / 16u;
+    for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += size_t(gridDim.x) * blockDim.x) {
+        const uint4 word = v[i];
+        __asm__ volatile("" ::"v"(word.x), "v"(word.y), "v"(word.z), "v"(word.w));
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Streaming (non-temporal) vector stores for results no later instruction of the same kernel reads.
 typedef float float2_nt __attribute__((ext_vector_type(2)));
 typedef float float4_nt __attribute__((ext_vector_type(4)));

@@ -120,6 +120,20 @@ def test_linear_kernel_selection():
     assert "chroma::tiled_linear<uint16_t>" in source  # float accumulators, one bf16 rounding at the store
 
 
+def test_large_weights_are_read_ahead_of_their_matrix_core_product():
+    """Matrix-core linears over 4-64 MiB of constant weights get a read-ahead launch (chroma_prefetch) just
+    before them; smaller weights, streamed few-row products and weights computed in the graph do not."""
+    big = lower(torch.nn.Linear(2048, 2048, bias=False).bfloat16().eval(), torch.ones(512, 2048, dtype=torch.bfloat16))
+    plan = [line.split()[1] for line in big.files["model.plan"].splitlines() if line.startswith("launch ")]
+    assert big.stats["weight_prefetches"] == 1 and plan[0].startswith("chroma_prefetch_") and len(plan) == 2
+    assert "chroma::prefetch_bytes(" in big.files["model.hip"] and f"{2048 * 2048 * 2}ull" in big.files["model.hip"]
+    small = lower(torch.nn.Linear(1024, 1024, bias=False).bfloat16().eval(), torch.ones(512, 1024, dtype=torch.bfloat16))
+    few = lower(torch.nn.Linear(2048, 2048, bias=False).bfloat16().eval(), torch.ones(2, 2048, dtype=torch.bfloat16))
+    computed = lower(Function(lambda x, w: torch.nn.functional.linear(x, w * 2)), torch.ones(512, 2048).bfloat16(),
+                     torch.ones(2048, 2048).bfloat16())
+    assert small.stats["weight_prefetches"] == few.stats["weight_prefetches"] == computed.stats["weight_prefetches"] == 0
+
+
 def test_shared_expressions_and_workspace_reuse():
     def fn(x, w):
         first = torch.nn.functional.linear(x, w)

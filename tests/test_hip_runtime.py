@@ -267,6 +267,23 @@ def test_mid_matrix_core_linear(tmp_path, rows, inner, columns):
     assert_close(got, want, **tolerance(want))
 
 
+def test_prefetched_weights_linear(tmp_path):
+    """A matrix-core linear over 8 MiB of weights is preceded by a launch that reads them into the
+    memory-side cache; the product, run twice, matches the oracle."""
+    generator = torch.Generator().manual_seed(31)
+    layer = torch.nn.Linear(2048, 2048, bias=False).eval()
+    with torch.no_grad():
+        layer.weight.copy_(torch.randn(2048, 2048, generator=generator) * 0.02)
+    layer = layer.to(torch.bfloat16)
+    x = torch.randn(512, 2048, generator=generator).to(torch.bfloat16)
+    exported = torch.export.export(layer, (x,))
+    want = compile_cpu(exported, tmp_path / "cpu")(numpy_of(x))
+    with chroma_amd.compile(exported, tmp_path / "hip") as model:
+        assert model.stats["weight_prefetches"] == 1 and model.stats["launches"] == 2
+        for _ in range(2):
+            assert_close(model(x), want, **tolerance(want))
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_matrix_core_contractions(tmp_path, dtype):
     """Attention-shaped einsums on the batched MFMA path: k-contiguous and n-contiguous right operands,
