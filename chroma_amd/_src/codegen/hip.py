@@ -84,9 +84,9 @@ MID_GEMM_TILE = (128, 192)  # chroma::kMidM, kMidN
 MID_GEMM_THREADS = 256
 MID_GEMM_MIN_TILES = 160
 MID_GEMMS = True
-# A matrix-core linear whose weights (a constant) take this many bytes or more, up to a quarter of the 256 MB
-# memory-side cache, is preceded by a launch that reads them (chroma::prefetch_bytes): its copy ring then
-# finds them in that cache instead of waiting an HBM round trip per stage
+# A matrix-core linear (other than the wide body) whose weights (a constant) take this many bytes or more, up
+# to a quarter of the 256 MB memory-side cache, is preceded by a launch that reads them (chroma::prefetch_bytes):
+# its copy ring then finds them in that cache instead of waiting an HBM round trip per stage
 PREFETCH_WEIGHT_BYTES = (4 << 20, 64 << 20)
 PREFETCH_BLOCKS = 2048
 WEIGHT_PREFETCH = True
@@ -2116,7 +2116,10 @@ class HIPCodegen(Codegen):
         self.weight_prefetches += 1
 
     def _mfma_linear(self, out, x, weight, bias, rows, columns, inner) -> None:
-        self._prefetch_weight(weight)
+        if not self._wide_gemm(out.dtype, inner, rows, columns):
+            # (the wide body's C5 QKV product gains 3.4 us from warm weights, less than the 6.6 us read-ahead;
+            # the mid body's output projection 15 us for 5.5)
+            self._prefetch_weight(weight)
         k = Kernel(1)
         args = [self._matrix_slot(k, x), self._matrix_slot(k, weight), self._matrix_slot(k, bias) if bias is not None else "nullptr"]
         out_slot = k.slot(out.name, out.dtype, writable=True, extent=self.extents[out.name])
