@@ -2582,7 +2582,7 @@ class HIPCodegen(Codegen):
             pow2 = mantissa == 0.5 and -64 <= exponent <= 1
             k.line(f"chroma::attention_heads_mfma_bf16<{dim}, {group}, {'true' if pow2 else 'false'}>(a);")
             operands = [entry[0] for entry in plan.values() if entry is not None] + [live]
-            self.launch(k, (-(-tokens // 16), kv_heads, 1), 64 * group, operands, kind="attention_heads")
+            self.launch(k, (kv_heads, -(-tokens // 16), 1), 64 * group, operands, kind="attention_heads")
         else:
             live = self._live_blocks(plan["mask"], tokens, keys) if shared_mask else None
             if live is not None:
@@ -2594,7 +2594,7 @@ class HIPCodegen(Codegen):
             # SIMD fit without spills up to D = 64 (D = 128 would spill)
             k.min_waves = 5 if dim <= 64 else 0
             operands = [entry[0] for entry in plan.values() if entry is not None] + ([live] if live is not None else [])
-            self.launch(k, (-(-tokens // 64), kv_heads * group, 1), 256, operands, kind="attention_mfma")
+            self.launch(k, (kv_heads * group, -(-tokens // 64), 1), 256, operands, kind="attention_mfma")
         self.fused_attentions += 1
         self.mfma_matmuls += 1
         return True

@@ -707,7 +707,7 @@ __device__ __forceinline__ void attention_combine(const float* partial, uint32_t
 // Matrix-core attention for long bfloat16 query blocks (the prefill of a cached export): the same
 // computation as ``attention_rows`` with the two contractions on v_mfma_f32_16x16x32_bf16.
 //
-// Workgroup: 4 waves = 64 queries of one head (grid.x: query blocks, grid.y: kv_head * group + g);
+// Workgroup: 4 waves = 64 queries of one head (grid.x: kv_head * group + g, grid.y: query blocks);
 // keys in blocks of 32, staged in LDS (K row-major, V transposed). Each wave computes
 // S^T[32 keys x 16 queries] = K . Q^T as two 16 x 16 tiles (lane l ends with keys 4(l/16)+r and
 // 16+4(l/16)+r of query l%16), so its own accumulators, rounded, become the B operand of
@@ -770,9 +770,10 @@ template <int D> __device__ __forceinline__ void attention_mfma_bf16(const Atten
     __shared__ uint16_t live_list[kLiveListMax];
     __shared__ uint32_t live_total;
     const uint32_t tid = threadIdx.x, lane = tid % 64u, wave = tid / 64u, quad = lane / 16u, col = lane % 16u;
-    const uint32_t head = blockIdx.y, kv = head / a.group, g = head % a.group;
-    // Later query blocks see more keys under a causal mask: they are dispatched first.
-    const uint32_t query_block = gridDim.x - 1u - blockIdx.x;
+    // grid (query heads, query blocks), dispatched x fastest: later query blocks see more keys under a causal
+    // mask, and every head's are dispatched before any head's earlier ones
+    const uint32_t head = blockIdx.x, kv = head / a.group, g = head % a.group;
+    const uint32_t query_block = gridDim.y - 1u - blockIdx.y;
     const uint32_t block_q0 = query_block * 64u;
     const uint32_t query = block_q0 + wave * 16u + col;
     const bool live = query < a.tokens;
@@ -1073,8 +1074,10 @@ template <int D, int G, bool POW2> __device__ __forceinline__ void attention_hea
     __shared__ uint16_t live_list[kLiveTilesMax];
     __shared__ uint32_t live_total;
     const uint32_t tid = threadIdx.x, lane = tid % 64u, g = tid / 64u, quad = lane / 16u, col = lane % 16u;
-    const uint32_t kv = blockIdx.y;
-    const uint32_t tile = gridDim.x - 1u - blockIdx.x;  // later query tiles see more keys: dispatched first
+    // grid (KV heads, query tiles): workgroups are dispatched x fastest, so every head's tile t is dispatched
+    // before any head's tile t - 1, and later query tiles (more keys) go first across all heads
+    const uint32_t kv = blockIdx.x;
+    const uint32_t tile = gridDim.y - 1u - blockIdx.y;
     const uint32_t q0 = tile * QT, query = q0 + col;
     const bool live = query < a.tokens;
     const uint32_t qrow = live ? query : a.tokens - 1u;
