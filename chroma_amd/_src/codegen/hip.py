@@ -126,6 +126,12 @@ ATTENTION_TICKETS = 64  # (query row, head) rows a split-key decode attention ca
 NARROW_COLUMNS = 64  # linears of at most this many columns over many rows take one workgroup per 16 rows
 SMALL_INPUT_BYTES = 64 << 10  # inputs up to this size are staged ahead of the larger ones
 MATRIX_ATTENTION_TOKENS = 64  # bfloat16 attention over at least this many queries runs on the matrix cores
+# query heads per wave of the grouped prefill attention (attention_heads): two share each K and V^T fragment
+# read from LDS, whose bandwidth bounds the one-head form; compiled for 3 resident workgroups per compute unit
+# (170 registers: unbounded it takes 204 and 2 fit, at 4 it spills). C5 full layer 132 -> 125 us standalone,
+# a 4-layer prefill slice 5.945 -> 5.890 ms, bit-identical
+ATTENTION_HEADS_PER_WAVE = 2
+ATTENTION_HEADS_MIN_BLOCKS = 3
 SPLIT_KEYS = 256  # keys per workgroup when an attention row's keys are split over workgroups
 DECODE_SPLIT_KEYS = 128  # the same for stored key/value rows read with 16-byte loads (decode steps)
 WAVE_ATTENTION_KEYS = 1024  # up to this many keys, attention runs one wave per query head
@@ -2580,9 +2586,11 @@ class HIPCodegen(Codegen):
             # a power-of-two scale <= 1 makes the scaled score a bfloat16 value: its rounding is left out
             mantissa, exponent = math.frexp(scale)
             pow2 = mantissa == 0.5 and -64 <= exponent <= 1
-            k.line(f"chroma::attention_heads_mfma_bf16<{dim}, {group}, {'true' if pow2 else 'false'}>(a);")
+            per_wave = ATTENTION_HEADS_PER_WAVE if group % ATTENTION_HEADS_PER_WAVE == 0 else 1
+            k.min_waves = ATTENTION_HEADS_MIN_BLOCKS if per_wave > 1 else 0
+            k.line(f"chroma::attention_heads_mfma_bf16<{dim}, {group}, {'true' if pow2 else 'false'}, {per_wave}>(a);")
             operands = [entry[0] for entry in plan.values() if entry is not None] + [live]
-            self.launch(k, (kv_heads, -(-tokens // 16), 1), 64 * group, operands, kind="attention_heads")
+            self.launch(k, (kv_heads, -(-tokens // 16), 1), 64 * group // per_wave, operands, kind="attention_heads")
         else:
             live = self._live_blocks(plan["mask"], tokens, keys) if shared_mask else None
             if live is not None:

@@ -1003,8 +1003,11 @@ template <int D> __device__ __forceinline__ void attention_mfma_bf16(const Atten
 
 // ---------------------------------------------------------------------------------------------
 // Matrix-core attention for long bfloat16 prefills, one workgroup per (16-query tile, key/value head) and
-// one wave per query head of the group: the K tile, the V^T tile and the mask tile of each 64-key block are
-// staged into LDS once and serve all G heads (the head-parallel form stages them once per head). Mask
+// one wave per HPW query heads of the group: the K tile, the V^T tile and the mask tile of each 64-key block
+// are staged into LDS once and serve all G heads (the head-parallel form stages them once per head). With
+// HPW = 2 every K and V^T fragment a wave reads from LDS feeds the products of both its heads, halving the
+// LDS reads per score (which bound the one-head form); each head's arithmetic is unchanged, so the results
+// are bit-identical. Mask
 // shared by every head (mh = mg = 0). Same computation as attention_mfma_bf16 and the reference chain:
 // S^T = K . Q^T on v_mfma_f32_16x16x32_bf16, each score rounded to bfloat16, scaled and rounded, masked
 // and rounded (gfx950's v_cvt_pk_bf16_f32 rounds two values at once, to nearest even like f32_to_bf16);
@@ -1054,9 +1057,10 @@ __device__ __forceinline__ void attention_live_tiles(const uint16_t* __restrict_
     }
 }
 
-template <int D, int G, bool POW2> __device__ __forceinline__ void attention_heads_mfma_bf16(const AttentionOperands& a) {
+template <int D, int G, bool POW2, int HPW = 1> __device__ __forceinline__ void attention_heads_mfma_bf16(const AttentionOperands& a) {
     static_assert(D % 32 == 0 && D <= 128 && G >= 1 && G <= 8, "head dimension and group");
-    constexpr int QT = 16, KB = 64, THREADS = 64 * G;
+    static_assert((HPW == 1 || HPW == 2) && G % HPW == 0, "one or two query heads per wave");
+    constexpr int QT = 16, KB = 64, THREADS = 64 * G / HPW;
     // K rows unpadded, their 16-byte chunk c stored at c ^ ((row / 2) & KSWZ) (KSWZ keeps it inside the
     // row): the 16-byte K fragment reads then hit no bank twice (with 144-byte padded rows they accounted
     // for every SQ_LDS_BANK_CONFLICT cycle of the kernel, 1.1x its LDS-active cycles). V^T rows of 136
@@ -1073,7 +1077,10 @@ template <int D, int G, bool POW2> __device__ __forceinline__ void attention_hea
     __shared__ __attribute__((aligned(16))) uint16_t m_s[2][QT * MPAD];
     __shared__ uint16_t live_list[kLiveTilesMax];
     __shared__ uint32_t live_total;
-    const uint32_t tid = threadIdx.x, lane = tid % 64u, g = tid / 64u, quad = lane / 16u, col = lane % 16u;
+    // wave w serves query heads HPW w .. HPW w + HPW - 1 of the group: with two, each K and V^T fragment read
+    // from LDS feeds both heads' matrix-core products (the LDS reads per score, which bound the one-head form,
+    // are halved)
+    const uint32_t tid = threadIdx.x, lane = tid % 64u, wave = tid / 64u, g0 = wave * HPW, quad = lane / 16u, col = lane % 16u;
     // grid (KV heads, query tiles): workgroups are dispatched x fastest, so every head's tile t is dispatched
     // before any head's tile t - 1, and later query tiles (more keys) go first across all heads
     const uint32_t kv = blockIdx.x;
@@ -1083,10 +1090,14 @@ template <int D, int G, bool POW2> __device__ __forceinline__ void attention_hea
     const uint32_t qrow = live ? query : a.tokens - 1u;
     const float neg_inf = -__builtin_inff();
 
-    bf16x8_t qf[D / 32];
+    bf16x8_t qf[HPW][D / 32];
 #pragma unroll
-    for (int ks = 0; ks < D / 32; ++ks) {
-        qf[ks] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(a.q + size_t(qrow) * a.qt + kv * a.qh + g * a.qg + ks * 32u + quad * 8u));
+    for (int hd = 0; hd < HPW; ++hd) {
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) {
+            qf[hd][ks] = __builtin_bit_cast(
+                bf16x8_t, *reinterpret_cast<const uint4*>(a.q + size_t(qrow) * a.qt + kv * a.qh + (g0 + hd) * a.qg + ks * 32u + quad * 8u));
+        }
     }
 
     // The 64-key blocks this tile visits, in key order, each with the MASKED flag unless its mask is all
@@ -1095,7 +1106,7 @@ template <int D, int G, bool POW2> __device__ __forceinline__ void attention_hea
     const uint32_t blocks = (a.keys + KB - 1) / KB;
     const bool listed = a.live_blocks != nullptr && blocks <= kLiveTilesMax;
     if (listed) {
-        if (g == 0) {
+        if (wave == 0) {
             const uint8_t* row = a.live_blocks + size_t(tile) * blocks;
             uint32_t n = 0;
             for (uint32_t base = 0; base < blocks; base += 64u) {
@@ -1186,42 +1197,54 @@ template <int D, int G, bool POW2> __device__ __forceinline__ void attention_hea
             }
         }
     };
-    // Scores of this lane (key 16 t + 4 quad + r of the block, query ``col`` of the tile) in u units;
-    // returns cs (s = u * cs).
-    auto scores = [&](int buffer, uint32_t entry, float (&u)[4][4]) -> float {
-        f32x4_t acc[4];
+    // Scores of this lane (key 16 t + 4 quad + r of the block, query ``col`` of the tile) for each of the
+    // wave's heads, in u units; returns cs (s = u * cs).
+    auto scores = [&](int buffer, uint32_t entry, float (&u)[HPW][4][4]) -> float {
+        f32x4_t acc[HPW][4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int hd = 0; hd < HPW; ++hd) {
+                acc[hd][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            }
 #pragma unroll
             for (int ks = 0; ks < D / 32; ++ks) {
                 const bf16x8_t kf = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(&k_s[buffer][(t * 16u + col) * KPAD + (((ks * 4u + quad) ^ (((t * 16u + col) >> 1) & KSWZ)) * 8u)]));
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ks], acc[t], 0, 0, 0);
+#pragma unroll
+                for (int hd = 0; hd < HPW; ++hd) {
+                    acc[hd][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[hd][ks], acc[hd][t], 0, 0, 0);
+                }
             }
         }
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
+        for (int hd = 0; hd < HPW; ++hd) {
 #pragma unroll
-            for (int r = 0; r < 4; r += 2) {
-                u[t][r] = acc[t][r];
-                u[t][r + 1] = acc[t][r + 1];
-                round_bf16_pair(u[t][r], u[t][r + 1]);
+            for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                for (int r = 0; r < 4; r += 2) {
+                    u[hd][t][r] = acc[hd][t][r];
+                    u[hd][t][r + 1] = acc[hd][t][r + 1];
+                    round_bf16_pair(u[hd][t][r], u[hd][t][r + 1]);
+                }
             }
         }
         if (POW2 && !(entry & MASKED)) {
             return a.scale;
         }
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
+        for (int hd = 0; hd < HPW; ++hd) {
 #pragma unroll
-            for (int r = 0; r < 4; r += 2) {
-                if constexpr (!POW2) {
-                    u[t][r] *= a.scale;
-                    u[t][r + 1] *= a.scale;
-                    round_bf16_pair(u[t][r], u[t][r + 1]);
-                } else {
-                    u[t][r] *= a.scale;  // exact: a power-of-two scale, no rounding (see above)
-                    u[t][r + 1] *= a.scale;
+            for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                for (int r = 0; r < 4; r += 2) {
+                    if constexpr (!POW2) {
+                        u[hd][t][r] *= a.scale;
+                        u[hd][t][r + 1] *= a.scale;
+                        round_bf16_pair(u[hd][t][r], u[hd][t][r + 1]);
+                    } else {
+                        u[hd][t][r] *= a.scale;  // exact: a power-of-two scale, no rounding (see above)
+                        u[hd][t][r + 1] *= a.scale;
+                    }
                 }
             }
         }
@@ -1229,12 +1252,15 @@ template <int D, int G, bool POW2> __device__ __forceinline__ void attention_hea
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const uint2 m = *reinterpret_cast<const uint2*>(&m_s[buffer][col * MPAD + t * 16u + quad * 4u]);
-                u[t][0] += __uint_as_float(m.x << 16);
-                u[t][1] += __uint_as_float(m.x & 0xffff0000u);
-                u[t][2] += __uint_as_float(m.y << 16);
-                u[t][3] += __uint_as_float(m.y & 0xffff0000u);
-                round_bf16_pair(u[t][0], u[t][1]);
-                round_bf16_pair(u[t][2], u[t][3]);
+#pragma unroll
+                for (int hd = 0; hd < HPW; ++hd) {
+                    u[hd][t][0] += __uint_as_float(m.x << 16);
+                    u[hd][t][1] += __uint_as_float(m.x & 0xffff0000u);
+                    u[hd][t][2] += __uint_as_float(m.y << 16);
+                    u[hd][t][3] += __uint_as_float(m.y & 0xffff0000u);
+                    round_bf16_pair(u[hd][t][0], u[hd][t][1]);
+                    round_bf16_pair(u[hd][t][2], u[hd][t][3]);
+                }
             }
         }
         return 1.0f;
@@ -1264,64 +1290,82 @@ template <int D, int G, bool POW2> __device__ __forceinline__ void attention_hea
         }
     };
 
-    float peak = neg_inf, total = 0.0f;
-    sweep(false, [&](int buffer, uint32_t entry) {
-        float u[4][4];
-        const float cs = scores(buffer, entry, u);
-        float top = neg_inf;
+    float peak[HPW], total[HPW];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            top = __builtin_fmaxf(top, __builtin_fmaxf(__builtin_fmaxf(u[t][0], u[t][1]), __builtin_fmaxf(u[t][2], u[t][3])));
-        }
-        top = __builtin_fmaxf(peak, top * cs);  // exact: cs is 1 or a power of two
-        if (top != neg_inf) {
-            // exp(s - top) = 2^(u * cs * log2(e) - top * log2(e)): one multiply-add per score
-            const float scale2 = cs * kLog2e, shift = -top * kLog2e;
-            float sum = 0.0f;
+    for (int hd = 0; hd < HPW; ++hd) {
+        peak[hd] = neg_inf;
+        total[hd] = 0.0f;
+    }
+    sweep(false, [&](int buffer, uint32_t entry) {
+        float u[HPW][4][4];
+        const float cs = scores(buffer, entry, u);
+#pragma unroll
+        for (int hd = 0; hd < HPW; ++hd) {
+            float top = neg_inf;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    sum += __builtin_amdgcn_exp2f(__builtin_fmaf(u[t][r], scale2, shift));
-                }
+                top = __builtin_fmaxf(top, __builtin_fmaxf(__builtin_fmaxf(u[hd][t][0], u[hd][t][1]), __builtin_fmaxf(u[hd][t][2], u[hd][t][3])));
             }
-            total = total * fast_exp(peak - top) + sum;
-            peak = top;
+            top = __builtin_fmaxf(peak[hd], top * cs);  // exact: cs is 1 or a power of two
+            if (top != neg_inf) {
+                // exp(s - top) = 2^(u * cs * log2(e) - top * log2(e)): one multiply-add per score
+                const float scale2 = cs * kLog2e, shift = -top * kLog2e;
+                float sum = 0.0f;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        sum += __builtin_amdgcn_exp2f(__builtin_fmaf(u[hd][t][r], scale2, shift));
+                    }
+                }
+                total[hd] = total[hd] * fast_exp(peak[hd] - top) + sum;
+                peak[hd] = top;
+            }
         }
     });
     // Combine the four lane groups that share a query, then fold in the sink.
-#pragma unroll
-    for (int offset = 16; offset < 64; offset <<= 1) {
-        softmax_stats_merge(peak, total, __shfl_xor(peak, offset, kWave), __shfl_xor(total, offset, kWave));
-    }
-    softmax_stats_add(peak, total, bf16_to_f32(a.sinks[kv * a.sh + g * a.sg]));
     // p = exp(s - peak) / total = 2^(s * log2(e) - (peak * log2(e) + log2(total))): the normalisation
     // rides in the exponent's one multiply-add (v_log_f32 is log2). Only a row whose scores and sink are
     // all -inf has total 0; its probabilities are NaN, as the reference's 0 / 0 is.
-    const float norm = -(peak * kLog2e + __builtin_amdgcn_logf(total));
-
-    f32x4_t o[D / 16];
+    float norm[HPW];
 #pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) {
-        o[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int hd = 0; hd < HPW; ++hd) {
+#pragma unroll
+        for (int offset = 16; offset < 64; offset <<= 1) {
+            softmax_stats_merge(peak[hd], total[hd], __shfl_xor(peak[hd], offset, kWave), __shfl_xor(total[hd], offset, kWave));
+        }
+        softmax_stats_add(peak[hd], total[hd], bf16_to_f32(a.sinks[kv * a.sh + (g0 + hd) * a.sg]));
+        norm[hd] = -(peak[hd] * kLog2e + __builtin_amdgcn_logf(total[hd]));
+    }
+
+    f32x4_t o[HPW][D / 16];
+#pragma unroll
+    for (int hd = 0; hd < HPW; ++hd) {
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt) {
+            o[hd][dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
     }
     sweep(true, [&](int buffer, uint32_t entry) {
-        float u[4][4];
+        float u[HPW][4][4];
         const float scale2 = scores(buffer, entry, u) * kLog2e;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             // keys 32 h + (4 quad + r) and 32 h + 16 + (4 quad + r): this lane's B operand slots 0-3 and 4-7
-            float e[8];
+            bf16x8_t pf[HPW];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                e[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(u[2 * h + i / 4][i % 4], scale2, norm));
-            }
-            bf16x8_t pf;
+            for (int hd = 0; hd < HPW; ++hd) {
+                float e[8];
 #pragma unroll
-            for (int i = 0; i < 8; i += 2) {
-                const bf16x2_t pair = __builtin_convertvector(f32x2_t{e[i], e[i + 1]}, bf16x2_t);
-                pf[i] = pair[0];
-                pf[i + 1] = pair[1];
+                for (int i = 0; i < 8; ++i) {
+                    e[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(u[hd][2 * h + i / 4][i % 4], scale2, norm[hd]));
+                }
+#pragma unroll
+                for (int i = 0; i < 8; i += 2) {
+                    const bf16x2_t pair = __builtin_convertvector(f32x2_t{e[i], e[i + 1]}, bf16x2_t);
+                    pf[hd][i] = pair[0];
+                    pf[hd][i + 1] = pair[1];
+                }
             }
 #pragma unroll
             for (int dt = 0; dt < D / 16; ++dt) {
@@ -1329,18 +1373,24 @@ template <int D, int G, bool POW2> __device__ __forceinline__ void attention_hea
                 const uint2 lo = *reinterpret_cast<const uint2*>(row + quad * 4u);
                 const uint2 hi = *reinterpret_cast<const uint2*>(row + 16u + quad * 4u);
                 const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, uint4{lo.x, lo.y, hi.x, hi.y});
-                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[dt], 0, 0, 0);
+#pragma unroll
+                for (int hd = 0; hd < HPW; ++hd) {
+                    o[hd][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[hd], o[hd][dt], 0, 0, 0);
+                }
             }
         }
     });
     if (live) {
-        uint16_t* dst = a.out + ((size_t(query) * a.kv_heads + kv) * a.group + g) * D;
 #pragma unroll
-        for (int dt = 0; dt < D / 16; ++dt) {
-            const uint32_t d = dt * 16u + quad * 4u;
-            const uint32_t w0 = uint32_t(f32_to_bf16(o[dt][0])) | (uint32_t(f32_to_bf16(o[dt][1])) << 16);
-            const uint32_t w1 = uint32_t(f32_to_bf16(o[dt][2])) | (uint32_t(f32_to_bf16(o[dt][3])) << 16);
-            *reinterpret_cast<uint2*>(dst + d) = uint2{w0, w1};
+        for (int hd = 0; hd < HPW; ++hd) {
+            uint16_t* dst = a.out + ((size_t(query) * a.kv_heads + kv) * a.group + g0 + hd) * D;
+#pragma unroll
+            for (int dt = 0; dt < D / 16; ++dt) {
+                const uint32_t d = dt * 16u + quad * 4u;
+                const uint32_t w0 = uint32_t(f32_to_bf16(o[hd][dt][0])) | (uint32_t(f32_to_bf16(o[hd][dt][1])) << 16);
+                const uint32_t w1 = uint32_t(f32_to_bf16(o[hd][dt][2])) | (uint32_t(f32_to_bf16(o[hd][dt][3])) << 16);
+                *reinterpret_cast<uint2*>(dst + d) = uint2{w0, w1};
+            }
         }
     }
 }

@@ -270,6 +270,21 @@ def test_long_cache_attention_with_wide_heads_cross_compiles(tmp_path, dtype, di
     build(generated, tmp_path / "program", load=False)
 
 
+def test_grouped_prefill_attention_takes_two_heads_per_wave():
+    """A bfloat16 prefill over a mask shared by every head (the workloads' case) runs ``attention_heads`` with
+    two query heads per wave when the group is even (half the waves: 256 threads for a group of 8, compiled
+    for three resident workgroups per compute unit), one otherwise."""
+    dtype = torch.bfloat16
+    for group, heads, threads in ((8, 2, 256), (3, 1, 192)):
+        mask = torch.zeros(128, 160, dtype=dtype)
+        inputs = (torch.randn(128, 1, group, 64).to(dtype), torch.randn(32, 1, 64).to(dtype), torch.randn(128, 1, 64).to(dtype),
+                  torch.randn(32, 1, 64).to(dtype), torch.randn(128, 1, 64).to(dtype), mask, torch.randn(group).to(dtype))
+        source = lower(CachedAttention(), *inputs).files["model.hip"]
+        assert f"chroma::attention_heads_mfma_bf16<64, {group}, true, {heads}>(a);" in source
+        bounds = f"__launch_bounds__({threads}, 3)" if heads == 2 else f"__launch_bounds__({threads})"
+        assert re.search(re.escape(bounds) + r" chroma_attention_heads_", source), source[:300]
+
+
 def test_decode_attention_is_two_launches_with_tickets_inside_the_error_region():
     """A long cache read by few (query row, head) rows: scores and statistics, then partial sums whose last
     split adds them (no combine launch); each row's ticket word lies in the error region's decode-attention

@@ -1416,6 +1416,47 @@ def test_fused_attention_additive_mask(tmp_path, tokens, past, dim):
     compare(got, want)
 
 
+@pytest.mark.parametrize("tokens, past, kv_heads, group, dim", [(200, 0, 1, 8, 64), (130, 70, 2, 4, 128), (96, 40, 2, 2, 64), (80, 0, 1, 3, 64)])
+def test_two_query_heads_per_attention_wave(tmp_path, monkeypatch, tokens, past, kv_heads, group, dim):
+    """The grouped prefill attention with two query heads per wave (each K and V^T fragment read from LDS
+    feeds both heads' products) against one head per wave, bit for bit: causal masks with a band of
+    additive bias, a fully masked query row, partial query and key tiles; an odd group (3) keeps one head
+    per wave. Both against the oracle's unfused chain."""
+    from chroma_amd._src.codegen import hip as codegen
+
+    generator = torch.Generator().manual_seed(tokens + group)
+    dtype = torch.bfloat16
+
+    def rand(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=generator) * scale).to(dtype)
+
+    keys = past + tokens
+    mask = torch.zeros(tokens, keys)
+    band = slice(keys // 3, keys // 3 + 50)
+    mask[:, band] = torch.randn(tokens, band.stop - band.start, generator=generator) * 0.5
+    for t in range(tokens):
+        mask[t, past + t + 1 :] = -math.inf
+    mask[1, :] = -math.inf
+    inputs = (rand(tokens, kv_heads, group, dim), rand(past or 1, kv_heads, dim), rand(tokens, kv_heads, dim),
+              rand(past or 1, kv_heads, dim), rand(tokens, kv_heads, dim), mask.to(dtype), rand(kv_heads * group, scale=2.0))
+    if not past:
+        module, inputs = FreshAttention(), (inputs[0], inputs[2], inputs[4], inputs[5], inputs[6])
+    else:
+        module = SinkAttention()
+    exported = torch.export.export(module, inputs)
+    outputs = {}
+    for per_wave in (1, 2):
+        monkeypatch.setattr(codegen, "ATTENTION_HEADS_PER_WAVE", per_wave)
+        with chroma_amd.compile(exported, tmp_path / f"hip{per_wave}") as model:
+            source = (tmp_path / f"hip{per_wave}" / "model.hip").read_text()
+            heads = per_wave if group % per_wave == 0 else 1
+            assert f"attention_heads_mfma_bf16<{dim}, {group}, " in source and f", {heads}>(a);" in source
+            outputs[per_wave] = model(*inputs)
+    np.testing.assert_array_equal(outputs[2].view(np.uint16), outputs[1].view(np.uint16))
+    want = compile_cpu(exported, tmp_path / "cpu")(*[numpy_of(v) for v in inputs])
+    compare(outputs[2], want)
+
+
 class PerHeadAttention(torch.nn.Module):
     """Attention whose mask differs per query head ([kv, group, queries, keys])."""
 
