@@ -128,7 +128,7 @@ SMALL_INPUT_BYTES = 64 << 10  # inputs up to this size are staged ahead of the l
 MATRIX_ATTENTION_TOKENS = 64  # bfloat16 attention over at least this many queries runs on the matrix cores
 # query heads per wave of the grouped prefill attention (attention_heads): two share each K and V^T fragment
 # read from LDS, whose bandwidth bounds the one-head form; compiled for 3 resident workgroups per compute unit
-# (170 registers: unbounded it takes 204 and 2 fit, at 4 it spills). C5 full layer 132 -> 125 us standalone,
+# (164 registers: unbounded it takes 204 and 2 fit, at 4 it spills). C5 full layer 132 -> 125 us standalone,
 # a 4-layer prefill slice 5.945 -> 5.890 ms, bit-identical
 ATTENTION_HEADS_PER_WAVE = 2
 ATTENTION_HEADS_MIN_BLOCKS = 3
