@@ -700,6 +700,17 @@ def test_bfloat16_storage_rounding_and_float_accumulation(tmp_path):
                 np.testing.assert_array_equal(as_float(got[2]), np.full(5, answers[2], dtype=np.float32))
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rank0_softmax_and_topk(tmp_path, dtype):
+    """Softmax and top-k of rank-0 tensors, which the lowering reshapes to one element (the reference's
+    lowering.py:252-256, :268-272), and the top-1 of a one-element row (value and int64 index): against the
+    oracle and eager torch, twice over and through a reload."""
+    x = torch.tensor(1.5).to(dtype)
+    check(tmp_path / "a", Function(lambda x: (torch.softmax(x, dim=-1), torch.softmax(x * 2, dim=0))), x)
+    check(tmp_path / "b", Function(lambda x: tuple(torch.topk(x, k=1))), x)
+    check(tmp_path / "c", Function(lambda x: tuple(torch.topk(x, k=1, largest=False))), torch.tensor([-0.75]).to(dtype))
+
+
 def test_nonfinite_math_scalars_and_long_chains(tmp_path):
     def fn(x):
         z = x.clamp(-1, 1)
