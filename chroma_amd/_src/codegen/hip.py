@@ -2624,8 +2624,11 @@ class HIPCodegen(Codegen):
             pointer = f"{base} + {offset}u" if offset else base
             function = "attention_live_blocks" if tile == (64, 32) else "attention_live_tiles"
             assert tile in ((64, 32), (16, 64))
+            threads = 256
+            if tile == (16, 64) and offset % 8 == 0 and strides[2] % 8 == 0:
+                function, threads = "attention_live_tiles_wave", 64  # 16-byte loads, one wave per tile
             k.line(f"chroma::{function}({pointer}, {strides[2]}u, {tokens}u, {keys}u, reinterpret_cast<uint8_t*>({flags}));")
-            self.launch(k, (query_blocks, key_blocks, 1), 256, [value], kind="attention_blocks")
+            self.launch(k, (query_blocks, key_blocks, 1), threads, [value], kind="attention_blocks")
             self.live_block_tables[key] = table
         return self.live_block_tables[key]
 

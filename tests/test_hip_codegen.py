@@ -283,6 +283,12 @@ def test_grouped_prefill_attention_takes_two_heads_per_wave():
         assert f"chroma::attention_heads_mfma_bf16<64, {group}, true, {heads}>(a);" in source
         bounds = f"__launch_bounds__({threads}, 3)" if heads == 2 else f"__launch_bounds__({threads})"
         assert re.search(re.escape(bounds) + r" chroma_attention_heads_", source), source[:300]
+        # the live-tile table of a mask whose rows are whole 16-byte chunks: one wave per tile
+        assert "chroma::attention_live_tiles_wave(" in source
+    ragged = (torch.randn(128, 1, 8, 64).to(dtype), torch.randn(36, 1, 64).to(dtype), torch.randn(128, 1, 64).to(dtype),
+              torch.randn(36, 1, 64).to(dtype), torch.randn(128, 1, 64).to(dtype), torch.zeros(128, 164, dtype=dtype), torch.randn(8).to(dtype))
+    source = lower(CachedAttention(), *ragged).files["model.hip"]
+    assert "chroma::attention_live_tiles(" in source and "attention_live_tiles_wave" not in source  # 164-key rows
 
 
 def test_decode_attention_is_two_launches_with_tickets_inside_the_error_region():
