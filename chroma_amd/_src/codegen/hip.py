@@ -131,6 +131,9 @@ MATRIX_ATTENTION_TOKENS = 64  # bfloat16 attention over at least this many queri
 # (164 registers: unbounded it takes 204 and 2 fit, at 4 it spills). C5 full layer 132 -> 125 us standalone,
 # a 4-layer prefill slice 5.945 -> 5.890 ms, bit-identical
 ATTENTION_HEADS_PER_WAVE = 2
+# the live-tile table of a mask whose rows are whole 16-byte chunks is built by one wave per tile
+# (chroma::attention_live_tiles_wave) instead of a 256-thread workgroup
+WAVE_LIVE_TILES = True
 ATTENTION_HEADS_MIN_BLOCKS = 3
 SPLIT_KEYS = 256  # keys per workgroup when an attention row's keys are split over workgroups
 DECODE_SPLIT_KEYS = 128  # the same for stored key/value rows read with 16-byte loads (decode steps)
@@ -2625,7 +2628,7 @@ class HIPCodegen(Codegen):
             function = "attention_live_blocks" if tile == (64, 32) else "attention_live_tiles"
             assert tile in ((64, 32), (16, 64))
             threads = 256
-            if tile == (16, 64) and offset % 8 == 0 and strides[2] % 8 == 0:
+            if WAVE_LIVE_TILES and tile == (16, 64) and offset % 8 == 0 and strides[2] % 8 == 0:
                 function, threads = "attention_live_tiles_wave", 64  # 16-byte loads, one wave per tile
             k.line(f"chroma::{function}({pointer}, {strides[2]}u, {tokens}u, {keys}u, reinterpret_cast<uint8_t*>({flags}));")
             self.launch(k, (query_blocks, key_blocks, 1), threads, [value], kind="attention_blocks")

@@ -1468,6 +1468,45 @@ def test_two_query_heads_per_attention_wave(tmp_path, monkeypatch, tokens, past,
     compare(outputs[2], want)
 
 
+@pytest.mark.parametrize("tokens, past", [(200, 0), (96, 40), (150, 170)])
+def test_live_tile_tables_from_one_wave_per_tile(tmp_path, monkeypatch, tokens, past):
+    """The grouped prefill attention's live-tile table built by one wave per tile (16-byte loads, ballots)
+    against the 256-thread workgroup form, through the attention's output bit for bit: a causal mask with a
+    band of additive bias, a band of -0.0, a fully masked query row and a fully masked key block, with key
+    counts that end inside a 64-key block (200, 136) or at its end (320) and query counts inside a 16-query tile."""
+    from chroma_amd._src.codegen import hip as codegen
+
+    generator = torch.Generator().manual_seed(tokens * 7 + past)
+    dtype = torch.bfloat16
+
+    def rand(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=generator) * scale).to(dtype)
+
+    keys = past + tokens
+    mask = torch.zeros(tokens, keys)
+    mask[:, keys // 4 : keys // 4 + 40] = torch.randn(tokens, 40, generator=generator) * 0.5
+    mask[:, keys // 2 : keys // 2 + 24] = -0.0
+    mask[:, 64:128] = -math.inf
+    for t in range(tokens):
+        mask[t, past + t + 1 :] = -math.inf
+    mask[3, :] = -math.inf
+    inputs = (rand(tokens, 1, 8, 64), rand(past or 1, 1, 64), rand(tokens, 1, 64), rand(past or 1, 1, 64), rand(tokens, 1, 64),
+              mask.to(dtype), rand(8, scale=2.0))
+    if not past:
+        module, inputs = FreshAttention(), (inputs[0], inputs[2], inputs[4], inputs[5], inputs[6])
+    else:
+        module = SinkAttention()
+    exported = torch.export.export(module, inputs)
+    outputs = {}
+    for wave in (False, True):
+        monkeypatch.setattr(codegen, "WAVE_LIVE_TILES", wave)
+        with chroma_amd.compile(exported, tmp_path / f"hip{wave}") as model:
+            assert ("attention_live_tiles_wave(" in (tmp_path / f"hip{wave}" / "model.hip").read_text()) == wave
+            outputs[wave] = model(*inputs)
+    np.testing.assert_array_equal(outputs[True].view(np.uint16), outputs[False].view(np.uint16))
+    compare(outputs[True], compile_cpu(exported, tmp_path / "cpu")(*[numpy_of(v) for v in inputs]))
+
+
 class PerHeadAttention(torch.nn.Module):
     """Attention whose mask differs per query head ([kv, group, queries, keys])."""
 
