@@ -1584,6 +1584,12 @@ __device__ __forceinline__ uint32_t expert_tile_rows(uint32_t count, uint32_t fi
     return count - first <= last ? count - first : 128u;
 }
 
+// The first kRouteHeld slots of each thread keep their expert in registers between the counting and the
+// scattering pass (slots past blockDim x kRouteHeld read their id again). The per-expert counts,
+// offsets and both tile tables come from the first wave, 64 experts at a time with wave prefix sums (the
+// same entries, in the same places, as a walk over the experts in order).
+constexpr uint32_t kRouteHeld = 16;
+
 __device__ __forceinline__ void route_slots(const int64_t* __restrict__ indices, uint32_t slots, uint32_t experts,
                                             int32_t* __restrict__ scratch, unsigned int* error) {
     extern __shared__ int32_t shared_counts[];
@@ -1596,42 +1602,72 @@ __device__ __forceinline__ void route_slots(const int64_t* __restrict__ indices,
         shared_counts[e] = 0;
     }
     __syncthreads();
-    for (uint32_t t = threadIdx.x; t < slots; t += blockDim.x) {
-        const uint32_t e = uint32_t(checked_index(indices[t], experts, true, error));
-        atomicAdd(&shared_counts[e], 1);
+    uint32_t held[kRouteHeld];
+#pragma unroll
+    for (uint32_t i = 0; i < kRouteHeld; ++i) {
+        const uint32_t t = threadIdx.x + i * blockDim.x;
+        held[i] = 0;
+        if (t < slots) {
+            held[i] = uint32_t(checked_index(indices[t], experts, true, error));
+            atomicAdd(&shared_counts[held[i]], 1);
+        }
+    }
+    for (uint32_t t = threadIdx.x + kRouteHeld * blockDim.x; t < slots; t += blockDim.x) {
+        atomicAdd(&shared_counts[uint32_t(checked_index(indices[t], experts, true, error))], 1);
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (threadIdx.x < kWave) {
+        const uint32_t lane = threadIdx.x;
         int32_t* tall_count = scratch + expert_table_word(slots, experts, kTallLastTile);
         int32_t* tall = tall_count + 1;
-        int32_t running = 0, tile = 0, tall_tile = 0;
-        for (uint32_t e = 0; e < experts; ++e) {
-            const int32_t count = shared_counts[e];
-            counts[e] = count;
-            offsets[e] = running;
-            const uint32_t n = expert_row_tiles(uint32_t(count), 128u), m = expert_row_tiles(uint32_t(count), kTallLastTile);
-            for (uint32_t t = 0; t < n; ++t) {
-                tiles[2 * tile] = int32_t(e);
-                tiles[2 * tile + 1] = int32_t(128u * t);
-                ++tile;
-                if (t < m) {
-                    tall[2 * tall_tile] = int32_t(e);
-                    tall[2 * tall_tile + 1] = int32_t(128u * t);
-                    ++tall_tile;
+        uint32_t running = 0, tile = 0, tall_tile = 0;  // totals of the experts before this step's 64
+        for (uint32_t e0 = 0; e0 < experts; e0 += kWave) {
+            const uint32_t e = e0 + lane;
+            const uint32_t count = e < experts ? uint32_t(shared_counts[e]) : 0u;
+            const uint32_t n = expert_row_tiles(count, 128u), m = expert_row_tiles(count, kTallLastTile);
+            uint32_t c_in = count, n_in = n, m_in = m;  // inclusive prefix sums over the lanes
+#pragma unroll
+            for (int d = 1; d < kWave; d <<= 1) {
+                const uint32_t c_up = __shfl_up(c_in, d, kWave), n_up = __shfl_up(n_in, d, kWave), m_up = __shfl_up(m_in, d, kWave);
+                if (lane >= uint32_t(d)) {
+                    c_in += c_up;
+                    n_in += n_up;
+                    m_in += m_up;
                 }
             }
-            running += count;
+            if (e < experts) {
+                const uint32_t offset = running + c_in - count, first = tile + n_in - n, first_tall = tall_tile + m_in - m;
+                counts[e] = int32_t(count);
+                offsets[e] = int32_t(offset);
+                for (uint32_t t = 0; t < n; ++t) {
+                    tiles[2 * (first + t)] = int32_t(e);
+                    tiles[2 * (first + t) + 1] = int32_t(128u * t);
+                }
+                for (uint32_t t = 0; t < m; ++t) {
+                    tall[2 * (first_tall + t)] = int32_t(e);
+                    tall[2 * (first_tall + t) + 1] = int32_t(128u * t);
+                }
+                shared_counts[e] = int32_t(offset);  // the scatter's cursor
+            }
+            running += __shfl(c_in, kWave - 1, kWave);
+            tile += __shfl(n_in, kWave - 1, kWave);
+            tall_tile += __shfl(m_in, kWave - 1, kWave);
         }
-        offsets[experts] = running;
-        *tile_count = tile;
-        *tall_count = tall_tile;
+        if (lane == 0) {
+            offsets[experts] = int32_t(running);
+            *tile_count = int32_t(tile);
+            *tall_count = int32_t(tall_tile);
+        }
     }
     __syncthreads();
-    for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) {
-        shared_counts[e] = offsets[e];
+#pragma unroll
+    for (uint32_t i = 0; i < kRouteHeld; ++i) {
+        const uint32_t t = threadIdx.x + i * blockDim.x;
+        if (t < slots) {
+            permutation[atomicAdd(&shared_counts[held[i]], 1)] = int32_t(t);
+        }
     }
-    __syncthreads();
-    for (uint32_t t = threadIdx.x; t < slots; t += blockDim.x) {
+    for (uint32_t t = threadIdx.x + kRouteHeld * blockDim.x; t < slots; t += blockDim.x) {
         int64_t raw = indices[t];
         raw = raw < 0 ? raw + int64_t(experts) : raw;
         const uint32_t e = (raw < 0 || raw >= int64_t(experts)) ? 0u : uint32_t(raw);
