@@ -2589,7 +2589,8 @@ class HIPCodegen(Codegen):
             # a power-of-two scale <= 1 makes the scaled score a bfloat16 value: its rounding is left out
             mantissa, exponent = math.frexp(scale)
             pow2 = mantissa == 0.5 and -64 <= exponent <= 1
-            per_wave = ATTENTION_HEADS_PER_WAVE if group % ATTENTION_HEADS_PER_WAVE == 0 else 1
+            # (head dimensions above 64 would need more registers than three workgroups per CU leave)
+            per_wave = ATTENTION_HEADS_PER_WAVE if group % ATTENTION_HEADS_PER_WAVE == 0 and dim <= 64 else 1
             k.min_waves = ATTENTION_HEADS_MIN_BLOCKS if per_wave > 1 else 0
             k.line(f"chroma::attention_heads_mfma_bf16<{dim}, {group}, {'true' if pow2 else 'false'}, {per_wave}>(a);")
             operands = [entry[0] for entry in plan.values() if entry is not None] + [live]

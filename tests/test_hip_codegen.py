@@ -272,8 +272,8 @@ def test_long_cache_attention_with_wide_heads_cross_compiles(tmp_path, dtype, di
 
 def test_grouped_prefill_attention_takes_two_heads_per_wave():
     """A bfloat16 prefill over a mask shared by every head (the workloads' case) runs ``attention_heads`` with
-    two query heads per wave when the group is even (half the waves: 256 threads for a group of 8, compiled
-    for three resident workgroups per compute unit), one otherwise."""
+    two query heads per wave when the group is even and the head dimension at most 64 (half the waves: 256
+    threads for a group of 8, compiled for three resident workgroups per compute unit), one otherwise."""
     dtype = torch.bfloat16
     for group, heads, threads in ((8, 2, 256), (3, 1, 192)):
         mask = torch.zeros(128, 160, dtype=dtype)
